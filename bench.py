@@ -1,0 +1,184 @@
+#!/usr/bin/env python3
+"""Benchmark of the RDT-1B attention hot path on one MI355X.
+
+Prints ONE JSON line (the driver's contract).  Workload: BASELINE config 2,
+the image cross-attention op (67 queries x 4374 keys, 32 heads x 64, bf16,
+batch 1), whose HBM roofline is the metric's second half; config-2 variants
+(batch 8, language keys with valid lengths) and the 67x67 self-attention are
+reported as extra fields.  Inputs are synthetic N(0,1) bf16 already resident
+in HBM when timing starts; timing uses HIP events on the stream the kernels
+run on.  The CPU baseline is the oracle's fp32 restatement of the reference's
+naive_attention_kernel (attention.cu:90-139) on the host cores, on a bounded
+sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "RDT-1B denoise-loop latency ms (bs=1) + cross-attn HBM GB/s vs roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def attn_bytes(B, H, Sq, Sk_valid_total, D=64, eb=2):
+    """Algorithmic HBM bytes of one attention op: K and V once, Q in, O out."""
+    return 2 * H * Sk_valid_total * D * eb + 2 * B * H * Sq * D * eb
+
+
+def attn_flops(B, H, Sq, Sk_valid_total, D=64):
+    return 4 * H * Sq * Sk_valid_total * D
+
+
+def time_op(fn, steps, warmup, stream):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per op
+
+
+def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32):
+    import numpy as np
+    import torch
+
+    from servoflow_amd.attention import attention, make_desc, workspace_bytes
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234 + B + Sk)
+    q = torch.randn(B, H, Sq, 64, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    # Output straight into [B, Sq, H*D], the layout the block's projection reads.
+    out = torch.empty(B, Sq, H, 64, device=dev, dtype=torch.bfloat16).permute(0, 2, 1, 3)
+    vl = None
+    if valid is not None:
+        vl = torch.from_numpy(np.asarray(valid, np.int32)).to(dev)
+    desc = make_desc(q, k, v, out, valid_len=vl)
+    ws = torch.empty(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    fn = lambda: attention(q, k, v, out=out, valid_len=vl, workspace=ws)  # noqa: E731
+    ms = time_op(fn, steps, warmup, stream)
+    sk_total = B * Sk if valid is None else int(np.sum(valid))
+    nbytes = attn_bytes(B, H, Sq, sk_total)
+    return {
+        "ms": ms,
+        "us": ms * 1e3,
+        "bytes": nbytes,
+        "GBps": nbytes / (ms * 1e-3) / 1e9,
+        "TFLOPs": attn_flops(B, H, Sq, sk_total) / (ms * 1e-3) / 1e12,
+        "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    }
+
+
+def cpu_baseline(budget_s=12.0):
+    """Oracle fp32 restatement of naive_attention_kernel on the host cores,
+    timed on the same image cross-attention shape (B=1)."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    B, H, Sq, Sk = 1, 32, 67, 4374
+    q = O.randn(1, (B, H, Sq, 64))
+    k = O.randn(2, (B, H, Sk, 64))
+    v = O.randn(3, (B, H, Sk, 64))
+    O.attention_f32(q, k, v)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        O.attention_f32(q, k, v)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    med = float(np.median(times))
+    nbytes = attn_bytes(B, H, Sq, B * Sk)
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {
+        "value": nbytes / med / 1e9,
+        "unit": "GB/s",
+        "ms_per_op": med * 1e3,
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{len(times)} runs of the full B=1 image cross-attention (1x32x67x4374x64, fp32), median",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(every GPU box here has one MI355X).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    torch.cuda.init()
+    rng = np.random.default_rng(7)
+    img1 = bench_attention(1, 4374, args.steps, args.warmup)
+    img8 = bench_attention(8, 4374, args.steps, args.warmup)
+    lang_valid8 = rng.integers(32, 1025, size=8)
+    lang8 = bench_attention(8, 1024, args.steps, args.warmup, valid=lang_valid8)
+    lang1 = bench_attention(1, 1024, args.steps, args.warmup, valid=[1024])
+    self1 = bench_attention(1, 67, args.steps, args.warmup)
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": METRIC,
+        "value": round(img1["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(img1["ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config 2: image cross-attention op, B=1, 32 heads x 64, "
+                               "67 queries x 4374 keys, bf16 in/out, [B,Sq,H*D] output"},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(img1["GBps"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(img1["frac_hbm"], 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "extra": {
+            "cross_img_b1_us": round(img1["us"], 3),
+            "cross_img_b8_us": round(img8["us"], 3),
+            "cross_img_b8_GBps": round(img8["GBps"], 1),
+            "cross_img_b8_frac": round(img8["frac_hbm"], 4),
+            "cross_lang_b8_us": round(lang8["us"], 3),
+            "cross_lang_b8_GBps": round(lang8["GBps"], 1),
+            "cross_lang_b1_full_us": round(lang1["us"], 3),
+            "self_b1_us": round(self1["us"], 3),
+            "self_b1_TFLOPs": round(self1["TFLOPs"], 3),
+        },
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

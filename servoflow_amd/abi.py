@@ -1,0 +1,98 @@
+"""ctypes bindings for libsf_hip_kernels.so (the C-ABI declared in include/sf_hip.h).
+
+The library is the product: these bindings only describe its entry points.
+Loading raises if the shared object is missing; nothing here computes on the
+CPU or falls back to another implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libsf_hip_kernels.so")
+
+SF_OK = 0
+SF_EINVAL = -1
+SF_ENOTSUP = -2
+SF_EWORKSPACE = -3
+SF_ELAUNCH = -4
+SF_EDEVICE = -5
+
+SF_F32 = 0
+SF_F16 = 1
+SF_BF16 = 2
+SF_I8 = 3
+SF_I32 = 5
+
+
+class AttnDesc(ctypes.Structure):
+    """Mirror of `sf_attn_desc`."""
+
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("Sq", ctypes.c_int32),
+        ("Sk", ctypes.c_int32),
+        ("D", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("in_dtype", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32),
+        ("is_causal", ctypes.c_int32),
+        ("num_splits", ctypes.c_int32),
+        ("kv_valid_len", ctypes.c_void_p),
+        ("q_stride", ctypes.c_int64 * 3),
+        ("k_stride", ctypes.c_int64 * 3),
+        ("v_stride", ctypes.c_int64 * 3),
+        ("o_stride", ctypes.c_int64 * 3),
+    ]
+
+
+class SfError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        super().__init__(f"{what}: {strerror(status)} (status {status})")
+        self.status = status
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libsf_hip_kernels.so once; raises FileNotFoundError if unbuilt."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+        )
+    L = ctypes.CDLL(LIB_PATH)
+    P = ctypes.POINTER(AttnDesc)
+    L.sf_attn_desc_init_bhsd.argtypes = [P] + [ctypes.c_int32] * 7
+    L.sf_attn_desc_init_bhsd.restype = None
+    L.sf_attn_workspace_bytes.argtypes = [P]
+    L.sf_attn_workspace_bytes.restype = ctypes.c_size_t
+    L.sf_attn_num_splits.argtypes = [P]
+    L.sf_attn_num_splits.restype = ctypes.c_int32
+    L.sf_attn_fwd.argtypes = [P, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    L.sf_attn_fwd.restype = ctypes.c_int
+    L.sf_strerror.argtypes = [ctypes.c_int]
+    L.sf_strerror.restype = ctypes.c_char_p
+    _lib = L
+    return L
+
+
+def strerror(status: int) -> str:
+    return lib().sf_strerror(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != SF_OK:
+        raise SfError(status, what)
+
+
+def attn_desc_bhsd(B, H, Sq, Sk, D=64, in_dtype=SF_BF16, out_dtype=SF_BF16) -> AttnDesc:
+    d = AttnDesc()
+    lib().sf_attn_desc_init_bhsd(ctypes.byref(d), B, H, Sq, Sk, D, in_dtype, out_dtype)
+    return d

@@ -1,0 +1,68 @@
+"""Torch-tensor front end for `sf_attn_fwd` (tests and bench plumbing).
+
+torch supplies device memory and the current HIP stream; the arithmetic runs
+in libsf_hip_kernels.so.  Mirrors IBackend::attention
+(include/servoflow/backend/backend.h:105-110): Q [B,H,Sq,D], K/V [B,H,Sk,D],
+out [B,H,Sq,D] (or any strided view with a contiguous head dim), mask
+semantics as documented on `sf_attn_desc`.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import abi
+
+_DT = {torch.bfloat16: abi.SF_BF16, torch.float32: abi.SF_F32, torch.float16: abi.SF_F16}
+
+
+def _strides3(t: torch.Tensor):
+    if t.dim() != 4 or t.stride(3) != 1:
+        raise ValueError("expected a 4-D tensor [B,H,S,D] with a contiguous last dim")
+    return (t.stride(0), t.stride(1), t.stride(2))
+
+
+def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_splits=0):
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    if k.shape != (B, H, Sk, D) or v.shape != (B, H, Sk, D) or out.shape != (B, H, Sq, D):
+        raise ValueError(f"shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} "
+                         f"v{tuple(v.shape)} out{tuple(out.shape)}")
+    d = abi.AttnDesc()
+    d.B, d.H, d.Sq, d.Sk, d.D = B, H, Sq, Sk, D
+    d.scale = float(scale)
+    d.in_dtype = _DT[q.dtype]
+    d.out_dtype = _DT[out.dtype]
+    d.is_causal = 1 if is_causal else 0
+    d.num_splits = int(num_splits)
+    if valid_len is not None:
+        if valid_len.dtype != torch.int32 or valid_len.numel() != B or not valid_len.is_cuda:
+            raise ValueError("valid_len must be a device int32 tensor of B elements")
+        d.kv_valid_len = valid_len.data_ptr()
+    for name, t in (("q_stride", q), ("k_stride", k), ("v_stride", v), ("o_stride", out)):
+        getattr(d, name)[:] = _strides3(t)
+    return d
+
+
+def workspace_bytes(desc) -> int:
+    return int(abi.lib().sf_attn_workspace_bytes(ctypes.byref(desc)))
+
+
+def attention(q, k, v, out=None, scale=0.0, is_causal=False, valid_len=None, num_splits=0,
+              out_dtype=None, workspace=None, stream=None):
+    """Runs sf_attn_fwd on torch's current stream (or `stream`) and returns `out`."""
+    if out is None:
+        od = out_dtype or q.dtype
+        out = torch.empty(q.shape, dtype=od, device=q.device)
+    desc = make_desc(q, k, v, out, scale, is_causal, valid_len, num_splits)
+    need = workspace_bytes(desc)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_n = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    s = stream if stream is not None else torch.cuda.current_stream(q.device)
+    st = abi.lib().sf_attn_fwd(ctypes.byref(desc), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                               out.data_ptr(), ws_ptr, ws_n, s.cuda_stream)
+    abi.check(st, "sf_attn_fwd")
+    return out

@@ -1,0 +1,101 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/*.h declares, and rejects bad descriptors with the documented status
+codes before touching the device."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from servoflow_amd import abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for path in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for m in re.finditer(r"\b(sf_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for required in ("sf_attn_fwd", "sf_attn_workspace_bytes", "sf_strerror"):
+        assert required in names
+
+
+@pytest.mark.parametrize("name", declared_functions())
+def test_library_exports_symbol(name):
+    L = abi.lib()
+    assert hasattr(L, name), f"{name} declared in include/ but not exported"
+
+
+def test_strerror_texts():
+    for st in (abi.SF_OK, abi.SF_EINVAL, abi.SF_ENOTSUP, abi.SF_EWORKSPACE, abi.SF_ELAUNCH, abi.SF_EDEVICE):
+        assert len(abi.strerror(st)) > 3
+    assert abi.strerror(12345) == "unknown status"
+
+
+def _fwd(desc, q=16, k=16, v=16, o=16, ws=None, wsn=0):
+    return abi.lib().sf_attn_fwd(ctypes.byref(desc), q, k, v, o, ws, wsn, None)
+
+
+def test_desc_init_bhsd_strides():
+    d = abi.attn_desc_bhsd(2, 32, 67, 4374)
+    assert (d.B, d.H, d.Sq, d.Sk, d.D) == (2, 32, 67, 4374, 64)
+    assert list(d.q_stride) == [32 * 67 * 64, 67 * 64, 64]
+    assert list(d.k_stride) == [32 * 4374 * 64, 4374 * 64, 64]
+    assert list(d.o_stride) == list(d.q_stride)
+    assert d.scale == 0.0 and d.num_splits == 0 and not d.kv_valid_len
+
+
+def test_rejects_unsupported_before_launch():
+    d = abi.attn_desc_bhsd(1, 2, 67, 67, D=128)
+    assert _fwd(d) == abi.SF_ENOTSUP
+    d = abi.attn_desc_bhsd(1, 2, 67, 67, in_dtype=abi.SF_F16)
+    assert _fwd(d) == abi.SF_ENOTSUP
+    d = abi.attn_desc_bhsd(1, 2, 67, 67, out_dtype=abi.SF_I8)
+    assert _fwd(d) == abi.SF_ENOTSUP
+
+
+def test_rejects_bad_arguments_before_launch():
+    d = abi.attn_desc_bhsd(1, 2, 67, 67)
+    assert abi.lib().sf_attn_fwd(None, 16, 16, 16, 16, None, 0, None) == abi.SF_EINVAL
+    assert _fwd(d, q=None) == abi.SF_EINVAL
+    assert _fwd(d, k=24) == abi.SF_EINVAL          # not 16-byte aligned
+    d.q_stride[2] = 65                               # row stride not a multiple of 8
+    assert _fwd(d) == abi.SF_EINVAL
+    d = abi.attn_desc_bhsd(1, 2, 67, 0)
+    assert _fwd(d) == abi.SF_EINVAL                 # keys required
+    d = abi.attn_desc_bhsd(1, 2, 67, 67)
+    d.num_splits = -1
+    assert _fwd(d) == abi.SF_EINVAL
+
+
+def test_empty_problem_is_a_noop():
+    d = abi.attn_desc_bhsd(0, 32, 67, 4374)
+    assert _fwd(d, None, None, None, None) == abi.SF_OK
+    d = abi.attn_desc_bhsd(1, 32, 0, 4374)
+    assert _fwd(d, None, None, None, None) == abi.SF_OK
+
+
+def test_workspace_contract():
+    d = abi.attn_desc_bhsd(1, 32, 67, 4374)
+    ns = abi.lib().sf_attn_num_splits(ctypes.byref(d))
+    assert ns > 1
+    need = abi.lib().sf_attn_workspace_bytes(ctypes.byref(d))
+    assert need == 1 * 32 * ns * 67 * (64 + 2) * 4
+    assert _fwd(d, ws=None, wsn=0) == abi.SF_EWORKSPACE
+    assert _fwd(d, ws=16, wsn=need - 4) == abi.SF_EWORKSPACE
+    # self-attention needs no split, hence no workspace
+    d1 = abi.attn_desc_bhsd(1, 32, 67, 67)
+    assert abi.lib().sf_attn_num_splits(ctypes.byref(d1)) == 1
+    assert abi.lib().sf_attn_workspace_bytes(ctypes.byref(d1)) == 0
+    d1.num_splits = 3
+    assert abi.lib().sf_attn_workspace_bytes(ctypes.byref(d1)) == 32 * 3 * 67 * 66 * 4

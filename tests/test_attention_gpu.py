@@ -1,0 +1,184 @@
+"""GPU parity of sf_attn_fwd (libsf_hip_kernels.so) against the CPU oracle.
+
+Inputs are N(0,1) from the oracle's SplitMix64/Box-Muller generator, rounded
+to bf16; the oracle receives the same rounded values in fp32.  The kernel's
+fp32 output must satisfy max-abs <= 2e-2 and sum|d|/sum|ref| <= 1e-3; its bf16
+output must be the fp32 output rounded to nearest (within one bf16 ulp).
+Full-size shapes follow BASELINE configs 1-2: self-attention 67x67, image
+cross-attention 67x4374 and language cross-attention 67x<=1024 with a
+per-batch valid length, 32 heads x 64, batch 1 and 8.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_close_bf16
+from oracle import oracle as O
+from servoflow_amd import abi
+from servoflow_amd.attention import attention
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def rounded(seed, shape, scale=1.0):
+    return O.bf16_round(O.randn(seed, shape) * scale)
+
+
+def to_dev(x, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV).to(dtype)
+
+
+def run(q, k, v, out_dtype=torch.float32, **kw):
+    out = attention(to_dev(q), to_dev(k), to_dev(v), out_dtype=out_dtype, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def lang_valid_lengths(seed, B, lo=32, hi=1024):
+    rng = np.random.default_rng(seed)
+    return rng.integers(lo, hi + 1, size=B).astype(np.int32)
+
+
+def test_self_attention_config1():
+    q, k, v = (rounded(s, (1, 32, 67, 64)) for s in (101, 102, 103))
+    got = run(q, k, v)
+    ref = O.attention_f32(q, k, v)
+    assert_close_bf16(got, ref, "self 1x32x67x67")
+
+
+def test_cross_image_b1():
+    q = rounded(111, (1, 32, 67, 64))
+    k, v = rounded(112, (1, 32, 4374, 64)), rounded(113, (1, 32, 4374, 64))
+    got = run(q, k, v)
+    assert_close_bf16(got, O.attention_f32(q, k, v), "cross img B=1")
+
+
+def test_cross_image_b8_subset():
+    B = 8
+    q = rounded(121, (B, 32, 67, 64))
+    k, v = rounded(122, (B, 32, 4374, 64)), rounded(123, (B, 32, 4374, 64))
+    got = run(q, k, v)
+    for b in (0, 5):
+        ref = O.attention_f32(q[b:b + 1], k[b:b + 1], v[b:b + 1])
+        assert_close_bf16(got[b:b + 1], ref, f"cross img B=8 b={b}")
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_cross_language_valid_len(B):
+    q = rounded(131 + B, (B, 32, 67, 64))
+    k, v = rounded(132 + B, (B, 32, 1024, 64)), rounded(133 + B, (B, 32, 1024, 64))
+    vl = lang_valid_lengths(7 + B, B)
+    got = run(q, k, v, valid_len=to_dev(vl, torch.int32))
+    ref = O.attention_f32(q, k, v, valid_len=vl)
+    assert_close_bf16(got, ref, f"cross lang B={B} valid={vl.tolist()}")
+    # masked(valid = L) == attention over K[:L], V[:L] (reference truncation)
+    b = int(np.argmin(vl))
+    L = int(vl[b])
+    trunc = run(q[b:b + 1], k[b:b + 1, :, :L].copy(), v[b:b + 1, :, :L].copy())
+    assert np.abs(trunc - got[b:b + 1]).max() < 1e-4
+
+
+def test_bf16_output_is_rounded_fp32_output():
+    q = rounded(141, (1, 32, 67, 64))
+    k, v = rounded(142, (1, 32, 4374, 64)), rounded(143, (1, 32, 4374, 64))
+    f32 = run(q, k, v, out_dtype=torch.float32)
+    b16 = run(q, k, v, out_dtype=torch.bfloat16)
+    r = O.bf16_round(f32)
+    ulp = np.abs(r) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(b16 - r) <= ulp)
+    assert np.mean(b16 == r) > 0.99
+
+
+@pytest.mark.parametrize("ns", [1, 3, 16, 40])
+def test_split_count_invariance(ns):
+    q = rounded(151, (1, 8, 67, 64))
+    k, v = rounded(152, (1, 8, 4374, 64)), rounded(153, (1, 8, 4374, 64))
+    got = run(q, k, v, num_splits=ns)
+    assert_close_bf16(got, O.attention_f32(q, k, v), f"num_splits={ns}")
+
+
+def test_causal_matches_oracle():
+    q, k, v = (rounded(s, (1, 4, 67, 64)) for s in (161, 162, 163))
+    got = run(q, k, v, is_causal=True)
+    assert_close_bf16(got, O.attention_f32(q, k, v, causal=True), "causal 67")
+
+
+def test_bshd_output_view_matches_bhsd():
+    q = rounded(171, (2, 32, 67, 64))
+    k, v = rounded(172, (2, 32, 700, 64)), rounded(173, (2, 32, 700, 64))
+    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+    bhsd = attention(qd, kd, vd, out_dtype=torch.float32)
+    seq = torch.empty(2, 67, 32, 64, device=DEV, dtype=torch.float32)
+    attention(qd, kd, vd, out=seq.permute(0, 2, 1, 3))
+    torch.cuda.synchronize()
+    assert torch.equal(seq.permute(0, 2, 1, 3), bhsd)
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk", [(1, 1, 1, 1), (1, 2, 3, 33), (2, 3, 200, 300),
+                                       (1, 1, 81, 129), (3, 2, 67, 5000)])
+def test_edge_shapes(B, H, Sq, Sk):
+    q, k, v = rounded(181, (B, H, Sq, 64)), rounded(182, (B, H, Sk, 64)), rounded(183, (B, H, Sk, 64))
+    got = run(q, k, v)
+    assert_close_bf16(got, O.attention_f32(q, k, v), f"edge {B},{H},{Sq},{Sk}")
+
+
+def test_valid_len_zero_gives_zeros_and_overlong_is_clamped():
+    q = rounded(191, (3, 2, 67, 64))
+    k, v = rounded(192, (3, 2, 256, 64)), rounded(193, (3, 2, 256, 64))
+    vl = np.array([0, 1000, 17], np.int32)
+    got = run(q, k, v, valid_len=to_dev(vl, torch.int32))
+    assert np.all(got[0] == 0)
+    ref = O.attention_f32(q, k, v, valid_len=vl)
+    assert_close_bf16(got, ref, "valid 0/overlong/17")
+
+
+def test_constant_inputs_bench_attention_case():
+    x = np.full((1, 32, 67, 64), 0.01, np.float32)
+    c = float(O.bf16_round(np.array([0.01], np.float32))[0])
+    got = run(x, x, x)
+    assert np.abs(got - c).max() < 1e-6
+
+
+def test_sharp_softmax_stays_stable():
+    q = rounded(201, (1, 4, 67, 64), scale=6.0)
+    k, v = rounded(202, (1, 4, 2000, 64), scale=6.0), rounded(203, (1, 4, 2000, 64))
+    got = run(q, k, v)
+    assert_close_bf16(got, O.attention_f32(q, k, v), "sharp")
+
+
+def test_graph_capture_replays_match_eager():
+    q = to_dev(rounded(211, (1, 32, 67, 64)))
+    k, v = to_dev(rounded(212, (1, 32, 4374, 64))), to_dev(rounded(213, (1, 32, 4374, 64)))
+    out = torch.empty(1, 32, 67, 64, device=DEV, dtype=torch.float32)
+    from servoflow_amd.attention import make_desc, workspace_bytes
+    ws = torch.empty(workspace_bytes(make_desc(q, k, v, out)), dtype=torch.uint8, device=DEV)
+    attention(q, k, v, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            attention(q, k, v, out=out, workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(4):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        _ = (q.float() * 2).sum().item()      # eager work between replays
+
+
+def test_error_paths_on_device():
+    q = to_dev(rounded(221, (1, 2, 67, 64)))
+    k = to_dev(rounded(222, (1, 2, 4374, 64)))
+    with pytest.raises(abi.SfError) as e:
+        attention(q, k, k, out_dtype=torch.float32, workspace=torch.empty(8, dtype=torch.uint8, device=DEV),
+                  num_splits=4)
+    assert e.value.status == abi.SF_EWORKSPACE
+    q128 = torch.zeros(1, 2, 4, 128, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(abi.SfError) as e:
+        attention(q128, q128, q128)
+    assert e.value.status == abi.SF_ENOTSUP
