@@ -33,20 +33,34 @@ def attn_flops(B, H, Sq, Sk_valid_total, D=64):
     return 4 * H * Sq * Sk_valid_total * D
 
 
-def time_op(fn, steps, warmup, stream):
+def time_graph(fn, steps, warmup, reps=20):
+    """Captures `reps` back-to-back calls of fn in one HIP graph and times
+    `steps` replays with HIP events on the capturing stream; returns ms per
+    call.  Graph replay keeps host launch overhead out of the kernel time."""
     import torch
 
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(reps):
+                fn()
+    torch.cuda.current_stream().wait_stream(s)
+    stream = torch.cuda.current_stream()
     for _ in range(warmup):
-        fn()
+        g.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(steps):
-        fn()
+        g.replay()
     stop.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps  # ms per op
+    return start.elapsed_time(stop) / (steps * reps)
 
 
 def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32):
@@ -67,10 +81,9 @@ def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32):
     if valid is not None:
         vl = torch.from_numpy(np.asarray(valid, np.int32)).to(dev)
     desc = make_desc(q, k, v, out, valid_len=vl)
-    ws = torch.empty(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream(dev)
+    ws = torch.zeros(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=dev)
     fn = lambda: attention(q, k, v, out=out, valid_len=vl, workspace=ws)  # noqa: E731
-    ms = time_op(fn, steps, warmup, stream)
+    ms = time_graph(fn, steps, warmup)
     sk_total = B * Sk if valid is None else int(np.sum(valid))
     nbytes = attn_bytes(B, H, Sq, sk_total)
     return {

@@ -67,7 +67,9 @@ typedef enum sf_dtype {
  * kv_valid_len: NULL (every key valid) or a DEVICE pointer to B int32
  * lengths; keys [valid_len[b], Sk) of batch b are ignored.  Lengths are
  * clamped to [0, Sk] on the device; a row with no valid key yields zeros.
- * num_splits: 0 chooses the split-K factor automatically; n > 0 forces n.
+ * num_splits: 0 chooses the split-K factor automatically; n > 0 forces n
+ * (at most 64).
+ * scale must be >= 0 (SF_ENOTSUP otherwise).
  *
  * Supported: in_dtype SF_BF16, out_dtype SF_BF16 or SF_F32, D == 64,
  * pointers 16-byte aligned, s/h/b strides multiples of 8 elements.
@@ -92,8 +94,10 @@ void sf_attn_desc_init_bhsd(sf_attn_desc* desc, int32_t B, int32_t H,
                             int32_t Sq, int32_t Sk, int32_t D,
                             int32_t in_dtype, int32_t out_dtype);
 
-/* Bytes of device workspace sf_attn_fwd needs for this descriptor (split-K
- * partials: fp32 running max, running sum and unnormalised output). */
+/* Bytes of device workspace sf_attn_fwd needs for this descriptor: the
+ * split-K partials (fp32 running max, running sum and unnormalised output),
+ * 0 when the call needs no split.  Its contents need no initialisation;
+ * calls that may run concurrently need separate workspaces. */
 size_t sf_attn_workspace_bytes(const sf_attn_desc* desc);
 
 /* Split-K factor sf_attn_fwd will use for this descriptor. */

@@ -58,7 +58,8 @@ def attention(q, k, v, out=None, scale=0.0, is_causal=False, valid_len=None, num
     desc = make_desc(q, k, v, out, scale, is_causal, valid_len, num_splits)
     need = workspace_bytes(desc)
     if need and workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        # Zero-filled once: the split-K tickets at its head must start at 0.
+        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_n = workspace.numel() * workspace.element_size() if workspace is not None else 0
     s = stream if stream is not None else torch.cuda.current_stream(q.device)

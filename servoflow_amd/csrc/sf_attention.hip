@@ -34,10 +34,12 @@
 namespace sfk {
 
 constexpr int kKT = 128;    // keys per tile per workgroup (4 waves x 32)
-constexpr int kRow = 72;    // LDS row pitch in bf16 elements (144 B, bank-skewed)
+constexpr int kRow = 72;    // K tile pitch in bf16 elements (144 B, bank-skewed)
+constexpr int kVRow = 136;  // transposed V tile pitch in bf16 elements (272 B)
 constexpr int kD = 64;      // head dim this kernel family is built for
 constexpr int kQB = 5;      // 16-row query blocks per workgroup (80 rows >= 67)
 constexpr int kThreads = 256;
+constexpr int kMaxSplits = 64;
 
 struct AttnArgs {
     const uint16_t* q;
@@ -53,6 +55,7 @@ struct AttnArgs {
     int64_t o_sb, o_sh, o_ss;
     int B, H, Sq, Sk;
     int nsplit;
+    int nqc;          // query chunks
     int out_f32;
     int causal;
     float scale_log2;   // scale * log2(e)
@@ -69,10 +72,20 @@ __device__ __forceinline__ void store_out(const AttnArgs& a, int b, int h, int q
 }
 
 // One (b, h, query chunk, key split) per workgroup.
-__global__ __launch_bounds__(kThreads) void attn_split_kernel(const AttnArgs a) {
+//
+// LDS: K tile row-major [128 keys][72] (144-byte pitch), V tile transposed
+// [64 d][136] (272-byte pitch), so both MFMA operands are read with 16- and
+// 8-byte loads, plus the resident Q tile [80][72]: 47,360 bytes, small
+// enough for two workgroups per CU.  The next tile is prefetched into VGPRs
+// while the current one is contracted.
+__global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(const AttnArgs a) {
     constexpr int QR = 16 * kQB;
-    constexpr int kTileElems = kKT * kRow;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * kTileElems];
+    constexpr int kKElems = kKT * kRow;          // 9216
+    constexpr int kVElems = kD * kVRow;          // 8704
+    constexpr int kBufElems = kKElems + kVElems;
+    constexpr int kQElems = QR * kRow;           // 5760
+    __shared__ __attribute__((aligned(16))) uint16_t lds[kBufElems + kQElems];
+    uint16_t* const qs = lds + kBufElems;        // Q tile [80][72], resident
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -103,18 +116,74 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(const AttnArgs a) 
     const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
     const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
 
-    // Q as the B operand of S^T = K.Q^T: lane holds query row (16qb + r),
-    // head-dim elements [32dc + 8g, +8).
-    bf16x8 qf[kQB][2];
+    // Buffer resources: rows outside [0, Sq) / [0, kend) read as zeros from
+    // the hardware's range check, so loads need no branches or clamping.
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qp, (uint32_t)(a.Sq * a.q_ss * 2));
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, (uint32_t)(kend * a.k_ss * 2));
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vp, (uint32_t)(kend * a.v_ss * 2));
+
+    // Global -> register prefetch of one tile.  K: 1024 16-byte chunks, four
+    // per thread, 8 threads per 128-byte key row.  V: thread (kg = tid/8,
+    // c = tid%8) loads keys 4kg..4kg+3, head dims 8c..8c+7, so it can write
+    // four consecutive keys of one head dim into the transposed tile.
+    u32x4 pk[4], pv[4];
+    const int vkg = tid >> 3;
+    const int vc = tid & 7;
+    auto gload = [&](int kt) {
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
-        const int row = q0 + 16 * qb + r;
-#pragma unroll
-        for (int dc = 0; dc < 2; ++dc) {
-            qf[qb][dc] = row < a.Sq ? load_bf16x8(qp + row * a.q_ss + 32 * dc + 8 * g)
-                                    : zero_bf16x8();
+        for (int j = 0; j < 4; ++j) {
+            const int c = tid + kThreads * j;
+            const int key = kt + (c >> 3);
+            pk[j] = buffer_load16(krs, (uint32_t)((key * a.k_ss + (c & 7) * 8) * 2));
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int key = kt + 4 * vkg + j;
+            pv[j] = buffer_load16(vrs, (uint32_t)((key * a.v_ss + vc * 8) * 2));
+        }
+    };
+    auto lstore = [&]() {
+        uint16_t* kl = lds;
+        uint16_t* vt = kl + kKElems;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = tid + kThreads * j;
+            *reinterpret_cast<u32x4*>(kl + (c >> 3) * kRow + (c & 7) * 8) = pk[j];
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t x0 = pv[0][p], x1 = pv[1][p], x2 = pv[2][p], x3 = pv[3][p];
+            uint2 ev, od;
+            ev.x = (x0 & 0xffffu) | (x1 << 16);
+            ev.y = (x2 & 0xffffu) | (x3 << 16);
+            od.x = (x0 >> 16) | (x1 & 0xffff0000u);
+            od.y = (x2 >> 16) | (x3 & 0xffff0000u);
+            const int d = vc * 8 + 2 * p;
+            *reinterpret_cast<uint2*>(vt + d * kVRow + 4 * vkg) = ev;
+            *reinterpret_cast<uint2*>(vt + (d + 1) * kVRow + 4 * vkg) = od;
+        }
+    };
+
+    // Q tile -> LDS (rows >= Sq read as zeros).  Its loads overlap tile 0's.
+    u32x4 pq[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int c = tid + kThreads * j;          // 640 chunks of 16 bytes
+        const int row = c >> 3;
+        pq[j] = c < QR * 8 ? buffer_load16(qrs, (uint32_t)(((q0 + row) * a.q_ss + (c & 7) * 8) * 2))
+                           : u32x4{0u, 0u, 0u, 0u};
     }
+    if (ntiles > 0) gload(kbeg);
+    // Retire Q and tile 0 here so the loop's prefetch loads are only ever
+    // waited for where they are stored to LDS.
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int c = tid + kThreads * j;
+        if (c < QR * 8) *reinterpret_cast<u32x4*>(qs + (c >> 3) * kRow + (c & 7) * 8) = pq[j];
+    }
+    if (ntiles > 0) lstore();
+    __syncthreads();
 
     f32x4 acc[kQB][4];   // O^T blocks: lane holds d = 16db + 4g + i, q = 16qb + r
     float m[kQB], l[kQB];
@@ -126,139 +195,124 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(const AttnArgs a) 
         for (int db = 0; db < 4; ++db) acc[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // Global -> register prefetch of one tile: 1024 16-byte chunks of K and
-    // of V, four of each per thread; 8 threads cover one 128-byte key row.
-    u32x4 pk[4], pv[4];
-    auto gload = [&](int kt) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = tid + kThreads * j;
-            const int row = c >> 3;
-            const int col = (c & 7) * 8;
-            const int key = kt + row;
-            if (key < kend) {
-                pk[j] = *reinterpret_cast<const u32x4*>(kp + key * a.k_ss + col);
-                pv[j] = *reinterpret_cast<const u32x4*>(vp + key * a.v_ss + col);
-            } else {
-                pk[j] = u32x4{0u, 0u, 0u, 0u};
-                pv[j] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-    };
-    auto lstore = [&](int buf) {
-        uint16_t* kl = lds + buf * 2 * kTileElems;
-        uint16_t* vl = kl + kTileElems;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = tid + kThreads * j;
-            const int row = c >> 3;
-            const int col = (c & 7) * 8;
-            *reinterpret_cast<u32x4*>(kl + row * kRow + col) = pk[j];
-            *reinterpret_cast<u32x4*>(vl + row * kRow + col) = pv[j];
-        }
-    };
-
-    if (ntiles > 0) {
-        gload(kbeg);
-        lstore(0);
-    }
-    __syncthreads();
-
     for (int t = 0; t < ntiles; ++t) {
         const int kt = kbeg + t * kKT;
         if (t + 1 < ntiles) gload(kt + kKT);
 
-        const uint16_t* kl = lds + (t & 1) * 2 * kTileElems;
-        const uint16_t* vl = kl + kTileElems;
+        const uint16_t* kl = lds;
+        const uint16_t* vt = kl + kKElems;
         const int wkey = 32 * w;   // this wave's first key inside the tile
 
-        // ---- S^T = K . Q^T for the wave's 32 keys (two 16-key blocks).
-        f32x4 s[2][kQB];
+        // ---- Operand fragments shared by the five query blocks: K rows of
+        //      the wave's two 16-key blocks (A of S^T = K.Q^T) and V^T rows
+        //      (A of O^T += V^T.P^T) holding the 8 keys {4g..4g+3,
+        //      16+4g..16+4g+3}, the key order the S^T accumulator gives P^T.
+        bf16x8 kf[2][2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             const uint16_t* krow = kl + (wkey + 16 * kb + r) * kRow + 8 * g;
-            const bf16x8 k0 = load_bf16x8(krow);
-            const bf16x8 k1 = load_bf16x8(krow + 32);
-#pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
-                f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                z = mfma16x16x32(k0, qf[qb][0], z);
-                s[kb][qb] = mfma16x16x32(k1, qf[qb][1], z);
-            }
+            kf[kb][0] = load_bf16x8(krow);
+            kf[kb][1] = load_bf16x8(krow + 32);
         }
-
-        // ---- V^T fragments: lane holds d = 16db + r and the 8 keys
-        //      {4g..4g+3, 16+4g..16+4g+3} of the wave's 32 (the same key
-        //      order the S^T accumulator gives P^T).
         bf16x8 vf[4];
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-            uint16_t e[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int key = wkey + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
-                e[j] = vl[key * kRow + 16 * db + r];
-            }
-            u32x4 pw;
-            pw.x = (uint32_t)e[0] | ((uint32_t)e[1] << 16);
-            pw.y = (uint32_t)e[2] | ((uint32_t)e[3] << 16);
-            pw.z = (uint32_t)e[4] | ((uint32_t)e[5] << 16);
-            pw.w = (uint32_t)e[6] | ((uint32_t)e[7] << 16);
-            vf[db] = u32x4_as_bf16x8(pw);
+            const uint16_t* vrow = vt + (16 * db + r) * kVRow + wkey + 4 * g;
+            const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow);
+            const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + 16);
+            vf[db] = u32x4_as_bf16x8(u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
         }
+        const bool need_mask = a.causal || kt + kKT > kend;
 
-        const bool need_mask = a.causal || (kt + kKT > kend);
+        // ---- S^T for all five query blocks (lane: query 16qb + r, keys
+        //      16kb + 4g + i), raw (unscaled) scores.  Q is the B operand:
+        //      row 16qb + r, head dims [32dc + 8g, +8).  Each phase below is
+        //      straight-line over the five blocks so their MFMA, shuffle and
+        //      exp latencies overlap.
+        f32x4 s[kQB][2];
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
-            const int qrow = q0 + 16 * qb + r;
-            float x[8];
+            const uint16_t* qrow_l = qs + (16 * qb + r) * kRow + 8 * g;
+            const bf16x8 qf0 = load_bf16x8(qrow_l);
+            const bf16x8 qf1 = load_bf16x8(qrow_l + 32);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
+                f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                z = mfma16x16x32(kf[kb][0], qf0, z);
+                s[qb][kb] = mfma16x16x32(kf[kb][1], qf1, z);
+            }
+        }
+        // Keys past the split end (and future keys when causal) drop out.
+        if (need_mask) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float v = s[kb][qb][i] * a.scale_log2;
-                    if (need_mask) {
+            for (int qb = 0; qb < kQB; ++qb) {
+                const int qrow = q0 + 16 * qb + r;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
                         const int key = kt + wkey + 16 * kb + 4 * g + i;
                         const bool dead = key >= kend || (a.causal && key > qrow);
-                        v = dead ? -INFINITY : v;
+                        s[qb][kb][i] = dead ? -INFINITY : s[qb][kb][i];
                     }
-                    x[4 * kb + i] = v;
                 }
             }
-            float mx = x[0];
+        }
+        // Row maxima in log2 units (scale_log2 > 0, so the max of the raw
+        // scores scales): 8 keys per lane, then the 4 lane groups of a query.
+        float mx[kQB];
 #pragma unroll
-            for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[j]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mnew = fmaxf(m[qb], mx);
-            const float muse = mnew == -INFINITY ? 0.f : mnew;
-            const float alpha = fast_exp2(m[qb] - muse);
-            m[qb] = mnew;
-            float ls = l[qb] * alpha;
+        for (int qb = 0; qb < kQB; ++qb) {
+            const f32x4 u = s[qb][0], v = s[qb][1];
+            mx[qb] = fmaxf(fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3])),
+                           fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        }
 #pragma unroll
-            for (int db = 0; db < 4; ++db) acc[qb][db] *= alpha;
-
-            // P = exp2(x - m) split into bf16 hi (truncated) + bf16 lo.
-            uint32_t hi[8], lo[8];
+        for (int qb = 0; qb < kQB; ++qb) mx[qb] = fmaxf(mx[qb], __shfl_xor(mx[qb], 16, 64));
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb)
+            mx[qb] = fmaxf(mx[qb], __shfl_xor(mx[qb], 32, 64)) * a.scale_log2;
+        // Lazy rescale (one vote per tile): keep each row's reference max
+        // unless it grew by more than 2^8; P = exp2(x - m) then stays <= 256.
+        bool grow = false;
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) grow |= mx[qb] > m[qb] + 8.f;
+        if (__any(grow)) {
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+                const float mnew = fmaxf(m[qb], mx[qb]);
+                const float alpha = fast_exp2(m[qb] - (mnew == -INFINITY ? 0.f : mnew));
+                m[qb] = mnew;
+                l[qb] *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) acc[qb][db] *= alpha;
+            }
+        }
+        // P = exp2(s * scale_log2 - m) as a bf16 (hi, lo) pair: hi is the
+        // truncated top half of P, lo the bf16 of the exact remainder.  Then
+        // O^T += V^T . P^T for both halves.
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+            const float nmuse = m[qb] == -INFINITY ? 0.f : -m[qb];
+            float ls = l[qb];
+            uint32_t pb[8], lb[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float p = fast_exp2(x[j] - muse);
+                const float p = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nmuse));
                 ls += p;
-                const uint32_t pb = __float_as_uint(p);
-                const uint32_t ph = pb & 0xffff0000u;
-                hi[j] = ph;
-                lo[j] = __float_as_uint(p - __uint_as_float(ph)) & 0xffff0000u;
+                pb[j] = __float_as_uint(p);
+                lb[j] = __float_as_uint(p - __uint_as_float(pb[j] & 0xffff0000u));
             }
             l[qb] = ls;
-            u32x4 phw, plw;
-            phw.x = (hi[0] >> 16) | hi[1];
-            phw.y = (hi[2] >> 16) | hi[3];
-            phw.z = (hi[4] >> 16) | hi[5];
-            phw.w = (hi[6] >> 16) | hi[7];
-            plw.x = (lo[0] >> 16) | lo[1];
-            plw.y = (lo[2] >> 16) | lo[3];
-            plw.z = (lo[4] >> 16) | lo[5];
-            plw.w = (lo[6] >> 16) | lo[7];
+            // perm selector 0x07060302: high halves of (second, first).
+            const u32x4 phw = {__builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u),
+                               __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
+                               __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u),
+                               __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)};
+            const u32x4 plw = {__builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u),
+                               __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u),
+                               __builtin_amdgcn_perm(lb[5], lb[4], 0x07060302u),
+                               __builtin_amdgcn_perm(lb[7], lb[6], 0x07060302u)};
             const bf16x8 ph8 = u32x4_as_bf16x8(phw);
             const bf16x8 pl8 = u32x4_as_bf16x8(plw);
 #pragma unroll
@@ -268,7 +322,10 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(const AttnArgs a) 
             }
         }
 
-        if (t + 1 < ntiles) lstore((t + 1) & 1);
+        if (t + 1 < ntiles) {
+            __syncthreads();   // every wave is done reading the tile
+            lstore();
+        }
         __syncthreads();
     }
 
@@ -280,12 +337,13 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(const AttnArgs a) 
         l[qb] += __shfl_xor(l[qb], 32, 64);
     }
 
-    // ---- Merge the four waves' (m, l, O) through LDS (tile buffers reused).
-    float* sm = reinterpret_cast<float*>(lds);   // [4][QR]
-    float* sl = sm + 4 * QR;                     // [4][QR]
-    float* sM = sl + 4 * QR;                     // [QR] merged max
-    float* sL = sM + QR;                         // [QR] merged sum
-    float* so = sL + QR;                         // [4][QR][32] half of O
+    // ---- Merge the four waves' (m, l, O).  Wave w owns head dims
+    //      [16w, 16w + 16); the other waves hand it their partial sums for
+    //      that d-block through LDS in two rounds (owners 0,1 then 2,3), so
+    //      each output element is summed once and stored as a 4-vector.
+    float* xo = reinterpret_cast<float*>(lds);          // [4 w][2 slot][kQB][64 lanes][4]
+    float* sm = xo + 4 * 2 * kQB * 64 * 4;               // [4][QR]
+    float* sl = sm + 4 * QR;                             // [4][QR]
     if (g == 0) {
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
@@ -294,20 +352,16 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(const AttnArgs a) 
         }
     }
     __syncthreads();
-    if (tid < QR) {
-        float M = sm[tid];
-        for (int ww = 1; ww < 4; ++ww) M = fmaxf(M, sm[ww * QR + tid]);
-        const float Muse = M == -INFINITY ? 0.f : M;
-        float L = 0.f;
-        for (int ww = 0; ww < 4; ++ww) L += sl[ww * QR + tid] * fast_exp2(sm[ww * QR + tid] - Muse);
-        sM[tid] = M;
-        sL[tid] = L;
-    }
-    __syncthreads();
+    float Lq[kQB], Mq[kQB];
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
-        const float M = sM[16 * qb + r];
+        const int q = 16 * qb + r;
+        const float m0 = sm[q], m1 = sm[QR + q], m2 = sm[2 * QR + q], m3 = sm[3 * QR + q];
+        const float M = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
         const float Muse = M == -INFINITY ? 0.f : M;
+        Lq[qb] = sl[q] * fast_exp2(m0 - Muse) + sl[QR + q] * fast_exp2(m1 - Muse) +
+                 sl[2 * QR + q] * fast_exp2(m2 - Muse) + sl[3 * QR + q] * fast_exp2(m3 - Muse);
+        Mq[qb] = M;
         const float f = fast_exp2(m[qb] - Muse);
 #pragma unroll
         for (int db = 0; db < 4; ++db) acc[qb][db] *= f;
@@ -315,63 +369,96 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(const AttnArgs a) 
 
     const size_t bh = (size_t)b * a.H + h;
     const size_t pbase = (bh * nsplit + split) * (size_t)a.Sq;
-    for (int half = 0; half < 2; ++half) {
+    const int d0 = 16 * w + 4 * g;
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
+    for (int round = 0; round < 2; ++round) {
 #pragma unroll
-            for (int dbh = 0; dbh < 2; ++dbh) {
-                const int db = 2 * half + dbh;
-                float* dst = so + (w * QR + 16 * qb + r) * 32 + 16 * dbh + 4 * g;
-                *reinterpret_cast<f32x4*>(dst) = acc[qb][db];
-            }
+        for (int j = 0; j < 2; ++j) {
+            const int owner = 2 * round + j;
+            if (owner == w) continue;
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb)
+                *reinterpret_cast<f32x4*>(xo + (((w * 2 + j) * kQB + qb) * 64 + lane) * 4) =
+                    acc[qb][owner];
         }
         __syncthreads();
-        for (int idx = tid; idx < QR * 32; idx += kThreads) {
-            const int qq = idx >> 5;
-            const int dd = idx & 31;
-            const int qrow = q0 + qq;
-            if (qrow < a.Sq) {
-                float val = so[qq * 32 + dd] + so[(QR + qq) * 32 + dd] +
-                            so[(2 * QR + qq) * 32 + dd] + so[(3 * QR + qq) * 32 + dd];
-                const int d = 32 * half + dd;
+        if ((w >> 1) == round) {
+            const int j = w & 1;
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+                // acc[qb][w] with constant indices (a runtime index would move
+                // the accumulators to scratch memory).
+                f32x4 o = j ? acc[qb][2 * round + 1] : acc[qb][2 * round];
+#pragma unroll
+                for (int ww = 0; ww < 4; ++ww) {
+                    if (ww == w) continue;
+                    o += *reinterpret_cast<const f32x4*>(xo + (((ww * 2 + j) * kQB + qb) * 64 + lane) * 4);
+                }
+                const int q = q0 + 16 * qb + r;
+                if (q >= a.Sq) continue;
                 if (nsplit == 1) {
-                    const float L = sL[qq];
-                    store_out(a, b, h, qrow, d, L > 0.f ? val / L : 0.f);
+                    const float inv = Lq[qb] > 0.f ? 1.f / Lq[qb] : 0.f;
+                    o *= inv;
+                    const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + d0;
+                    if (a.out_f32) {
+                        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.o) + off) = o;
+                    } else {
+                        uint2 pk2;
+                        pk2.x = pack_bf16x2(o[0], o[1]);
+                        pk2.y = pack_bf16x2(o[2], o[3]);
+                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.o) + off) = pk2;
+                    }
                 } else {
-                    a.part_o[(pbase + qrow) * kD + d] = val;
+                    *reinterpret_cast<f32x4*>(a.part_o + (pbase + q) * kD + d0) = o;
+                    if (w == 0 && g == 0) {
+                        a.part_ml[(pbase + q) * 2 + 0] = Mq[qb];
+                        a.part_ml[(pbase + q) * 2 + 1] = Lq[qb];
+                    }
                 }
             }
         }
-        __syncthreads();
+        if (round == 0) __syncthreads();
     }
-    if (nsplit > 1 && tid < QR && q0 + tid < a.Sq) {
-        a.part_ml[(pbase + q0 + tid) * 2 + 0] = sM[tid];
-        a.part_ml[(pbase + q0 + tid) * 2 + 1] = sL[tid];
-    }
+
 }
 
-// Log-sum-exp merge of the split partials: one thread per (q, d).
+// Log-sum-exp merge of the split partials.  One wave per output row
+// (b, h, q): lane s < nsplit loads split s's (max, sum), the wave reduces
+// them, and each lane then accumulates head dim d = lane over the splits with
+// the loads unrolled so they overlap.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
-    const int tid = threadIdx.x;
-    const int q = blockIdx.x * 4 + (tid >> 6);
-    const int d = tid & 63;
+    const int lane = threadIdx.x & 63;
+    const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int h = blockIdx.y;
     const int b = blockIdx.z;
     if (q >= a.Sq) return;
     const int ns = a.nsplit;
-    const size_t bh = (size_t)b * a.H + h;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s)
-        M = fmaxf(M, a.part_ml[((bh * ns + s) * a.Sq + q) * 2]);
-    const float Muse = M == -INFINITY ? 0.f : M;
-    float L = 0.f, O = 0.f;
-    for (int s = 0; s < ns; ++s) {
-        const size_t row = (bh * ns + s) * a.Sq + q;
-        const float f = fast_exp2(a.part_ml[row * 2] - Muse);
-        L += f * a.part_ml[row * 2 + 1];
-        O += f * a.part_o[row * kD + d];
+    const size_t row0 = ((size_t)b * a.H + h) * ns * (size_t)a.Sq + q;   // split 0's row
+    float ms = -INFINITY, ls = 0.f;
+    if (lane < ns) {
+        const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (row0 + (size_t)lane * a.Sq) * 2);
+        ms = ml.x;
+        ls = ml.y;
     }
-    store_out(a, b, h, q, d, L > 0.f ? O / L : 0.f);
+    float M = ms;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    const float Muse = M == -INFINITY ? 0.f : M;
+    float wgt = lane < ns ? fast_exp2(ms - Muse) : 0.f;
+    float L = wgt * ls;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
+    wgt *= L > 0.f ? 1.f / L : 0.f;
+    float o = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            v[j] = s0 + j < ns ? a.part_o[(row0 + (size_t)(s0 + j) * a.Sq) * kD + lane] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o += __shfl(wgt, s0 + j < ns ? s0 + j : 0, 64) * v[j];
+    }
+    store_out(a, b, h, q, lane, o);
 }
 
 }  // namespace sfk
@@ -381,18 +468,23 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kMaxSplits = 64;
+using sfk::kMaxSplits;
 
 int query_chunks(const sf_attn_desc* d) { return (d->Sq + 16 * sfk::kQB - 1) / (16 * sfk::kQB); }
+
+// MI355X has 256 CUs and the split kernel fits two workgroups per CU (two
+// waves per SIMD).  Splits are chosen so the grid is one round of
+// workgroups, each split covering at least 256 keys.
+constexpr long kNumCUs = 256;
+constexpr long kWgPerCU = 2;
 
 int choose_splits(const sf_attn_desc* d) {
     if (d->num_splits > 0) return d->num_splits < kMaxSplits ? d->num_splits : kMaxSplits;
     const long base = (long)d->B * d->H * query_chunks(d);
     if (base <= 0) return 1;
-    // Aim for ~2 workgroups per CU on a 256-CU part, with >= 256 keys a split.
-    long want = (512 + base - 1) / base;
-    long cap = d->Sk / 256;
-    long ns = want < cap ? want : cap;
+    long ns = kNumCUs * kWgPerCU / base;
+    const long cap = d->Sk / 256;
+    if (ns > cap) ns = cap;
     if (ns < 1) ns = 1;
     if (ns > kMaxSplits) ns = kMaxSplits;
     return (int)ns;
@@ -407,6 +499,7 @@ int validate(const sf_attn_desc* d) {
     if (d->in_dtype != SF_BF16) return SF_ENOTSUP;
     if (d->out_dtype != SF_BF16 && d->out_dtype != SF_F32) return SF_ENOTSUP;
     if (d->num_splits < 0) return SF_EINVAL;
+    if (!(d->scale >= 0.f)) return SF_ENOTSUP;   // negative or NaN scale
     const int64_t* st[4] = {d->q_stride, d->k_stride, d->v_stride, d->o_stride};
     for (int i = 0; i < 3; ++i)
         for (int j = 0; j < 3; ++j)
@@ -414,6 +507,11 @@ int validate(const sf_attn_desc* d) {
     for (int j = 0; j < 3; ++j)
         if (d->o_stride[j] < 0) return SF_EINVAL;
     if (d->Sk == 0 && d->B > 0 && d->H > 0 && d->Sq > 0) return SF_EINVAL;
+    // Per-head byte ranges are addressed with 32-bit buffer offsets.
+    if ((int64_t)d->Sq * d->q_stride[2] * 2 > 0x7fffffffLL ||
+        (int64_t)d->Sk * d->k_stride[2] * 2 > 0x7fffffffLL ||
+        (int64_t)d->Sk * d->v_stride[2] * 2 > 0x7fffffffLL)
+        return SF_ENOTSUP;
     return SF_OK;
 }
 
@@ -470,6 +568,7 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     a.o_sb = d->o_stride[0]; a.o_sh = d->o_stride[1]; a.o_ss = d->o_stride[2];
     a.B = d->B; a.H = d->H; a.Sq = d->Sq; a.Sk = d->Sk;
     a.nsplit = ns;
+    a.nqc = nqc;
     a.out_f32 = d->out_dtype == SF_F32;
     a.causal = d->is_causal != 0;
     const float scale = d->scale != 0.f ? d->scale : 1.f / sqrtf((float)d->D);

@@ -99,3 +99,6 @@ def test_workspace_contract():
     assert abi.lib().sf_attn_workspace_bytes(ctypes.byref(d1)) == 0
     d1.num_splits = 3
     assert abi.lib().sf_attn_workspace_bytes(ctypes.byref(d1)) == 32 * 3 * 67 * 66 * 4
+    d1.num_splits = 0
+    d1.scale = -1.0
+    assert _fwd(d1) == abi.SF_ENOTSUP

@@ -152,7 +152,7 @@ def test_graph_capture_replays_match_eager():
     k, v = to_dev(rounded(212, (1, 32, 4374, 64))), to_dev(rounded(213, (1, 32, 4374, 64)))
     out = torch.empty(1, 32, 67, 64, device=DEV, dtype=torch.float32)
     from servoflow_amd.attention import make_desc, workspace_bytes
-    ws = torch.empty(workspace_bytes(make_desc(q, k, v, out)), dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(workspace_bytes(make_desc(q, k, v, out)), dtype=torch.uint8, device=DEV)
     attention(q, k, v, out=out, workspace=ws)
     torch.cuda.synchronize()
     eager = out.clone()
@@ -182,3 +182,24 @@ def test_error_paths_on_device():
     with pytest.raises(abi.SfError) as e:
         attention(q128, q128, q128)
     assert e.value.status == abi.SF_ENOTSUP
+
+
+def test_workspace_reuse_across_calls():
+    from servoflow_amd.attention import make_desc, workspace_bytes
+    q = to_dev(rounded(231, (2, 32, 67, 64)))
+    k, v = to_dev(rounded(232, (2, 32, 1500, 64))), to_dev(rounded(233, (2, 32, 1500, 64)))
+    out = torch.empty(2, 32, 67, 64, device=DEV, dtype=torch.float32)
+    need = workspace_bytes(make_desc(q, k, v, out, num_splits=5))
+    ws = torch.full((need,), 0x7f, dtype=torch.uint8, device=DEV)   # garbage contents are fine
+    ref = None
+    for i in range(3):
+        attention(q, k, v, out=out, workspace=ws, num_splits=5)
+        torch.cuda.synchronize()
+        if ref is None:
+            ref = out.clone()
+        assert torch.equal(out, ref), f"call {i}"
+        # a smaller problem reusing the same workspace in between
+        attention(q[:1], k[:1, :, :700], v[:1, :, :700], workspace=ws, num_splits=3)
+    torch.cuda.synchronize()
+    assert_close_bf16(ref.cpu().numpy(), O.attention_f32(*(x.float().cpu().numpy() for x in (q, k, v))),
+                      "reuse")
