@@ -108,6 +108,83 @@ int sf_attn_fwd(const sf_attn_desc* desc, const void* q, const void* k,
                 const void* v, void* out, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Projections: C[M,N] = act(A[M,K] . W[N,K]^T + bias[N]).
+ *
+ * Replaces IBackend::gemm_bias_act as the RDT layers call it (trans_b = true;
+ * backend.h:159-183, cuda_backend.cu:337-467; callers dit_block.cu:152-160,
+ * 207, 233, 284, 291, 321) and folds in the ops around it:
+ *   act: SF_ACT_GELU_TANH is GeluOp, SF_ACT_SILU is SiluOp
+ *        (src/backend/cuda/ops/elementwise.cuh:35-68);
+ *   epilogue SF_EPI_PLAIN: C (row stride ldc) in c_dtype; accumulate != 0
+ *        adds into an fp32 C (the residual adds of dit_block.cu:372-384);
+ *   epilogue SF_EPI_HEADS: the N columns are 1..3 sections of H*64 (Q|K|V or
+ *        K|V, the order of split_qkv / split_kv, split_ops.cuh:62-84,
+ *        210-226); section j goes to head_out[j][b][h][s][d] (bf16, element
+ *        strides head_stride[j] = {b, h, s}) with row m = b*S + s, after an
+ *        RMSNorm over the 64 head dims with head_gamma[j] when that pointer
+ *        is non-NULL (q_norm / k_norm, dit_block.cu:219-220, 307-308);
+ *   w_dtype SF_I8: int8 weights with one fp32 scale per row (w_scale[N]),
+ *        the weight-only dequant of quantization.cu:18-51 done in registers.
+ * A and W rows must be 16-byte aligned (lda, ldw multiples of 8 elements),
+ * K a multiple of 32; bias, w_scale, head_gamma are fp32.
+ * ------------------------------------------------------------------------- */
+typedef enum sf_act { SF_ACT_NONE = 0, SF_ACT_GELU_TANH = 1, SF_ACT_SILU = 2 } sf_act;
+typedef enum sf_epilogue { SF_EPI_PLAIN = 0, SF_EPI_HEADS = 1 } sf_epilogue;
+
+typedef struct sf_gemm_desc {
+    int32_t M, N, K;
+    const void* A;          /* [M][lda] bf16 */
+    int64_t lda;
+    int32_t a_dtype;
+    const void* W;          /* [N][ldw] bf16 or int8 */
+    int64_t ldw;
+    int32_t w_dtype;
+    const float* w_scale;   /* [N] for int8 weights */
+    const float* bias;      /* [N] or NULL */
+    int32_t act;
+    int32_t epilogue;
+    void* C;                /* SF_EPI_PLAIN output */
+    int64_t ldc;
+    int32_t c_dtype;
+    int32_t accumulate;
+    int32_t H, S;           /* SF_EPI_HEADS: heads per section, rows per batch */
+    float eps;
+    const float* head_gamma[3];
+    void* head_out[3];
+    int64_t head_stride[3][3];
+} sf_gemm_desc;
+
+int sf_gemm(const sf_gemm_desc* desc, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Normalisation and dequant.
+ * ------------------------------------------------------------------------- */
+/* out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * gamma, fp32 accumulation
+ * (rms_norm_kernel_impl, src/backend/cuda/ops/norm.cuh:89-122;
+ * IBackend::rms_norm, backend.h:120-122).  x in SF_F32 or SF_BF16, out in
+ * SF_BF16 or SF_F32, gamma fp32 [cols]. */
+int sf_rmsnorm(const void* x, int32_t x_dtype, int64_t ldx, const float* gamma,
+               void* out, int32_t out_dtype, int64_t ldo, int32_t rows,
+               int32_t cols, float eps, void* stream);
+
+/* residual[r] += delta[r]; out[r] = rmsnorm(residual[r]) * gamma
+ * (fused_add_rms_norm_kernel, norm.cuh:130-171; IBackend::fused_add_rms_norm,
+ * backend.h:127-134).  residual fp32 (kept in fp32 here), delta SF_F32 or
+ * SF_BF16, out SF_BF16 or SF_F32. */
+int sf_add_rmsnorm(const void* delta, int32_t delta_dtype, float* residual,
+                   const float* gamma, void* out, int32_t out_dtype,
+                   int32_t rows, int32_t cols, float eps, void* stream);
+
+/* out[i] = float(q[i]) * scale[i / K] (per_channel != 0) or * scale[0],
+ * q int8 [N][K] row-major (dequantize_int8_fp16_kernel,
+ * src/backend/cuda/ops/quantization.cu:18-51; IBackend::dequantize,
+ * backend.h:205-206).  out in SF_F32 or SF_BF16 (the reference writes fp16
+ * with an fp16 scale; here the scale is fp32). */
+int sf_dequant_int8(const int8_t* q, const float* scale, int32_t per_channel,
+                    void* out, int32_t out_dtype, int64_t N, int64_t K,
+                    void* stream);
+
 /* Static text for a status code. */
 const char* sf_strerror(int status);
 

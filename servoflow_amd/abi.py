@@ -48,6 +48,33 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+SF_ACT_NONE = 0
+SF_ACT_GELU_TANH = 1
+SF_ACT_SILU = 2
+SF_EPI_PLAIN = 0
+SF_EPI_HEADS = 1
+
+
+class GemmDesc(ctypes.Structure):
+    """Mirror of `sf_gemm_desc`."""
+
+    _fields_ = [
+        ("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32),
+        ("A", ctypes.c_void_p), ("lda", ctypes.c_int64), ("a_dtype", ctypes.c_int32),
+        ("W", ctypes.c_void_p), ("ldw", ctypes.c_int64), ("w_dtype", ctypes.c_int32),
+        ("w_scale", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("act", ctypes.c_int32),
+        ("epilogue", ctypes.c_int32),
+        ("C", ctypes.c_void_p), ("ldc", ctypes.c_int64), ("c_dtype", ctypes.c_int32),
+        ("accumulate", ctypes.c_int32),
+        ("H", ctypes.c_int32), ("S", ctypes.c_int32), ("eps", ctypes.c_float),
+        ("head_gamma", ctypes.c_void_p * 3),
+        ("head_out", ctypes.c_void_p * 3),
+        ("head_stride", (ctypes.c_int64 * 3) * 3),
+    ]
+
+
 class SfError(RuntimeError):
     def __init__(self, status: int, what: str):
         super().__init__(f"{what}: {strerror(status)} (status {status})")
@@ -77,6 +104,15 @@ def lib() -> ctypes.CDLL:
     L.sf_attn_fwd.argtypes = [P, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     L.sf_attn_fwd.restype = ctypes.c_int
+    L.sf_gemm.argtypes = [ctypes.POINTER(GemmDesc), ctypes.c_void_p]
+    L.sf_gemm.restype = ctypes.c_int
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    L.sf_rmsnorm.argtypes = [vp, i32, i64, vp, vp, i32, i64, i32, i32, ctypes.c_float, vp]
+    L.sf_rmsnorm.restype = ctypes.c_int
+    L.sf_add_rmsnorm.argtypes = [vp, i32, vp, vp, vp, i32, i32, i32, ctypes.c_float, vp]
+    L.sf_add_rmsnorm.restype = ctypes.c_int
+    L.sf_dequant_int8.argtypes = [vp, vp, i32, vp, i32, i64, i64, vp]
+    L.sf_dequant_int8.restype = ctypes.c_int
     L.sf_strerror.argtypes = [ctypes.c_int]
     L.sf_strerror.restype = ctypes.c_char_p
     _lib = L

@@ -1,0 +1,94 @@
+"""Torch-tensor front ends for sf_gemm, sf_rmsnorm, sf_add_rmsnorm and
+sf_dequant_int8 (test and bench plumbing: torch supplies device memory and
+the stream; the arithmetic runs in libsf_hip_kernels.so)."""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import abi
+
+_DT = {torch.bfloat16: abi.SF_BF16, torch.float32: abi.SF_F32, torch.int8: abi.SF_I8}
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat16,
+         accumulate=False, w_scale=None):
+    """out[M,N] = act(a[M,K] w[N,K]^T + bias) (bf16 a; bf16 or int8 w with
+    per-row fp32 w_scale).  accumulate adds into an fp32 `out`."""
+    M, K = a.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=out_dtype, device=a.device)
+    d = abi.GemmDesc()
+    d.M, d.N, d.K = M, N, K
+    d.A, d.lda, d.a_dtype = a.data_ptr(), a.stride(0), _DT[a.dtype]
+    d.W, d.ldw, d.w_dtype = w.data_ptr(), w.stride(0), _DT[w.dtype]
+    d.w_scale = _p(w_scale)
+    d.bias = _p(bias)
+    d.act = act
+    d.epilogue = abi.SF_EPI_PLAIN
+    d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), _DT[out.dtype]
+    d.accumulate = 1 if accumulate else 0
+    abi.check(abi.lib().sf_gemm(ctypes.byref(d), _stream(a)), "sf_gemm")
+    return out
+
+
+def gemm_heads(a, w, bias, S, H, outs, gammas=(None, None, None), eps=1e-6, w_scale=None):
+    """Projection whose N columns are sections of H*64, written per head to
+    outs[j] ([B,H,S,64] bf16 views) with optional per-head RMSNorm."""
+    M, K = a.shape
+    N = w.shape[0]
+    d = abi.GemmDesc()
+    d.M, d.N, d.K = M, N, K
+    d.A, d.lda, d.a_dtype = a.data_ptr(), a.stride(0), _DT[a.dtype]
+    d.W, d.ldw, d.w_dtype = w.data_ptr(), w.stride(0), _DT[w.dtype]
+    d.w_scale = _p(w_scale)
+    d.bias = _p(bias)
+    d.epilogue = abi.SF_EPI_HEADS
+    d.H, d.S, d.eps = H, S, eps
+    for j, o in enumerate(outs):
+        d.head_out[j] = o.data_ptr()
+        d.head_gamma[j] = _p(gammas[j])
+        d.head_stride[j][:] = (o.stride(0), o.stride(1), o.stride(2))
+    abi.check(abi.lib().sf_gemm(ctypes.byref(d), _stream(a)), "sf_gemm")
+    return outs
+
+
+def rmsnorm(x, gamma, eps=1e-6, out_dtype=torch.bfloat16, out=None):
+    rows, cols = x.shape
+    if out is None:
+        out = torch.empty(rows, cols, dtype=out_dtype, device=x.device)
+    st = abi.lib().sf_rmsnorm(x.data_ptr(), _DT[x.dtype], x.stride(0), gamma.data_ptr(),
+                              out.data_ptr(), _DT[out.dtype], out.stride(0), rows, cols, eps,
+                              _stream(x))
+    abi.check(st, "sf_rmsnorm")
+    return out
+
+
+def add_rmsnorm(delta, residual, gamma, eps=1e-6, out_dtype=torch.bfloat16):
+    rows, cols = residual.shape
+    out = torch.empty(rows, cols, dtype=out_dtype, device=residual.device)
+    st = abi.lib().sf_add_rmsnorm(delta.data_ptr(), _DT[delta.dtype], residual.data_ptr(),
+                                  gamma.data_ptr(), out.data_ptr(), _DT[out.dtype], rows, cols,
+                                  eps, _stream(residual))
+    abi.check(st, "sf_add_rmsnorm")
+    return out
+
+
+def dequant_int8(q, scale, per_channel=True, out_dtype=torch.float32):
+    N = q.shape[0]
+    K = q.numel() // max(N, 1)
+    out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
+    st = abi.lib().sf_dequant_int8(q.data_ptr(), scale.data_ptr(), 1 if per_channel else 0,
+                                   out.data_ptr(), _DT[out_dtype], N, K, _stream(q))
+    abi.check(st, "sf_dequant_int8")
+    return out

@@ -1,0 +1,169 @@
+"""GPU parity of sf_gemm, sf_rmsnorm, sf_add_rmsnorm and sf_dequant_int8
+against the CPU oracle (bf16-rounded inputs shared by both sides).
+
+GEMM inputs are bf16, so products are exact and only the fp32 summation
+order differs from the oracle: fp32 outputs are held to max-abs <= 2e-2 and
+mean-rel <= 1e-4.  The int8 unpack and indexing are bit-exact (dequant
+kernel vs oracle, all 256 codes, the reference's KATs)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_close_bf16, mean_rel
+from oracle import oracle as O
+from servoflow_amd import abi
+from servoflow_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def rounded(seed, shape, scale=1.0):
+    return O.bf16_round(O.randn(seed, shape) * scale)
+
+
+def dev(x, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV).to(dtype)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def close(got, ref, what, rel=1e-4):
+    assert np.isfinite(got).all(), what
+    mx = float(np.abs(got - ref).max())
+    mr = mean_rel(got, ref)
+    assert mx <= 2e-2 and mr <= rel, f"{what}: max-abs {mx:.3e} mean-rel {mr:.3e}"
+
+
+@pytest.mark.parametrize("M,N,K", [(67, 2048, 2048), (1, 2048, 256), (80, 6144, 2048),
+                                   (81, 100, 1152), (200, 48, 64), (64, 2048, 256), (16, 128, 2048)])
+@pytest.mark.parametrize("act", [abi.SF_ACT_NONE, abi.SF_ACT_GELU_TANH, abi.SF_ACT_SILU])
+def test_gemm_bias_act_f32_out(M, N, K, act):
+    a, w = rounded(1 + M, (M, K)), rounded(2 + N, (N, K), 0.02)
+    b = O.randn(3, (N,), 0.02)
+    got = host(K_gemm(a, w, b, act))
+    ref = O.linear(a, w, b, act=act)
+    close(got, ref, f"gemm {M}x{N}x{K} act {act}")
+
+
+def K_gemm(a, w, b, act, out_dtype=torch.float32):
+    return K.gemm(dev(a), dev(w), dev(b, torch.float32) if b is not None else None, act,
+                  out_dtype=out_dtype)
+
+
+def test_gemm_bf16_out_is_rounded_f32():
+    a, w = rounded(11, (67, 2048)), rounded(12, (2048, 2048), 0.02)
+    f32 = host(K_gemm(a, w, None, 0))
+    b16 = host(K_gemm(a, w, None, 0, torch.bfloat16))
+    assert np.array_equal(b16, O.bf16_round(f32))
+
+
+def test_gemm_accumulate_into_residual():
+    a, w = rounded(21, (67, 2048)), rounded(22, (2048, 2048), 0.02)
+    b = O.randn(23, (2048,), 0.02)
+    x = O.randn(24, (67, 2048))
+    xd = dev(x, torch.float32)
+    K.gemm(dev(a), dev(w), dev(b, torch.float32), out=xd, accumulate=True)
+    close(host(xd), x + O.linear(a, w, b), "residual add", rel=1e-5)
+
+
+def test_gemm_heads_qkv_with_qk_norm():
+    B, S, H, D = 2, 67, 32, 64
+    a = rounded(31, (B * S, 2048))
+    w = rounded(32, (3 * H * D, 2048), 0.02)
+    b = O.randn(33, (3 * H * D,), 0.02)
+    gq = 1.0 + O.randn(34, (64,), 0.1)
+    gk = 1.0 + O.randn(35, (64,), 0.1)
+    outs = [torch.empty(B, H, S, D, device=DEV, dtype=torch.bfloat16) for _ in range(3)]
+    K.gemm_heads(dev(a), dev(w), dev(b, torch.float32), S, H, outs,
+                 (dev(gq, torch.float32), dev(gk, torch.float32), None))
+    qkv = O.linear(a, w, b).reshape(B, S, 3 * H * D)
+    Q, Kh, V = O.split_qkv(qkv, H, D)
+    Q = O.rms_norm(Q, gq)
+    Kh = O.rms_norm(Kh, gk)
+    for got, ref, nm in zip(outs, (Q, Kh, V), "QKV"):
+        g = host(got)
+        assert np.all(np.abs(g - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-3), nm  # within a bf16 ulp
+        assert mean_rel(g, ref) < 3e-3, nm
+
+
+def test_gemm_heads_kv_strided_output():
+    # cross-attention K/V projection of 729 condition tokens into [B,H,Sk,D]
+    B, S, H, D = 1, 729, 32, 64
+    a = rounded(41, (B * S, 2048))
+    w = rounded(42, (2 * H * D, 2048), 0.02)
+    b = O.randn(43, (2 * H * D,), 0.02)
+    gk = 1.0 + O.randn(44, (64,), 0.1)
+    outs = [torch.empty(B, H, S, D, device=DEV, dtype=torch.bfloat16) for _ in range(2)]
+    K.gemm_heads(dev(a), dev(w), dev(b, torch.float32), S, H, outs, (dev(gk, torch.float32), None))
+    kv = O.linear(a, w, b).reshape(B, S, 2 * H * D)
+    Kh, V = O.split_kv(kv, H, D)
+    Kh = O.rms_norm(Kh, gk)
+    for got, ref in zip(outs, (Kh, V)):
+        assert mean_rel(host(got), ref) < 3e-3
+
+
+def test_gemm_int8_weights():
+    a = rounded(51, (67, 2048))
+    wf = O.randn(52, (2048, 2048), 0.02)
+    q, s = O.quantize_int8_rows(wf)
+    b = O.randn(53, (2048,), 0.02)
+    got = host(K.gemm(dev(a), dev(q, torch.int8), dev(b, torch.float32), out_dtype=torch.float32,
+                      w_scale=dev(s, torch.float32)))
+    ref = O.linear(a, O.dequant_int8(q, s), b)
+    close(got, ref, "int8 gemm")
+
+
+def test_rmsnorm_matches_oracle():
+    x = O.randn(61, (67, 2048)) * 3.0
+    g = 1.0 + O.randn(62, (2048,), 0.1)
+    got = host(K.rmsnorm(dev(x, torch.float32), dev(g, torch.float32), out_dtype=torch.float32))
+    ref = O.rms_norm(x, g)
+    assert np.abs(got - ref).max() < 1e-5
+    b16 = host(K.rmsnorm(dev(x, torch.float32), dev(g, torch.float32)))
+    # the bf16 output is the fp32 result rounded: within one bf16 ulp of the oracle
+    assert np.all(np.abs(b16 - ref) <= np.abs(ref) * 2.0 ** -7)
+    assert np.mean(b16 == O.bf16_round(ref)) > 0.999
+
+
+def test_add_rmsnorm_updates_residual():
+    x = O.randn(71, (67, 2048))
+    dlt = rounded(72, (67, 2048))
+    g = 1.0 + O.randn(73, (2048,), 0.1)
+    res = dev(x, torch.float32)
+    out = K.add_rmsnorm(dev(dlt), res, dev(g, torch.float32), out_dtype=torch.float32)
+    ref_out, ref_res = O.fused_add_rms_norm(dlt, x, g)
+    assert np.array_equal(host(res), ref_res)
+    assert np.abs(host(out) - ref_out).max() < 1e-5
+
+
+def test_dequant_reference_kats_and_exhaustive():
+    kats = json.load(open(os.path.join(ROOT, "tests", "golden", "reference_kats.json")))
+    for key in ("dequant_per_tensor", "dequant_per_channel"):
+        k = kats[key]
+        q = np.array(k["input"], np.int8).reshape(k["shape"])
+        s = np.array(k["scale"], np.float32)
+        got = host(K.dequant_int8(dev(q, torch.int8), dev(s, torch.float32), len(s) > 1))
+        assert np.abs(got.ravel() - np.array(k["expected"])).max() <= k["tol"]
+        assert np.array_equal(got, O.dequant_int8(q, s, len(s) > 1))
+    q = np.arange(-128, 128, dtype=np.int8).reshape(4, 64)
+    s = np.array([1.0, 0.5, 3.0, 1.0 / 127], np.float32)
+    got = host(K.dequant_int8(dev(q, torch.int8), dev(s, torch.float32)))
+    assert np.array_equal(got, O.dequant_int8(q, s))      # bit-exact unpack + row index
+    got16 = host(K.dequant_int8(dev(q, torch.int8), dev(s, torch.float32), out_dtype=torch.bfloat16))
+    assert np.array_equal(got16, O.bf16_round(O.dequant_int8(q, s)))
+
+
+def test_gemm_rejects_bad_shapes():
+    a = torch.zeros(4, 48, device=DEV, dtype=torch.bfloat16)   # K = 48 not a multiple of 32
+    w = torch.zeros(16, 48, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(abi.SfError) as e:
+        K.gemm(a, w)
+    assert e.value.status == abi.SF_ENOTSUP
