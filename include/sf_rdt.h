@@ -1,0 +1,141 @@
+/*
+ * sf_rdt.h — RDT-1B denoise-loop runtime on MI355X (libsf_rdt.so) and the
+ * element-wise building blocks it uses (libsf_hip_kernels.so).
+ *
+ * The runtime is the native caller of the attention path: it owns the RDT-1B
+ * weights, the per-inference cross-attention K/V cache and the hipGraph of
+ * the fixed-shape Euler loop.  Reference interfaces it replaces (paths
+ * relative to the servoflow tree):
+ *   sf_rdt_set_condition     the condition half of RDT1BModel::encode_condition
+ *                            (src/models/rdt1b/rdt1b.cpp:167-239) plus the
+ *                            per-block K/V projection that
+ *                            CrossAttention::forward repeats on every call
+ *                            (src/models/rdt1b/dit_block.cu:288-308); here it
+ *                            runs once per inference and is cached.
+ *   sf_rdt_encode_condition  RDT1BModel::encode_condition: lang / img / state
+ *                            adaptors (rdt1b.cpp:35-85, 167-239), then
+ *                            sf_rdt_set_condition.
+ *   sf_rdt_denoise_step      RDT1BModel::denoise_step (rdt1b.cpp:254-369,
+ *                            IVLAModel::denoise_step,
+ *                            include/servoflow/engine/inference_engine.h:83-87),
+ *                            any batch size (the reference throws for B != 1,
+ *                            rdt1b.cpp:268-270).
+ *   sf_rdt_sample            FlowMatchingSampler::sample
+ *                            (src/sampling/flow_matching.cpp:25-93): Euler
+ *                            steps t_i = 1 - i/N, captured once into a
+ *                            hipGraph and replayed.
+ * All entry points return sf_status codes (sf_hip.h) and never throw.
+ */
+#ifndef SF_RDT_H_
+#define SF_RDT_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sf_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- element-wise building blocks (libsf_hip_kernels.so) ----------------- */
+
+/* p[i] = N(0,1)(seed, i) * std as bf16 or fp32: a counter-based generator,
+ * element i depends only on (seed, i).  Synthetic weight initialisation. */
+int sf_init_normal(void* p, int32_t dtype, int64_t n, uint64_t seed, float std, void* stream);
+int sf_fill_f32(float* p, int64_t n, float v, void* stream);
+/* Rows of N(0,std)(seed, row*K + c) quantised per row: scale = max|w|/127,
+ * q = clamp(rint(w/scale), -127, 127). */
+int sf_init_int8_rows(int8_t* q, float* scale, int64_t N, int64_t K, uint64_t seed, float std,
+                      void* stream);
+/* out[r] = bf16([x_t[r], 1...1]) for rows of A actions: the state adaptor's
+ * input cat(noisy_action, action_mask) (rdt1b.cpp:286-300). */
+int sf_build_action_input(const float* x_t, void* out, int64_t rows, int32_t A, void* stream);
+/* x[b] = [t_emb, f_emb, state[b], act[b, 0..T)] + pos (rdt1b.cpp:319-340);
+ * x fp32 [B, T+3, D], state bf16 [B, D], act fp32 [B, T, D], pos fp32 [T+3, D]. */
+int sf_assemble_tokens(float* x, const float* t_emb, const float* f_emb, const void* state,
+                       const float* act, const float* pos, int32_t B, int32_t T, int32_t D,
+                       void* stream);
+/* out[b, l] = bf16(tok[b, l] + pos[l]) for l < L (rdt1b.cpp:342-349). */
+int sf_add_pos_bf16(const void* tok, const float* pos, void* out, int32_t B, int32_t L, int32_t D,
+                    void* stream);
+/* x[b, t] += dt * v[b*S + 3 + t] (last T of S token rows; rdt1b.cpp:362,
+ * flow_matching.cpp:77-78). */
+int sf_euler_update(float* x, const float* v, int32_t B, int32_t T, int32_t A, int32_t S,
+                    float dt, void* stream);
+
+/* ---- model runtime (libsf_rdt.so) ---------------------------------------- */
+
+/* RDT1BConfig (include/servoflow/models/rdt1b/config.h:26-71) plus the batch
+ * and weight format.  The FFN has no expansion (config.h:60-61). */
+typedef struct sf_rdt_config {
+    int32_t hidden;              /* 2048 */
+    int32_t layers;              /* 28 */
+    int32_t heads;               /* 32 (head_dim 64) */
+    int32_t action_dim;          /* 128 */
+    int32_t horizon;             /* 64 action tokens; sequence = horizon + 3 */
+    int32_t freq_dim;            /* 256 */
+    int32_t state_dim;           /* 128 */
+    int32_t lang_max;            /* 1024 padded language tokens */
+    int32_t img_len;             /* 4374 image tokens */
+    int32_t lang_token_dim;      /* 4096 (T5-XXL) */
+    int32_t img_token_dim;       /* 1152 (SigLIP) */
+    int32_t num_train_timesteps; /* 1000 */
+    int32_t ctrl_freq;           /* 25 */
+    int32_t num_steps;           /* 5 Euler steps */
+    int32_t batch;
+    int32_t int8_weights;        /* block projections as int8 + fp32 row scale */
+    float eps;                   /* 1e-6 */
+} sf_rdt_config;
+
+typedef struct sf_rdt sf_rdt;
+
+void sf_rdt_config_default(sf_rdt_config* cfg);
+/* Allocates weights, caches and buffers on the current HIP device. */
+int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out);
+void sf_rdt_destroy(sf_rdt* m);
+
+/* Synthetic weights: matrices, biases and position embeddings ~ N(0, std),
+ * RMSNorm gammas = 1 (the PyTorch init, test_rdt1b_alignment.py:76). */
+int sf_rdt_init_random(sf_rdt* m, uint64_t seed, float std, void* stream);
+
+/* Parameter table, named as the reference checkpoint keys. */
+int32_t sf_rdt_num_params(const sf_rdt* m);
+int sf_rdt_param_info(const sf_rdt* m, int32_t idx, const char** name, int32_t* dtype,
+                      int32_t* ndim, int64_t shape[4]);
+void* sf_rdt_param_data(sf_rdt* m, int32_t idx);        /* device pointer */
+float* sf_rdt_param_scale(sf_rdt* m, int32_t idx);      /* int8 row scales or NULL */
+int32_t sf_rdt_find_param(const sf_rdt* m, const char* name);
+
+/* Condition for the next inferences.  lang_c bf16 [B, lang_max, D],
+ * lang_len int32 [B] (device; keys >= lang_len[b] are masked), img_c bf16
+ * [B, img_len, D], state_tok bf16 [B, D]: the adaptor outputs.  Adds the
+ * position embeddings and projects every block's cross-attention K/V once. */
+int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t* lang_len,
+                         const void* img_c, const void* state_tok, void* stream);
+/* Raw tokens: lang bf16 [B, lang_max, 4096], img bf16 [B, img_len, 1152],
+ * state bf16 [B, state_dim]; runs the adaptors then sf_rdt_set_condition. */
+int sf_rdt_encode_condition(sf_rdt* m, const void* lang_tokens, const int32_t* lang_len,
+                            const void* img_tokens, const void* state, void* stream);
+
+/* RDTBlock::forward (src/models/rdt1b/dit_block.cu:349-387) for blocks
+ * [first, first + count) on the residual stream x fp32 [B, horizon+3, D]
+ * (device, updated in place), with the cached condition. */
+int sf_rdt_run_blocks(sf_rdt* m, float* x, int32_t first, int32_t count, void* stream);
+
+/* velocity[B, T, A] = v(x_t, t) for fp32 device buffers. */
+int sf_rdt_denoise_step(sf_rdt* m, const float* x_t, float t, float* velocity, void* stream);
+
+/* x[B, T, A] (fp32, device) <- num_steps Euler steps from t = 1 to 0.
+ * use_graph != 0 captures the loop into a hipGraph on the first call and
+ * replays it afterwards (inputs are copied in and out around the graph). */
+int sf_rdt_sample(sf_rdt* m, float* x, int32_t use_graph, void* stream);
+
+/* Cross-attention K or V cache of block `layer` ([B, H, S, 64] bf16). */
+void* sf_rdt_cache_ptr(sf_rdt* m, int32_t layer, int32_t which_v);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* SF_RDT_H_ */

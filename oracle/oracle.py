@@ -49,6 +49,9 @@ def lib():
     L.sfo_dequant_int8.argtypes = [_i8p, _f32p, _f32p, i64, i64, i32]
     L.sfo_quantize_int8_rows.argtypes = [_f32p, i64, i64, _i8p, _f32p]
     L.sfo_linspace.argtypes = [i32, f32, f32, _f32p]
+    L.sfo_sincos_table.argtypes = [i32, i32, _f32p]
+    L.sfo_timestep_index.argtypes = [f32, i32]
+    L.sfo_timestep_index.restype = i32
     _lib = L
     return L
 
@@ -195,3 +198,15 @@ def linspace(num_steps, t_start=1.0, t_end=0.0):
     out = np.empty(num_steps + 1, np.float32)
     lib().sfo_linspace(num_steps, t_start, t_end, out)
     return out
+
+
+def sincos_table(max_steps=1000, freq_dim=256):
+    """TimestepEmbedding::build_sincos_table, src/models/rdt1b/dit_block.cu:58-72."""
+    out = np.empty((max_steps, freq_dim), np.float32)
+    lib().sfo_sincos_table(max_steps, freq_dim, out)
+    return out
+
+
+def timestep_index(t, num_train_timesteps=1000):
+    """round(t * (T - 1)) clamped, src/models/rdt1b/rdt1b.cpp:312-313."""
+    return int(lib().sfo_timestep_index(float(t), num_train_timesteps))

@@ -1,0 +1,166 @@
+"""CPU restatement of the RDT-1B block, denoise step and Euler loop.
+
+TEST INFRASTRUCTURE ONLY: the checker for the MI355X model runtime
+(servoflow_amd/host).  Orchestration is numpy; every contraction,
+normalisation and attention runs in the C oracle (oracle/sf_oracle.c).
+
+Parameters are a dict name -> float32 array, named as in the reference
+checkpoint (tests/alignment/test_rdt1b_alignment.py:213-257,
+docs/RDT1B_ARCHITECTURE.md key list).
+
+`rb` (round to bf16): when True, values are rounded to bf16 at exactly the
+points where the GPU pipeline stores bf16 (GEMM inputs, per-head q/k/v,
+attention outputs, the cross-attention K/V cache); the residual stream and
+GEMM outputs that feed it stay fp32.  With rb=False everything is fp32 (the
+pure restatement).  The reference's own bf16 build rounds at all of these
+points and also rounds the residual (norm.cuh:146).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import oracle as O
+
+
+@dataclass
+class RdtConfig:
+    hidden: int = 2048
+    layers: int = 28
+    heads: int = 32
+    action_dim: int = 128
+    horizon: int = 64
+    freq_dim: int = 256
+    state_dim: int = 128
+    lang_max: int = 1024
+    img_len: int = 4374
+    num_train_timesteps: int = 1000
+    ctrl_freq: int = 25
+    num_steps: int = 5
+    eps: float = 1e-6
+
+    @property
+    def seq(self):            # t, freq, state, actions (config.h:64)
+        return self.horizon + 3
+
+
+def _r(x, rb):
+    return O.bf16_round(x) if rb else np.ascontiguousarray(x, np.float32)
+
+
+def heads_of(x, H):
+    """[B,S,H*64] -> [B,H,S,64] (seq_to_head, split_ops.cuh:123-137)."""
+    return O.seq_to_head(x, H, 64)
+
+
+def cross_kv(p, i, cond, cfg, rb=True):
+    """K/V of block i's cross-attention over condition tokens cond [B,Sc,D]:
+    kv = c Wkv^T + b, split_kv, k_norm on K (dit_block.cu:288-308)."""
+    pre = f"blocks.{i}.cross_attn."
+    B, Sc, D = cond.shape
+    kv = O.linear(cond, p[pre + "kv.weight"], p[pre + "kv.bias"]).reshape(B, Sc, 2 * D)
+    K, V = O.split_kv(kv, cfg.heads, 64)
+    K = O.rms_norm(K, p[pre + "k_norm.weight"], cfg.eps)
+    return _r(K, rb), _r(V, rb)
+
+
+def rdt_block(p, i, x, ck, cv, cond_len, cfg, rb=True):
+    """RDTBlock::forward, src/models/rdt1b/dit_block.cu:349-387, with the
+    cross-attention K/V precomputed (cross_kv).  x [B,S,D] fp32, updated."""
+    B, S, D = x.shape
+    H = cfg.heads
+    pre = f"blocks.{i}."
+    # self-attention branch (dit_block.cu:198-238)
+    n1 = _r(O.rms_norm(x, p[pre + "norm1.weight"], cfg.eps), rb)
+    qkv = O.linear(n1, p[pre + "attn.qkv.weight"], p[pre + "attn.qkv.bias"])
+    Q, K, V = O.split_qkv(qkv.reshape(B, S, 3 * D), H, 64)
+    Q = _r(O.rms_norm(Q, p[pre + "attn.q_norm.weight"], cfg.eps), rb)
+    K = _r(O.rms_norm(K, p[pre + "attn.k_norm.weight"], cfg.eps), rb)
+    V = _r(V, rb)
+    a = _r(O.head_to_seq(O.attention_f32(Q, K, V)), rb)
+    x = x + O.linear(a, p[pre + "attn.proj.weight"], p[pre + "attn.proj.bias"])
+    # cross-attention branch (dit_block.cu:274-326), norm2 from fused_add_rms_norm
+    n2 = _r(O.rms_norm(x, p[pre + "norm2.weight"], cfg.eps), rb)
+    cq = O.linear(n2, p[pre + "cross_attn.q.weight"], p[pre + "cross_attn.q.bias"])
+    cq = _r(O.rms_norm(heads_of(cq.reshape(B, S, D), H), p[pre + "cross_attn.q_norm.weight"], cfg.eps), rb)
+    ca = _r(O.head_to_seq(O.attention_f32(cq, ck, cv, valid_len=cond_len)), rb)
+    x = x + O.linear(ca, p[pre + "cross_attn.proj.weight"], p[pre + "cross_attn.proj.bias"])
+    # FFN branch (Mlp::forward, dit_block.cu:143-163: fc1 + GELU, fc2)
+    n3 = _r(O.rms_norm(x, p[pre + "norm3.weight"], cfg.eps), rb)
+    h = _r(O.linear(n3, p[pre + "ffn.fc1.weight"], p[pre + "ffn.fc1.bias"], act=1), rb)
+    return x + O.linear(h, p[pre + "ffn.fc2.weight"], p[pre + "ffn.fc2.bias"])
+
+
+def timestep_embed(p, name, step, cfg, rb=True):
+    """TimestepEmbedding::forward, dit_block.cu:102-127: sincos row ->
+    Linear + SiLU -> Linear.  Returns [1, D] fp32."""
+    table = O.sincos_table(cfg.num_train_timesteps, cfg.freq_dim)
+    step = max(0, min(int(step), cfg.num_train_timesteps - 1))
+    e = _r(table[step:step + 1], rb)
+    hdn = _r(O.linear(e, p[name + ".mlp.0.weight"], p[name + ".mlp.0.bias"], act=2), rb)
+    return O.linear(hdn, p[name + ".mlp.2.weight"], p[name + ".mlp.2.bias"])
+
+
+def mlp_adaptor(p, name, x, depth, rb=True):
+    """MlpAdaptor::forward, rdt1b.cpp:56-85: (Linear + GELU) x (depth-1), Linear."""
+    h = _r(x, rb)
+    for j in range(depth - 1):
+        h = _r(O.linear(h, p[f"{name}.{2 * j}.weight"], p[f"{name}.{2 * j}.bias"], act=1), rb)
+    return O.linear(h, p[f"{name}.{2 * (depth - 1)}.weight"], p[f"{name}.{2 * (depth - 1)}.bias"])
+
+
+def condition_tokens(p, lang_c, img_c, cfg, rb=True):
+    """lang_c + lang_cond_pos_embed[:L], img_c + img_cond_pos_embed
+    (rdt1b.cpp:342-349), rounded where the GPU stores them."""
+    L = lang_c.shape[1]
+    lang = _r(lang_c + p["lang_cond_pos_embed"][:, :L], rb)
+    img = _r(img_c + p["img_cond_pos_embed"], rb)
+    return lang, img
+
+
+def encode_caches(p, lang_c, img_c, cfg, rb=True):
+    """Per-layer cross K/V caches (even layers: language, odd: image,
+    dit_block.cu:369)."""
+    lang, img = condition_tokens(p, lang_c, img_c, cfg, rb)
+    return [cross_kv(p, i, lang if i % 2 == 0 else img, cfg, rb) for i in range(cfg.layers)]
+
+
+def denoise_step(p, x_t, t, state_tok, caches, lang_len, cfg, rb=True):
+    """RDT1BModel::denoise_step, src/models/rdt1b/rdt1b.cpp:254-369 (batch
+    generalised): x_t [B,T,A] fp32, state_tok [B,D] (the condition's state
+    token), returns the velocity [B,T,A]."""
+    B, T, A = x_t.shape
+    D = cfg.hidden
+    ones = np.ones_like(x_t)
+    act_in = np.concatenate([x_t, ones], axis=-1)                      # :289-300
+    action_traj = mlp_adaptor(p, "state_adaptor", act_in, 3, rb)       # :302
+    t_int = O.timestep_index(t, cfg.num_train_timesteps)              # :312-313
+    t_emb = timestep_embed(p, "t_embedder", t_int, cfg, rb)
+    f_emb = timestep_embed(p, "freq_embedder", cfg.ctrl_freq, cfg, rb)
+    x = np.empty((B, T + 3, D), np.float32)
+    x[:, 0] = t_emb[0]
+    x[:, 1] = f_emb[0]
+    x[:, 2] = _r(state_tok, rb)
+    x[:, 3:] = action_traj
+    x = x + p["x_pos_embed"]                                            # :340
+    for i in range(cfg.layers):                                         # :353-355
+        ck, cv = caches[i]
+        x = rdt_block(p, i, x, ck, cv, lang_len if i % 2 == 0 else None, cfg, rb)
+    # FinalLayer::forward (dit_block.cu:407-412), last T tokens (rdt1b.cpp:362)
+    nf = _r(O.rms_norm(x, p["final_layer.norm_final.weight"], cfg.eps), rb)
+    hf = _r(O.linear(nf, p["final_layer.ffn_final.fc1.weight"], p["final_layer.ffn_final.fc1.bias"], act=1), rb)
+    out = O.linear(hf, p["final_layer.ffn_final.fc2.weight"], p["final_layer.ffn_final.fc2.bias"])
+    return out[:, 3:]
+
+
+def sample(p, x_init, state_tok, caches, lang_len, cfg, rb=True):
+    """FlowMatchingSampler::sample, src/sampling/flow_matching.cpp:25-93:
+    t_i = linspace(1 -> 0), x <- x + (t_{i+1} - t_i) v(x, t_i)."""
+    ts = O.linspace(cfg.num_steps, 1.0, 0.0)
+    x = np.array(x_init, np.float32, copy=True)
+    for s in range(cfg.num_steps):
+        v = denoise_step(p, x, float(ts[s]), state_tok, caches, lang_len, cfg, rb)
+        dt = np.float32(ts[s + 1] - ts[s])
+        x = x + dt * v                                                   # :77-78
+    return x

@@ -306,3 +306,26 @@ void sfo_linspace(int num_steps, float t_start, float t_end, float* out) {
         out[i] = t_start + alpha * (t_end - t_start);
     }
 }
+
+/* ---- timestep embedding, dit_block.cu:58-72 and rdt1b.cpp:312-313 --------- */
+
+void sfo_sincos_table(int max_steps, int freq_dim, float* table) {
+    const float max_period = 10000.f;
+    const int half = freq_dim / 2;
+    for (int step = 0; step < max_steps; ++step) {
+        const float t = (float)step;
+        for (int i = 0; i < half; ++i) {
+            const float freq = expf(-logf(max_period) * (float)i / (float)half);
+            const float angle = t * freq;
+            table[(int64_t)step * freq_dim + i] = cosf(angle);
+            table[(int64_t)step * freq_dim + half + i] = sinf(angle);
+        }
+    }
+}
+
+int sfo_timestep_index(float t, int num_train_timesteps) {
+    long v = lroundf(t * (float)(num_train_timesteps - 1));
+    if (v < 0) v = 0;
+    if (v > num_train_timesteps - 1) v = num_train_timesteps - 1;
+    return (int)v;
+}

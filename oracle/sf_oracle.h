@@ -88,6 +88,14 @@ void sfo_quantize_int8_rows(const float* W, int64_t N, int64_t K, int8_t* q, flo
 /* ---- schedule, Schedule::linspace, src/sampling/flow_matching.cpp:10-17 --- */
 void sfo_linspace(int num_steps, float t_start, float t_end, float* out);
 
+/* ---- timestep embedding table, TimestepEmbedding::build_sincos_table,
+ * src/models/rdt1b/dit_block.cu:58-72: table[step][i] = cos(step * f_i),
+ * table[step][half + i] = sin(step * f_i), f_i = exp(-log(10000) * i / half),
+ * all in float. ------------------------------------------------------------- */
+void sfo_sincos_table(int max_steps, int freq_dim, float* table);
+/* t in [0,1] -> integer timestep, rdt1b.cpp:312-313: round(t * (T - 1)) clamped. */
+int sfo_timestep_index(float t, int num_train_timesteps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,236 @@
+"""GPU parity of the RDT-1B runtime (libsf_rdt.so) against the CPU oracle
+(oracle/rdt.py, restating dit_block.cu:349-387, rdt1b.cpp:254-369 and
+flow_matching.cpp:25-93).
+
+Weights are initialised on the device, read back and handed to the oracle,
+so both sides use identical values; the oracle rounds to bf16 exactly where
+the GPU stores bf16.
+
+Tolerances:
+  * the cross K/V cache (one projection from bf16 inputs): max-abs <= 2e-2,
+    mean-rel <= 2e-3 and every element within one bf16 ulp;
+  * block-stack residual, velocity and sampled action: max-abs <= 2e-2, and
+    mean-rel within 4x the oracle's own noise floor, measured in the same
+    test as the distance between the oracle and the oracle with its
+    attention outputs scaled by (1 + 1e-6) before their bf16 rounding.
+    Downstream of bf16 storage a ppm-level difference flips roundings that
+    the following layers carry on (about 1.6e-3 mean-rel on the velocity
+    after one block with std-0.02 weights), so no independent implementation
+    with bf16 activations can agree more closely than that floor.
+Full hidden width (2048, 32 heads), reduced depth and condition lengths so
+the oracle finishes in seconds; the full 28-layer shape is covered by
+invariants (graph replay == eager, finite, moves the state)."""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_close_bf16, mean_rel
+from oracle import oracle as O
+from oracle import rdt as OR
+from servoflow_amd import rdt as R
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def small_cfg(**over):
+    base = dict(layers=2, lang_max=96, img_len=200, batch=2)
+    base.update(over)
+    return R.default_config(**base)
+
+
+def oracle_cfg(c):
+    return OR.RdtConfig(hidden=c.hidden, layers=c.layers, heads=c.heads, action_dim=c.action_dim,
+                        horizon=c.horizon, freq_dim=c.freq_dim, state_dim=c.state_dim,
+                        lang_max=c.lang_max, img_len=c.img_len,
+                        num_train_timesteps=c.num_train_timesteps, ctrl_freq=c.ctrl_freq,
+                        num_steps=c.num_steps, eps=c.eps)
+
+
+def bf(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV).to(torch.bfloat16)
+
+
+def make_condition(c, seed=5, lang_len=None):
+    B, D = c.batch, c.hidden
+    lang = O.bf16_round(O.randn(seed, (B, c.lang_max, D)))
+    img = O.bf16_round(O.randn(seed + 1, (B, c.img_len, D)))
+    state = O.bf16_round(O.randn(seed + 2, (B, D)))
+    if lang_len is None:
+        lang_len = np.linspace(c.lang_max // 3, c.lang_max, B).astype(np.int32)
+    return lang, np.asarray(lang_len, np.int32), img, state
+
+
+def build(c, seed=1234):
+    m = R.RdtModel(c)
+    m.init_random(seed, 0.02)
+    torch.cuda.synchronize()
+    return m
+
+
+def set_cond(m, lang, lang_len, img, state):
+    ll = torch.from_numpy(lang_len).to(DEV)
+    m.set_condition(bf(lang), ll, bf(img), bf(state))
+    return ll
+
+
+def oracle_noise_floor(fn):
+    """mean-rel between fn() and fn() with attention outputs scaled by 1+1e-6."""
+    base = fn()
+    orig = O.attention_f32
+    O.attention_f32 = lambda q, k, v, scale=0.0, causal=False, valid_len=None: (
+        orig(q, k, v, scale, causal, valid_len) * np.float32(1 + 1e-6))
+    try:
+        pert = fn()
+    finally:
+        O.attention_f32 = orig
+    return base, mean_rel(pert, base)
+
+
+def assert_within_floor(got, ref, floor, what):
+    mx = float(np.abs(got - ref).max())
+    mr = mean_rel(got, ref)
+    assert np.isfinite(got).all(), what
+    assert mx <= 2e-2 and mr <= 4 * floor, f"{what}: max-abs {mx:.3e} mean-rel {mr:.3e} floor {floor:.3e}"
+
+
+def test_block_stack_matches_oracle():
+    c = small_cfg(layers=3)
+    m = build(c)
+    lang, ll, img, state = make_condition(c)
+    set_cond(m, lang, ll, img, state)
+    S = c.horizon + 3
+    x = O.randn(77, (c.batch, S, c.hidden))
+    xd = torch.from_numpy(x).to(DEV)
+    m.run_blocks(xd)
+    got = xd.cpu().numpy()
+    p = m.state_dict()
+    oc = oracle_cfg(c)
+    caches = OR.encode_caches(p, lang, img, oc, rb=True)
+
+    def stack():
+        r = x
+        for i in range(c.layers):
+            r = OR.rdt_block(p, i, r, caches[i][0], caches[i][1], ll if i % 2 == 0 else None, oc, True)
+        return r
+
+    ref, floor = oracle_noise_floor(stack)
+    assert_within_floor(got, ref, floor, "3-block stack residual")
+
+
+def test_kv_cache_matches_oracle():
+    c = small_cfg()
+    m = build(c)
+    lang, ll, img, state = make_condition(c)
+    set_cond(m, lang, ll, img, state)
+    p = m.state_dict()
+    caches = OR.encode_caches(p, lang, img, oracle_cfg(c), rb=True)
+    for i in range(c.layers):
+        for wv in (0, 1):
+            got = m.cache_numpy(i, wv)
+            ref = caches[i][wv]
+            assert mean_rel(got, ref) < 2e-3, (i, wv)
+            assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-3), (i, wv)
+
+
+@pytest.mark.parametrize("int8", [0, 1])
+def test_denoise_step_matches_oracle(int8):
+    c = small_cfg(int8_weights=int8)
+    m = build(c)
+    lang, ll, img, state = make_condition(c)
+    set_cond(m, lang, ll, img, state)
+    x_t = O.randn(99, (c.batch, c.horizon, c.action_dim))
+    v = m.denoise_step(torch.from_numpy(x_t).to(DEV), 1.0)
+    got = v.cpu().numpy()
+    p = m.state_dict()
+    oc = oracle_cfg(c)
+    caches = OR.encode_caches(p, lang, img, oc, rb=True)
+    ref, floor = oracle_noise_floor(
+        lambda: OR.denoise_step(p, x_t, 1.0, state, caches, ll, oc, rb=True))
+    assert_within_floor(got, ref, floor, f"denoise step int8={int8}")
+    ref32 = OR.denoise_step(p, x_t, 1.0, state, OR.encode_caches(p, lang, img, oc, rb=False), ll, oc,
+                            rb=False)
+    assert mean_rel(got, ref32) < 2e-2
+
+
+def test_sample_graph_equals_eager_and_oracle():
+    c = small_cfg()
+    m = build(c)
+    lang, ll, img, state = make_condition(c)
+    set_cond(m, lang, ll, img, state)
+    x0 = O.randn(7, (c.batch, c.horizon, c.action_dim))
+    xe = torch.from_numpy(x0).to(DEV)
+    m.sample(xe, use_graph=False)
+    outs = []
+    for _ in range(3):       # capture, then two replays
+        xg = torch.from_numpy(x0).to(DEV)
+        m.sample(xg, use_graph=True)
+        torch.cuda.synchronize()
+        outs.append(xg.cpu().numpy())
+        _ = (xg * 2).sum().item()   # eager work between replays
+    eager = xe.cpu().numpy()
+    for o in outs:
+        assert np.array_equal(o, eager)
+    p = m.state_dict()
+    oc = oracle_cfg(c)
+    caches = OR.encode_caches(p, lang, img, oc, rb=True)
+    ref, floor = oracle_noise_floor(lambda: OR.sample(p, x0, state, caches, ll, oc, rb=True))
+    assert_within_floor(eager, ref, floor, "5-step Euler loop")
+    # the sampled action moved away from the noise by the loop matches closely
+    assert mean_rel(eager - x0, ref - x0) < 8 * max(floor, 1e-4)
+
+
+def test_batch_slots_are_independent():
+    c2 = small_cfg(batch=2)
+    c1 = small_cfg(batch=1)
+    m2, m1 = build(c2), build(c1)
+    lang, ll, img, state = make_condition(c2, lang_len=[50, 96])
+    set_cond(m2, lang, ll, img, state)
+    x_t = O.randn(11, (2, c2.horizon, c2.action_dim))
+    v2 = m2.denoise_step(torch.from_numpy(x_t).to(DEV), 0.6).cpu().numpy()
+    for b in range(2):
+        set_cond(m1, lang[b:b + 1], ll[b:b + 1], img[b:b + 1], state[b:b + 1])
+        v1 = m1.denoise_step(torch.from_numpy(x_t[b:b + 1]).to(DEV), 0.6).cpu().numpy()
+        assert np.abs(v1 - v2[b:b + 1]).max() < 1e-3, b
+
+
+def test_encode_condition_runs_adaptors():
+    c = small_cfg(batch=1)
+    m = build(c)
+    lt = O.bf16_round(O.randn(21, (1, c.lang_max, c.lang_token_dim)))
+    it = O.bf16_round(O.randn(22, (1, c.img_len, c.img_token_dim)))
+    st = O.bf16_round(O.randn(23, (1, c.state_dim)))
+    ll = torch.tensor([70], dtype=torch.int32, device=DEV)
+    m.encode_condition(bf(lt), ll, bf(it), bf(st))
+    p = m.state_dict()
+    oc = oracle_cfg(c)
+    lang_c = O.bf16_round(OR.mlp_adaptor(p, "lang_adaptor", lt, 2, True))
+    img_c = O.bf16_round(OR.mlp_adaptor(p, "img_adaptor", it, 2, True))
+    st_in = np.concatenate([st, np.zeros_like(st)], -1)
+    state_tok = O.bf16_round(OR.mlp_adaptor(p, "state_adaptor", st_in, 3, True))
+    caches = OR.encode_caches(p, lang_c, img_c, oc, rb=True)
+    got = m.cache_numpy(1, 0)
+    assert mean_rel(got, caches[1][0]) < 5e-3
+    x_t = O.randn(24, (1, c.horizon, c.action_dim))
+    v = m.denoise_step(torch.from_numpy(x_t).to(DEV), 0.2).cpu().numpy()
+    ref, floor = oracle_noise_floor(
+        lambda: OR.denoise_step(p, x_t, 0.2, state_tok, caches, np.array([70], np.int32), oc, rb=True))
+    assert_within_floor(v, ref, floor, "encode_condition + step")
+
+
+def test_full_rdt1b_shape_graph_loop():
+    c = R.default_config()           # 28 layers, lang 1024, img 4374, batch 1
+    m = build(c)
+    lang, ll, img, state = make_condition(c, lang_len=[517])
+    set_cond(m, lang, ll, img, state)
+    x0 = O.randn(8, (1, c.horizon, c.action_dim))
+    xe = torch.from_numpy(x0).to(DEV)
+    m.sample(xe, use_graph=False)
+    xg = torch.from_numpy(x0).to(DEV)
+    m.sample(xg, use_graph=True)
+    xg2 = torch.from_numpy(x0).to(DEV)
+    m.sample(xg2, use_graph=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(xe).all()
+    assert torch.equal(xe, xg) and torch.equal(xg, xg2)
+    assert float((xe - torch.from_numpy(x0).to(DEV)).abs().max()) > 0
