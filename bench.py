@@ -1,15 +1,27 @@
 #!/usr/bin/env python3
-"""Benchmark of the RDT-1B attention hot path on one MI355X.
+"""Benchmark of the RDT-1B denoise loop and its attention hot path on one MI355X.
 
-Prints ONE JSON line (the driver's contract).  Workload: BASELINE config 2,
-the image cross-attention op (67 queries x 4374 keys, 32 heads x 64, bf16,
-batch 1), whose HBM roofline is the metric's second half; config-2 variants
-(batch 8, language keys with valid lengths) and the 67x67 self-attention are
-reported as extra fields.  Inputs are synthetic N(0,1) bf16 already resident
-in HBM when timing starts; timing uses HIP events on the stream the kernels
-run on.  The CPU baseline is the oracle's fp32 restatement of the reference's
-naive_attention_kernel (attention.cu:90-139) on the host cores, on a bounded
-sample of the same workload.
+Prints ONE JSON line (the driver's contract).
+
+Headline (`value`, BASELINE config 4 at batch 1): latency of one full
+denoise loop -- 5 Euler steps of the 28-layer RDT-1B (hidden 2048, 32 heads,
+67 tokens, FFN 1x) with the condition K/V projected once per inference and
+cached -- replayed as one hipGraph.  One bench "step" is one such inference
+(graph replay, input copy-in and result copy-out included); inputs are
+synthetic and resident in HBM; weights are random-init (std 0.02, RMSNorm
+gamma = 1).  Timing uses HIP events on the stream the graph runs on.
+
+`roofline` is the metric's second half: the image cross-attention op the loop
+runs (67 queries x 4374 cached keys, 32 heads x 64, bf16, batch 1), algorithmic
+bytes (K and V once, Q in, O out) over its measured duration against the 8 TB/s
+HBM peak.  `extra` reports the other configs: cross-attention batch 8 and
+language keys with valid lengths (config 2), the block stack (config 3), the
+loop at batch 16 (config 4) and the int8-weight loop at batch 32 (config 5),
+and the one-time condition encode.
+
+`cpu_baseline` is the CPU oracle (oracle/, the fp32 restatement of the
+reference's RDTBlock / denoise_step / naive attention) timed on the host
+cores: one full 28-layer denoise step, scaled by 5 to a loop.
 """
 import argparse
 import json
@@ -29,14 +41,19 @@ def attn_bytes(B, H, Sq, Sk_valid_total, D=64, eb=2):
     return 2 * H * Sk_valid_total * D * eb + 2 * B * H * Sq * D * eb
 
 
-def attn_flops(B, H, Sq, Sk_valid_total, D=64):
+def attn_flops(H, Sq, Sk_valid_total, D=64):
     return 4 * H * Sq * Sk_valid_total * D
+
+
+def _events():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
 def time_graph(fn, steps, warmup, reps=20):
     """Captures `reps` back-to-back calls of fn in one HIP graph and times
-    `steps` replays with HIP events on the capturing stream; returns ms per
-    call.  Graph replay keeps host launch overhead out of the kernel time."""
+    `steps` replays with HIP events on the capturing stream; ms per call."""
     import torch
 
     fn()
@@ -53,8 +70,7 @@ def time_graph(fn, steps, warmup, reps=20):
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
+    start, stop = _events()
     start.record(stream)
     for _ in range(steps):
         g.replay()
@@ -75,7 +91,7 @@ def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32):
     q = torch.randn(B, H, Sq, 64, device=dev, generator=g).to(torch.bfloat16)
     k = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
     v = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
-    # Output straight into [B, Sq, H*D], the layout the block's projection reads.
+    # output straight into [B, Sq, H*D], the layout the block's projection reads
     out = torch.empty(B, Sq, H, 64, device=dev, dtype=torch.bfloat16).permute(0, 2, 1, 3)
     vl = None
     if valid is not None:
@@ -86,55 +102,162 @@ def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32):
     ms = time_graph(fn, steps, warmup)
     sk_total = B * Sk if valid is None else int(np.sum(valid))
     nbytes = attn_bytes(B, H, Sq, sk_total)
-    return {
-        "ms": ms,
-        "us": ms * 1e3,
-        "bytes": nbytes,
-        "GBps": nbytes / (ms * 1e-3) / 1e9,
-        "TFLOPs": attn_flops(B, H, Sq, sk_total) / (ms * 1e-3) / 1e12,
-        "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-    }
+    return {"us": ms * 1e3, "bytes": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9,
+            "TFLOPs": attn_flops(H, Sq, sk_total) / (ms * 1e-3) / 1e12,
+            "frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
-def cpu_baseline(budget_s=12.0):
-    """Oracle fp32 restatement of naive_attention_kernel on the host cores,
-    timed on the same image cross-attention shape (B=1)."""
+def make_model(B, int8=False, seed=1234):
+    """RDT-1B (28 layers) with random weights and a synthetic condition:
+    language N(0,1) with valid lengths ~ U{32..1024}, image N(0,1) 4374 tokens,
+    state token N(0,1).  Returns (model, encode_ms)."""
+    import numpy as np
+    import torch
+
+    from servoflow_amd import rdt as R
+
+    cfg = R.default_config(batch=B, int8_weights=1 if int8 else 0)
+    m = R.RdtModel(cfg)
+    m.init_random(seed, 0.02)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + B)
+    lang = torch.randn(B, cfg.lang_max, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
+    img = torch.randn(B, cfg.img_len, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
+    state = torch.randn(B, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
+    rng = np.random.default_rng(seed + B)
+    ll = torch.from_numpy(rng.integers(32, 1025, size=B).astype(np.int32)).to(dev)
+    m.set_condition(lang, ll, img, state)          # warm-up (first launch of each kernel)
+    torch.cuda.synchronize()
+    start, stop = _events()
+    start.record()
+    m.set_condition(lang, ll, img, state)
+    stop.record()
+    torch.cuda.synchronize()
+    del lang, img
+    return m, start.elapsed_time(stop)
+
+
+def bench_loop(m, steps, warmup):
+    """ms per graph-replayed 5-step denoise loop (copy-in/out included)."""
+    import torch
+
+    cfg = m.cfg
+    dev = torch.device("cuda:0")
+    x0 = torch.randn(cfg.batch, cfg.horizon, cfg.action_dim, device=dev)
+    x = x0.clone()
+    m.sample(x, use_graph=True)          # capture + first replay
+    for _ in range(warmup):
+        x.copy_(x0)
+        m.sample(x, use_graph=True)
+    torch.cuda.synchronize()
+    start, stop = _events()
+    start.record()
+    for _ in range(steps):
+        m.sample(x, use_graph=True)
+    stop.record()
+    torch.cuda.synchronize()
+    if not torch.isfinite(x).all():
+        raise RuntimeError("non-finite sampler output")
+    return start.elapsed_time(stop) / steps
+
+
+def bench_blocks(m, steps):
+    """Config 3: the 28-block stack, one denoise step's worth, eager launches."""
+    import torch
+
+    cfg = m.cfg
+    x = torch.randn(cfg.batch, cfg.horizon + 3, cfg.hidden, device="cuda:0")
+    m.run_blocks(x)
+    torch.cuda.synchronize()
+    start, stop = _events()
+    start.record()
+    for _ in range(steps):
+        m.run_blocks(x)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def cpu_baseline(budget_s=25.0):
+    """The oracle's fp32 RDT-1B denoise step (28 layers, batch 1, image keys
+    4374, language 1024 padded keys with a valid length) on the host cores.
+    Weights are N(0, 0.02); one layer's weights are shared by all 28 layers
+    (the timing does not depend on the values) and the condition caches are
+    random.  One step is timed and scaled by 5 to the loop."""
     import numpy as np
 
     from oracle import oracle as O
+    from oracle import rdt as OR
 
-    B, H, Sq, Sk = 1, 32, 67, 4374
-    q = O.randn(1, (B, H, Sq, 64))
-    k = O.randn(2, (B, H, Sk, 64))
-    v = O.randn(3, (B, H, Sk, 64))
-    O.attention_f32(q, k, v)  # warm-up
+    c = OR.RdtConfig()
+    D = c.hidden
+    seeds = iter(range(1, 1000))
+
+    def mat(N, K):
+        return O.bf16_round(O.randn(next(seeds), (N, K), 0.02))
+
+    def vec(N):
+        return O.randn(next(seeds), (N,), 0.02)
+
+    p = {}
+    shared = {
+        "attn.qkv.weight": mat(3 * D, D), "attn.qkv.bias": vec(3 * D),
+        "attn.proj.weight": mat(D, D), "attn.proj.bias": vec(D),
+        "cross_attn.q.weight": mat(D, D), "cross_attn.q.bias": vec(D),
+        "cross_attn.proj.weight": mat(D, D), "cross_attn.proj.bias": vec(D),
+        "ffn.fc1.weight": mat(D, D), "ffn.fc1.bias": vec(D),
+        "ffn.fc2.weight": mat(D, D), "ffn.fc2.bias": vec(D),
+    }
+    ones_d, ones_64 = np.ones(D, np.float32), np.ones(64, np.float32)
+    for i in range(c.layers):
+        pre = f"blocks.{i}."
+        for k, v in shared.items():
+            p[pre + k] = v
+        for nm in ("norm1", "norm2", "norm3"):
+            p[pre + nm + ".weight"] = ones_d
+        for nm in ("attn.q_norm", "attn.k_norm", "cross_attn.q_norm", "cross_attn.k_norm"):
+            p[pre + nm + ".weight"] = ones_64
+    for a, k in (("state_adaptor.0", 2 * c.state_dim), ("state_adaptor.2", D), ("state_adaptor.4", D),
+                 ("t_embedder.mlp.0", c.freq_dim), ("t_embedder.mlp.2", D),
+                 ("freq_embedder.mlp.0", c.freq_dim), ("freq_embedder.mlp.2", D),
+                 ("final_layer.ffn_final.fc1", D)):
+        p[a + ".weight"], p[a + ".bias"] = mat(D, k), vec(D)
+    p["final_layer.ffn_final.fc2.weight"] = mat(c.action_dim, D)
+    p["final_layer.ffn_final.fc2.bias"] = vec(c.action_dim)
+    p["final_layer.norm_final.weight"] = ones_d
+    p["x_pos_embed"] = O.randn(900, (1, c.seq, D), 0.02)
+    lang_k = O.bf16_round(O.randn(901, (1, c.heads, c.lang_max, 64)))
+    img_k = O.bf16_round(O.randn(902, (1, c.heads, c.img_len, 64)))
+    caches = [(lang_k, lang_k) if i % 2 == 0 else (img_k, img_k) for i in range(c.layers)]
+    state = O.randn(903, (1, D))
+    x_t = O.randn(904, (1, c.horizon, c.action_dim))
+    ll = np.array([517], np.int32)
     times = []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
+    while not times or (time.perf_counter() < t_end and len(times) < 3):
         t0 = time.perf_counter()
-        O.attention_f32(q, k, v)
+        OR.denoise_step(p, x_t, 1.0, state, caches, ll, c, rb=False)
         times.append(time.perf_counter() - t0)
-        if len(times) >= 200:
-            break
-    med = float(np.median(times))
-    nbytes = attn_bytes(B, H, Sq, B * Sk)
+    step_s = float(np.median(times))
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {
-        "value": nbytes / med / 1e9,
-        "unit": "GB/s",
-        "ms_per_op": med * 1e3,
+        "value": round(step_s * c.num_steps * 1e3, 1),
+        "unit": "ms",
         "cores": cores,
         "kind": "port",
-        "sample": f"{len(times)} runs of the full B=1 image cross-attention (1x32x67x4374x64, fp32), median",
+        "sample": f"{len(times)} timed fp32 oracle denoise step(s) (28 layers, batch 1, lang 1024 "
+                  f"keys with valid length 517, image 4374 keys), median {step_s * 1e3:.0f} ms, x5 steps",
     }
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50, help="timed denoise-loop inferences")
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--quick", action="store_true", help="headline and roofline only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -145,50 +268,73 @@ def main():
     import torch
 
     torch.cuda.init()
-    rng = np.random.default_rng(7)
-    img1 = bench_attention(1, 4374, args.steps, args.warmup)
-    img8 = bench_attention(8, 4374, args.steps, args.warmup)
-    lang_valid8 = rng.integers(32, 1025, size=8)
-    lang8 = bench_attention(8, 1024, args.steps, args.warmup, valid=lang_valid8)
-    lang1 = bench_attention(1, 1024, args.steps, args.warmup, valid=[1024])
-    self1 = bench_attention(1, 67, args.steps, args.warmup)
-
+    extra = {}
+    # ---- headline: batch-1 loop (config 4)
+    m1, enc1 = make_model(1)
+    loop1 = bench_loop(m1, args.steps, args.warmup)
+    extra["encode_condition_b1_ms"] = round(enc1, 3)
+    if not args.quick:
+        extra["block_stack_b1_ms"] = round(bench_blocks(m1, 5), 3)
+    m1.close()
+    del m1
+    torch.cuda.empty_cache()
+    # ---- roofline: the loop's image cross-attention op (config 2, batch 1)
+    att_steps = max(10, args.steps // 2)
+    img1 = bench_attention(1, 4374, att_steps, args.warmup)
+    extra["cross_img_b1_us"] = round(img1["us"], 3)
+    if not args.quick:
+        img8 = bench_attention(8, 4374, att_steps, args.warmup)
+        rng = np.random.default_rng(7)
+        lv8 = rng.integers(32, 1025, size=8)
+        lang8 = bench_attention(8, 1024, att_steps, args.warmup, valid=lv8)
+        lang1 = bench_attention(1, 1024, att_steps, args.warmup, valid=[517])
+        self1 = bench_attention(1, 67, att_steps, args.warmup)
+        extra.update({
+            "cross_img_b8_us": round(img8["us"], 3),
+            "cross_img_b8_GBps": round(img8["GBps"], 1),
+            "cross_img_b8_frac": round(img8["frac"], 4),
+            "cross_lang_b8_us": round(lang8["us"], 3),
+            "cross_lang_b8_GBps": round(lang8["GBps"], 1),
+            "cross_lang_b1_L517_us": round(lang1["us"], 3),
+            "self_b1_us": round(self1["us"], 3),
+        })
+        for B, int8, key in ((16, False, "loop_b16_ms"), (32, True, "loop_int8_b32_ms")):
+            m, enc = make_model(B, int8=int8)
+            extra[key] = round(bench_loop(m, max(3, args.steps // 10), 2), 3)
+            extra[key.replace("loop", "encode")] = round(enc, 3)
+            m.close()
+            del m
+            torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC,
-        "value": round(img1["GBps"], 2),
-        "unit": "GB/s",
+        "value": round(loop1, 4),
+        "unit": "ms",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(img1["ms"], 6),
-        "higher_is_better": True,
+        "ms_per_step": round(loop1, 4),
+        "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "config 2: image cross-attention op, B=1, 32 heads x 64, "
-                               "67 queries x 4374 keys, bf16 in/out, [B,Sq,H*D] output"},
+        "config": {"workload": "config 4: RDT-1B denoise loop, 5 Euler steps, batch 1, 28 layers, "
+                               "hidden 2048, 32 heads, 67 tokens, lang 1024 keys (valid length "
+                               "U{32..1024}) / image 4374 keys cached once, one hipGraph replay "
+                               "per step, random-init weights"},
         "roofline": {
             "bound": "hbm",
-            "achieved": round(img1["GBps"], 2),
+            "achieved": round(img1["GBps"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(img1["frac_hbm"], 4),
+            "frac": round(img1["frac"], 4),
             "traffic": None,
+            "kernel": "cross-attention op (attn_split_kernel + attn_merge_kernel), 1x32x67x4374x64 "
+                      f"bf16, {img1['bytes']} algorithmic bytes per launch, {img1['us']:.2f} us",
         },
         "cpu_baseline": cpu,
-        "extra": {
-            "cross_img_b1_us": round(img1["us"], 3),
-            "cross_img_b8_us": round(img8["us"], 3),
-            "cross_img_b8_GBps": round(img8["GBps"], 1),
-            "cross_img_b8_frac": round(img8["frac_hbm"], 4),
-            "cross_lang_b8_us": round(lang8["us"], 3),
-            "cross_lang_b8_GBps": round(lang8["GBps"], 1),
-            "cross_lang_b1_full_us": round(lang1["us"], 3),
-            "self_b1_us": round(self1["us"], 3),
-            "self_b1_TFLOPs": round(self1["TFLOPs"], 3),
-        },
+        "extra": extra,
     }
     print(json.dumps(line))
 
