@@ -124,13 +124,27 @@ int sf_attn_fwd(const sf_attn_desc* desc, const void* q, const void* k,
  *        strides head_stride[j] = {b, h, s}) with row m = b*S + s, after an
  *        RMSNorm over the 64 head dims with head_gamma[j] when that pointer
  *        is non-NULL (q_norm / k_norm, dit_block.cu:219-220, 307-308);
+ *   epilogue SF_EPI_ADD_NORM: C (fp32 residual) += result, then
+ *        norm_out[m] = C[m] * rsqrt(mean(C[m]^2) + eps) * norm_gamma in
+ *        norm_dtype (row stride norm_ldo): the branch add followed by the
+ *        next RMSNorm, fused_add_rms_norm (norm.cuh:130-171,
+ *        backend.h:127-134) as RDTBlock chains them (dit_block.cu:372-384);
+ *        N <= 4096;
  *   w_dtype SF_I8: int8 weights with one fp32 scale per row (w_scale[N]),
  *        the weight-only dequant of quantization.cu:18-51 done in registers.
  * A and W rows must be 16-byte aligned (lda, ldw multiples of 8 elements),
- * K a multiple of 32; bias, w_scale, head_gamma are fp32.
+ * K a multiple of 32; bias, w_scale, head_gamma, norm_gamma are fp32;
+ * head_out must be 8-byte aligned with strides that are multiples of 4.
+ *
+ * workspace: fp32 scratch of sf_gemm_workspace_bytes() for the split-K
+ * path (M <= 160, N a multiple of 16), which spreads one weight matrix over
+ * all CUs.  With workspace == NULL (or a shape outside that range) a
+ * single-pass kernel runs instead and nothing beyond A, W and the outputs is
+ * touched.  A non-NULL workspace that is too small is SF_EWORKSPACE.  Calls
+ * that may run concurrently need separate workspaces.
  * ------------------------------------------------------------------------- */
 typedef enum sf_act { SF_ACT_NONE = 0, SF_ACT_GELU_TANH = 1, SF_ACT_SILU = 2 } sf_act;
-typedef enum sf_epilogue { SF_EPI_PLAIN = 0, SF_EPI_HEADS = 1 } sf_epilogue;
+typedef enum sf_epilogue { SF_EPI_PLAIN = 0, SF_EPI_HEADS = 1, SF_EPI_ADD_NORM = 2 } sf_epilogue;
 
 typedef struct sf_gemm_desc {
     int32_t M, N, K;
@@ -153,7 +167,17 @@ typedef struct sf_gemm_desc {
     const float* head_gamma[3];
     void* head_out[3];
     int64_t head_stride[3][3];
+    const float* norm_gamma; /* SF_EPI_ADD_NORM */
+    void* norm_out;
+    int64_t norm_ldo;
+    int32_t norm_dtype;
+    void* workspace;         /* split-K partial sums, or NULL */
+    int64_t workspace_bytes;
 } sf_gemm_desc;
+
+/* Bytes of workspace the split-K path needs for this shape (0: the shape
+ * always runs single-pass). */
+size_t sf_gemm_workspace_bytes(const sf_gemm_desc* desc);
 
 int sf_gemm(const sf_gemm_desc* desc, void* stream);
 

@@ -53,6 +53,7 @@ SF_ACT_GELU_TANH = 1
 SF_ACT_SILU = 2
 SF_EPI_PLAIN = 0
 SF_EPI_HEADS = 1
+SF_EPI_ADD_NORM = 2
 
 
 class GemmDesc(ctypes.Structure):
@@ -72,6 +73,9 @@ class GemmDesc(ctypes.Structure):
         ("head_gamma", ctypes.c_void_p * 3),
         ("head_out", ctypes.c_void_p * 3),
         ("head_stride", (ctypes.c_int64 * 3) * 3),
+        ("norm_gamma", ctypes.c_void_p), ("norm_out", ctypes.c_void_p),
+        ("norm_ldo", ctypes.c_int64), ("norm_dtype", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -106,6 +110,8 @@ def lib() -> ctypes.CDLL:
     L.sf_attn_fwd.restype = ctypes.c_int
     L.sf_gemm.argtypes = [ctypes.POINTER(GemmDesc), ctypes.c_void_p]
     L.sf_gemm.restype = ctypes.c_int
+    L.sf_gemm_workspace_bytes.argtypes = [ctypes.POINTER(GemmDesc)]
+    L.sf_gemm_workspace_bytes.restype = ctypes.c_size_t
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     L.sf_rmsnorm.argtypes = [vp, i32, i64, vp, vp, i32, i64, i32, i32, ctypes.c_float, vp]
     L.sf_rmsnorm.restype = ctypes.c_int

@@ -5,7 +5,9 @@
 // RDT layers call it: C[M,N] = act(A[M,K] . W[N,K]^T + bias[N])
 // (trans_b = true, dit_block.cu:207, 233, 284, 291, 321, 152-160), plus the
 // neighbouring ops folded into the epilogue:
-//   * residual add (the x += branch adds of dit_block.cu:372, 379, 384),
+//   * residual add (the x += branch adds of dit_block.cu:372, 379, 384) and
+//     the RMSNorm that follows it (fused_add_rms_norm_kernel,
+//     src/backend/cuda/ops/norm.cuh:130-171, as norm2 / norm3 / next norm1),
 //   * split into per-head [B,H,S,D] tensors with the per-head RMSNorm of
 //     q_norm / k_norm (split_qkv, split_kv, seq_to_head of
 //     src/backend/cuda/ops/split_ops.cuh:62-84, 123-137, 210-226 followed by
@@ -16,14 +18,21 @@
 //     product in the epilogue (sum_k (q_nk s_n) a_mk = s_n sum_k q_nk a_mk).
 //
 // Shape regime: at batch 1 the RDT projections have M = 67 rows, so every
-// GEMM is weight streaming (arithmetic intensity = M flop/byte).  The kernel
-// computes C^T = W . A^T so weight rows are MFMA rows: each lane loads 16
+// GEMM is weight streaming (arithmetic intensity = M flop/byte).  Both paths
+// compute C^T = W . A^T so weight rows are MFMA rows: each lane loads 16
 // contiguous bytes of a weight row straight from HBM into the operand
-// registers (no LDS staging, every weight byte is read once), and the few
-// activation rows are the MFMA columns, read from L2.  A workgroup of 8
-// waves covers NR weight rows over all of K: the waves split K and reduce
-// in LDS, so no split-K partials touch HBM.  M > 80 is handled as a grid of
-// 80-row tiles.
+// registers (no LDS staging, every weight byte is read once) and the few
+// activation rows are the MFMA columns.
+//
+//   split-K path (M <= 160, caller workspace): a 2048 x 2048 weight is only
+//   32 KB per CU, so the matrix is cut into 64-row x KT-wide tiles, one per
+//   workgroup, enough to cover all 256 CUs.  Each workgroup issues all of its
+//   weight loads at once, stages its activation slice in LDS once for its
+//   waves, and writes fp32 partial sums; a reduce kernel sums the K slices in
+//   a fixed order (deterministic) and applies the epilogue, including the
+//   residual add + RMSNorm that follows a block branch.
+//   single-pass path (no workspace, or M > 160): one workgroup of 8 waves per
+//   16 or 64 weight rows over all of K, reduced in LDS, epilogue in place.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -32,6 +41,12 @@
 
 #include "sf_device.h"
 #include "sf_hip.h"
+
+#define SF_CHECK_OK(expr)                  \
+    do {                                   \
+        const int _st = (expr);            \
+        if (_st != SF_OK) return _st;      \
+    } while (0)
 
 namespace sfk {
 
@@ -219,6 +234,337 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_smallm_kernel(const GemmArg
     }
 }
 
+// ---------------------------------------------------------------------------
+// split-K path
+// ---------------------------------------------------------------------------
+constexpr int kSkMaxSplits = 16;
+
+struct SkArgs {
+    const uint16_t* a;     // [M][lda] bf16
+    const void* w;         // [N][ldw] bf16 or int8
+    float* part;           // [splits][M][N] fp32
+    int64_t lda, ldw;
+    int M, N, K;
+};
+
+// LDS barrier that leaves outstanding global loads in flight (a plain
+// __syncthreads also waits for every vector-memory load of the wave).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Workgroup (blockIdx.x, blockIdx.y, blockIdx.z) = (16*NW-row weight tile,
+// KT-wide K slice, 16*MB-row activation tile); NW waves share the LDS copy
+// of the activation slice.  Lane (g4 = lane/16, r = lane%16) of wave w
+// supplies weight row 16w + r and activation row 16mb + r, k = 32t + 8g4
+// .. +7 of MFMA step t; its accumulator holds C^T[16w + 4g4 + i][16mb + r].
+template <int MB, int KT, int NW, bool W8>
+__global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
+    constexpr int kSkThreads = 64 * NW;
+    constexpr int kSkRows = 16 * NW;
+    constexpr int MR = 16 * MB;
+    constexpr int PITCH = 2 * KT + 16;       // bytes per LDS activation row (+16: bank shift)
+    constexpr int CH = KT / 8;               // 16-byte chunks per activation row
+    constexpr int NCH = MR * CH;
+    constexpr int PER = (NCH + kSkThreads - 1) / kSkThreads;
+    constexpr int STEPS = KT / 32;
+    __shared__ __attribute__((aligned(16))) char lds[MR * PITCH];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int g4 = lane >> 4;
+    const int r = lane & 15;
+    const int nw = blockIdx.x * kSkRows;
+    const int k0 = blockIdx.y * KT;
+    const int m0 = blockIdx.z * MR;
+    const int nsteps = min(KT, g.K - k0) / 32;
+
+    // activation slice first (needed first); rows past M read as zeros
+    const int mrows = min(MR, g.M - m0);
+    const __amdgpu_buffer_rsrc_t ars =
+        make_rsrc(g.a + (int64_t)m0 * g.lda, (uint32_t)((int64_t)mrows * g.lda * 2));
+    u32x4 av[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int c = tid + kSkThreads * i;
+        const int row = c / CH;
+        const int k = k0 + 8 * (c % CH);
+        const uint32_t off = (c < NCH && k < g.K) ? (uint32_t)((row * g.lda + k) * 2) : 0x80000000u;
+        av[i] = buffer_load16(ars, off);
+    }
+    // every weight fragment of this wave in flight at once; rows past N read 0
+    constexpr int WB = W8 ? 1 : 2;
+    const int wrows = min(kSkRows, g.N - nw);
+    const __amdgpu_buffer_rsrc_t wrs =
+        make_rsrc(static_cast<const char*>(g.w) + (int64_t)nw * g.ldw * WB,
+                  (uint32_t)((int64_t)wrows * g.ldw * WB));
+    const uint32_t wrow_off = (uint32_t)((16 * w + r) * g.ldw * WB);
+    u32x4 wv[W8 ? 1 : STEPS];
+    uint2 wq[W8 ? STEPS : 1];
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t) {
+        const int k = k0 + 32 * t + 8 * g4;
+        const uint32_t off = t < nsteps ? wrow_off + (uint32_t)(k * WB) : 0x80000000u;
+        if constexpr (W8)
+            wq[t] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wrs, off, 0, 0));
+        else
+            wv[t] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int c = tid + kSkThreads * i;
+        if (c < NCH)
+            *reinterpret_cast<u32x4*>(lds + (c / CH) * PITCH + (c % CH) * 16) = av[i];
+    }
+    lds_barrier();
+
+    f32x4 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t) {
+        if (t < nsteps) {
+            bf16x8 wf;
+            if constexpr (W8) wf = i8x8_to_bf16x8(wq[t]);
+            else wf = __builtin_bit_cast(bf16x8, wv[t]);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const bf16x8 af = *reinterpret_cast<const bf16x8*>(
+                    lds + (16 * mb + r) * PITCH + (32 * t + 8 * g4) * 2);
+                acc[mb] = mfma16x16x32(wf, af, acc[mb]);
+            }
+        }
+    }
+
+    float* P = g.part + (int64_t)blockIdx.y * g.M * g.N;
+    const int n = nw + 16 * w + 4 * g4;
+    if (n < g.N) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const int m = m0 + 16 * mb + r;
+            if (m < g.M) *reinterpret_cast<f32x4*>(P + (int64_t)m * g.N + n) = acc[mb];
+        }
+    }
+}
+
+struct EpiArgs {
+    const float* part;     // [splits][M][N]
+    int splits;
+    int M, N;
+    const float* w_scale;  // [N] or null
+    const float* bias;     // [N] or null
+    int act;
+    // plain
+    void* c;
+    int64_t ldc;
+    int c_f32, accumulate;
+    // per-head
+    int H, S;
+    float eps;
+    const float* head_gamma[3];
+    uint16_t* head_out[3];
+    int64_t head_sb[3], head_sh[3], head_ss[3];
+    // residual add + RMSNorm
+    const float* norm_gamma;
+    void* norm_out;
+    int64_t norm_ldo;
+    int norm_f32;
+};
+
+// Sum of the K-slice partials for C[m][n..n+3], slices in ascending order,
+// then scale, bias and activation.  All NS loads are issued before the
+// first add (indices past `splits` re-read the last slice and are masked),
+// so the sum costs one memory round trip.
+template <int NS>
+__device__ __forceinline__ f32x4 finish4(const EpiArgs& e, int m, int n) {
+    const float* p = e.part + (int64_t)m * e.N + n;
+    const int64_t stride = (int64_t)e.M * e.N;
+    f32x4 part[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+        part[s] = *reinterpret_cast<const f32x4*>(p + min(s, e.splits - 1) * stride);
+    f32x4 v = part[0];
+#pragma unroll
+    for (int s = 1; s < NS; ++s)
+        if (s < e.splits) v += part[s];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float x = v[j];
+        if (e.w_scale) x *= e.w_scale[n + j];
+        if (e.bias) x += e.bias[n + j];
+        v[j] = apply_act(e.act, x);
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint2 pack_bf16x4(f32x4 v) {
+    return uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+}
+
+template <int NS>
+__global__ __launch_bounds__(256) void reduce_plain_kernel(const EpiArgs e) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int n4 = e.N / 4;
+    if (idx >= (int64_t)e.M * n4) return;
+    const int m = (int)(idx / n4);
+    const int n = 4 * (int)(idx % n4);
+    f32x4 v = finish4<NS>(e, m, n);
+    const int64_t off = (int64_t)m * e.ldc + n;
+    if (e.c_f32) {
+        f32x4* cp = reinterpret_cast<f32x4*>(static_cast<float*>(e.c) + off);
+        if (e.accumulate) v += *cp;
+        *cp = v;
+    } else {
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.c) + off) = pack_bf16x4(v);
+    }
+}
+
+// 16 consecutive lanes hold the 64 columns of one head of one row.
+template <int NS>
+__global__ __launch_bounds__(256) void reduce_heads_kernel(const EpiArgs e) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int n4 = e.N / 4;
+    if (idx >= (int64_t)e.M * n4) return;   // whole 16-lane groups (N % 64 == 0)
+    const int m = (int)(idx / n4);
+    const int n = 4 * (int)(idx % n4);
+    f32x4 v = finish4<NS>(e, m, n);
+    const int cols = e.H * 64;
+    const int sec = n / cols;
+    const int h = (n % cols) / 64;
+    const int d = n % 64;
+    const float* gamma = e.head_gamma[sec];
+    if (gamma) {
+        // rms_norm_kernel_impl over the 64 head dims (norm.cuh:89-122)
+        float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 64);
+        const float inv_rms = 1.f / sqrtf(ss / 64.f + e.eps);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = v[j] * inv_rms * gamma[d + j];
+    }
+    const int b = m / e.S;
+    const int s = m % e.S;
+    uint16_t* o = e.head_out[sec] + b * e.head_sb[sec] + h * e.head_sh[sec] + s * e.head_ss[sec] + d;
+    *reinterpret_cast<uint2*>(o) = pack_bf16x4(v);
+}
+
+// One workgroup per row: x[m] += result[m]; out[m] = rmsnorm(x[m]) * gamma.
+constexpr int kAddNormMaxChunks = 4;   // N <= 4 * 256 * 4 = 4096
+template <int NS>
+__global__ __launch_bounds__(256) void reduce_addnorm_kernel(const EpiArgs e) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const int n4 = e.N / 4;
+    float* x = static_cast<float*>(e.c) + (int64_t)m * e.ldc;
+    f32x4 xv[kAddNormMaxChunks];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kAddNormMaxChunks; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        xv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (c < n4) {
+            f32x4 v = finish4<NS>(e, m, 4 * c);
+            f32x4* xp = reinterpret_cast<f32x4*>(x + 4 * c);
+            v += *xp;
+            *xp = v;
+            xv[i] = v;
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    const float inv_rms = 1.f / sqrtf(total / (float)e.N + e.eps);
+#pragma unroll
+    for (int i = 0; i < kAddNormMaxChunks; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        if (c < n4) {
+            f32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = xv[i][j] * inv_rms * e.norm_gamma[4 * c + j];
+            const int64_t off = (int64_t)m * e.norm_ldo + 4 * c;
+            if (e.norm_f32)
+                *reinterpret_cast<f32x4*>(static_cast<float*>(e.norm_out) + off) = o;
+            else
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.norm_out) + off) = pack_bf16x4(o);
+        }
+    }
+}
+
+struct SkPlan {
+    bool split = false;
+    int mb = 0, kt = 0, nw = 0, splits = 0, mtiles = 0, ntiles = 0;
+    size_t ws_bytes = 0;
+};
+
+// Tile choice: one 64-row weight tile per workgroup and K slices of 256, so
+// a 2048 x 2048 weight becomes 256 workgroups of 32 KB each and the
+// 6144-row QKV weight 768 (three per CU: LDS <= 42 KB each, so the whole
+// grid is resident at once).  Slices of 512 only when 256 would need more
+// than 16 slices or more workgroups than fit on the chip at once.
+constexpr int kSkResident = 256 * 3;
+inline SkPlan plan_splitk(int M, int N, int K) {
+    SkPlan p;
+    if (M <= 0 || M > 160 || N <= 0 || (N & 15) || K <= 0 || (K & 31)) return p;
+    p.mb = M <= 80 ? (M + 15) / 16 : 5;
+    p.mtiles = (M + 16 * p.mb - 1) / (16 * p.mb);
+    p.nw = 4;
+    p.ntiles = (N + 16 * p.nw - 1) / (16 * p.nw);
+    p.kt = 256;
+    p.splits = (K + 255) / 256;
+    if ((int64_t)p.ntiles * p.mtiles * p.splits > kSkResident || p.splits > kSkMaxSplits) {
+        p.kt = 512;
+        p.splits = (K + 511) / 512;
+    }
+    if (p.splits > kSkMaxSplits) return SkPlan{};
+    p.split = true;
+    p.ws_bytes = (size_t)p.splits * M * N * 4;
+    return p;
+}
+
+template <int KT, int NW, bool W8>
+void launch_splitk_mb(const SkArgs& a, const SkPlan& p, hipStream_t s) {
+    const dim3 grid(p.ntiles, p.splits, p.mtiles), block(64 * NW);
+    switch (p.mb) {
+        case 1: hipLaunchKernelGGL((gemm_splitk_kernel<1, KT, NW, W8>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((gemm_splitk_kernel<2, KT, NW, W8>), grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL((gemm_splitk_kernel<3, KT, NW, W8>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((gemm_splitk_kernel<4, KT, NW, W8>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((gemm_splitk_kernel<5, KT, NW, W8>), grid, block, 0, s, a); break;
+    }
+}
+
+template <bool W8>
+void launch_splitk_w(const SkArgs& a, const SkPlan& p, hipStream_t s) {
+    if (p.kt == 256) {
+        if (p.nw == 8) launch_splitk_mb<256, 8, W8>(a, p, s);
+        else launch_splitk_mb<256, 4, W8>(a, p, s);
+    } else {
+        if (p.nw == 8) launch_splitk_mb<512, 8, W8>(a, p, s);
+        else launch_splitk_mb<512, 4, W8>(a, p, s);
+    }
+}
+
+inline void launch_splitk(const SkArgs& a, const SkPlan& p, bool w8, hipStream_t s) {
+    if (w8) launch_splitk_w<true>(a, p, s);
+    else launch_splitk_w<false>(a, p, s);
+}
+
+template <int NS>
+void launch_reduce(const sf_gemm_desc* d, const EpiArgs& e, hipStream_t s) {
+    const int64_t quads = (int64_t)d->M * d->N / 4;
+    const unsigned blocks = (unsigned)((quads + 255) / 256);
+    if (d->epilogue == SF_EPI_HEADS)
+        hipLaunchKernelGGL(reduce_heads_kernel<NS>, dim3(blocks), dim3(256), 0, s, e);
+    else if (d->epilogue == SF_EPI_ADD_NORM)
+        hipLaunchKernelGGL(reduce_addnorm_kernel<NS>, dim3(d->M), dim3(256), 0, s, e);
+    else
+        hipLaunchKernelGGL(reduce_plain_kernel<NS>, dim3(blocks), dim3(256), 0, s, e);
+}
+
 template <int NR, bool W8>
 hipError_t launch_smallm(const GemmArgs& g, int mb, dim3 grid, hipStream_t s) {
     switch (mb) {
@@ -238,21 +584,76 @@ hipError_t launch_smallm(const GemmArgs& g, int mb, dim3 grid, hipStream_t s) {
 // ---------------------------------------------------------------------------
 namespace {
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-}  // namespace
+bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
-extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
-    if (!d) return SF_EINVAL;
-    if (d->M < 0 || d->N < 0 || d->K < 0) return SF_EINVAL;
-    if ((long)d->M * d->N == 0) return SF_OK;
+// Shape / pointer checks shared by both paths; fills the epilogue fields.
+int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
     if (d->K == 0 || (d->K & 31)) return SF_ENOTSUP;
     if (d->a_dtype != SF_BF16) return SF_ENOTSUP;
     if (d->w_dtype != SF_BF16 && d->w_dtype != SF_I8) return SF_ENOTSUP;
     if (d->act < 0 || d->act > 2) return SF_EINVAL;
     if (!d->A || !d->W) return SF_EINVAL;
     if (!al16(d->A) || !al16(d->W) || (d->lda & 7) || d->lda < d->K) return SF_EINVAL;
-    if (d->w_dtype == SF_BF16 && ((d->ldw & 7) || d->ldw < d->K)) return SF_EINVAL;
-    if (d->w_dtype == SF_I8 && ((d->ldw & 7) || d->ldw < d->K || !d->w_scale)) return SF_EINVAL;
+    if ((d->ldw & 7) || d->ldw < d->K) return SF_EINVAL;
+    if (d->w_dtype == SF_I8 && !d->w_scale) return SF_EINVAL;
     if ((int64_t)std::max(1, std::min(80, d->M)) * d->lda * 2 > 0x7fffffffLL) return SF_ENOTSUP;
+    if ((int64_t)std::min(64, d->N) * d->ldw * 2 > 0x7fffffffLL) return SF_ENOTSUP;
+    e.M = d->M;
+    e.N = d->N;
+    e.w_scale = d->w_dtype == SF_I8 ? d->w_scale : nullptr;
+    e.bias = d->bias;
+    e.act = d->act;
+    e.eps = d->eps;
+    if (d->epilogue == SF_EPI_HEADS) {
+        if (d->H <= 0 || d->S <= 0 || d->M % d->S) return SF_EINVAL;
+        const int cols = d->H * 64;
+        if (d->N % cols || d->N / cols > 3) return SF_EINVAL;
+        for (int j = 0; j < d->N / cols; ++j) {
+            if (!d->head_out[j] || !al8(d->head_out[j])) return SF_EINVAL;
+            for (int q = 0; q < 3; ++q)
+                if (d->head_stride[j][q] & 3) return SF_EINVAL;
+            e.head_out[j] = static_cast<uint16_t*>(d->head_out[j]);
+            e.head_gamma[j] = d->head_gamma[j];
+            e.head_sb[j] = d->head_stride[j][0];
+            e.head_sh[j] = d->head_stride[j][1];
+            e.head_ss[j] = d->head_stride[j][2];
+        }
+        e.H = d->H;
+        e.S = d->S;
+    } else if (d->epilogue == SF_EPI_PLAIN || d->epilogue == SF_EPI_ADD_NORM) {
+        if (!d->C || d->ldc < d->N) return SF_EINVAL;
+        if (d->c_dtype != SF_BF16 && d->c_dtype != SF_F32) return SF_ENOTSUP;
+        if ((d->accumulate || d->epilogue == SF_EPI_ADD_NORM) && d->c_dtype != SF_F32) return SF_EINVAL;
+        e.c = d->C;
+        e.ldc = d->ldc;
+        e.c_f32 = d->c_dtype == SF_F32;
+        e.accumulate = d->accumulate != 0 || d->epilogue == SF_EPI_ADD_NORM;
+        if (d->epilogue == SF_EPI_ADD_NORM) {
+            if (!d->norm_gamma || !d->norm_out || d->norm_ldo < d->N) return SF_EINVAL;
+            if (d->norm_dtype != SF_BF16 && d->norm_dtype != SF_F32) return SF_ENOTSUP;
+            if (d->N > 4096) return SF_ENOTSUP;
+            e.norm_gamma = d->norm_gamma;
+            e.norm_out = d->norm_out;
+            e.norm_ldo = d->norm_ldo;
+            e.norm_f32 = d->norm_dtype == SF_F32;
+        }
+    } else {
+        return SF_EINVAL;
+    }
+    return SF_OK;
+}
+
+// The split path needs 16-byte rows for its vector epilogue stores.
+bool splittable(const sf_gemm_desc* d) {
+    if (d->epilogue == SF_EPI_HEADS) return true;
+    if ((d->ldc & 3) || !(d->c_dtype == SF_F32 ? al16(d->C) : al8(d->C))) return false;
+    if (d->epilogue == SF_EPI_ADD_NORM &&
+        ((d->norm_ldo & 3) || !(d->norm_dtype == SF_F32 ? al16(d->norm_out) : al8(d->norm_out))))
+        return false;
+    return true;
+}
+
+int gemm_single_pass(const sf_gemm_desc* d, const sfk::EpiArgs& e, hipStream_t s) {
     sfk::GemmArgs g{};
     g.a = static_cast<const uint16_t*>(d->A);
     g.w = d->W;
@@ -265,41 +666,71 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     g.eps = d->eps;
     const bool w8 = d->w_dtype == SF_I8;
     if (d->epilogue == SF_EPI_HEADS) {
-        if (d->H <= 0 || d->S <= 0 || d->M % d->S) return SF_EINVAL;
-        const int cols = d->H * 64;
-        if (d->N % cols || d->N / cols > 3) return SF_EINVAL;
-        for (int j = 0; j < d->N / cols; ++j) {
-            if (!d->head_out[j]) return SF_EINVAL;
-            g.head_out[j] = static_cast<uint16_t*>(d->head_out[j]);
-            g.head_gamma[j] = d->head_gamma[j];
-            g.head_sb[j] = d->head_stride[j][0];
-            g.head_sh[j] = d->head_stride[j][1];
-            g.head_ss[j] = d->head_stride[j][2];
+        for (int j = 0; j < 3; ++j) {
+            g.head_out[j] = e.head_out[j];
+            g.head_gamma[j] = e.head_gamma[j];
+            g.head_sb[j] = e.head_sb[j];
+            g.head_sh[j] = e.head_sh[j];
+            g.head_ss[j] = e.head_ss[j];
         }
         g.heads = 1;
-        g.H = d->H;
-        g.S = d->S;
-    } else if (d->epilogue == SF_EPI_PLAIN) {
-        if (!d->C || d->ldc < d->N) return SF_EINVAL;
-        if (d->c_dtype != SF_BF16 && d->c_dtype != SF_F32) return SF_ENOTSUP;
-        if (d->accumulate && d->c_dtype != SF_F32) return SF_EINVAL;
+        g.H = e.H;
+        g.S = e.S;
+    } else {
         g.c = d->C;
         g.ldc = d->ldc;
-        g.c_f32 = d->c_dtype == SF_F32;
-        g.accumulate = d->accumulate != 0;
-    } else {
-        return SF_EINVAL;
+        g.c_f32 = e.c_f32;
+        g.accumulate = e.accumulate;
     }
-    hipStream_t s = static_cast<hipStream_t>(stream);
     const int mtiles = (d->M + 79) / 80;
     const int mb = d->M >= 80 ? 5 : (d->M + 15) / 16;
-    hipError_t e;
+    hipError_t err;
     if (g.heads) {
         const dim3 grid(d->N / 64, mtiles);
-        e = w8 ? sfk::launch_smallm<64, true>(g, mb, grid, s) : sfk::launch_smallm<64, false>(g, mb, grid, s);
+        err = w8 ? sfk::launch_smallm<64, true>(g, mb, grid, s) : sfk::launch_smallm<64, false>(g, mb, grid, s);
     } else {
         const dim3 grid((d->N + 15) / 16, mtiles);
-        e = w8 ? sfk::launch_smallm<16, true>(g, mb, grid, s) : sfk::launch_smallm<16, false>(g, mb, grid, s);
+        err = w8 ? sfk::launch_smallm<16, true>(g, mb, grid, s) : sfk::launch_smallm<16, false>(g, mb, grid, s);
     }
-    return e == hipSuccess ? SF_OK : SF_ELAUNCH;
+    if (err != hipSuccess) return SF_ELAUNCH;
+    if (d->epilogue == SF_EPI_ADD_NORM)
+        return sf_rmsnorm(d->C, SF_F32, d->ldc, d->norm_gamma, d->norm_out, d->norm_dtype, d->norm_ldo,
+                          d->M, d->N, d->eps, s);
+    return SF_OK;
+}
+}  // namespace
+
+extern "C" size_t sf_gemm_workspace_bytes(const sf_gemm_desc* d) {
+    if (!d) return 0;
+    const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K);
+    return p.split ? p.ws_bytes : 0;
+}
+
+extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
+    if (!d) return SF_EINVAL;
+    if (d->M < 0 || d->N < 0 || d->K < 0) return SF_EINVAL;
+    if ((long)d->M * d->N == 0) return SF_OK;
+    sfk::EpiArgs e{};
+    SF_CHECK_OK(validate(d, e));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K);
+    if (!d->workspace || !p.split || !splittable(d)) return gemm_single_pass(d, e, s);
+    if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < p.ws_bytes) return SF_EWORKSPACE;
+    if (!al16(d->workspace)) return SF_EINVAL;
+    sfk::SkArgs a{};
+    a.a = static_cast<const uint16_t*>(d->A);
+    a.w = d->W;
+    a.part = static_cast<float*>(d->workspace);
+    a.lda = d->lda;
+    a.ldw = d->ldw;
+    a.M = d->M; a.N = d->N; a.K = d->K;
+    sfk::launch_splitk(a, p, d->w_dtype == SF_I8, s);
+    if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
+    e.part = a.part;
+    e.splits = p.splits;
+    if (p.splits <= 1) sfk::launch_reduce<1>(d, e, s);
+    else if (p.splits <= 4) sfk::launch_reduce<4>(d, e, s);
+    else if (p.splits <= 8) sfk::launch_reduce<8>(d, e, s);
+    else sfk::launch_reduce<16>(d, e, s);
+    return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
 }

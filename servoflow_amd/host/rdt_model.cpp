@@ -11,9 +11,12 @@
 //     allocated once at creation from one device arena, so the step issues
 //     no allocation and is capturable (the reference calls cudaMallocAsync in
 //     every op, cuda_backend.cu:51-62, 490);
-//   * the block is 11 launches of fused kernels (sf_hip.h) instead of ~25:
-//     QKV projection writes normed per-head Q/K/V, attention writes
-//     [B,S,H*64] directly, projections add into the fp32 residual;
+//   * the block is a short chain of fused kernels (sf_hip.h) instead of
+//     ~25 launches: the QKV projection writes normed per-head Q/K/V,
+//     attention writes [B,S,H*64] directly, and each branch projection adds
+//     into the fp32 residual and applies the next RMSNorm in its epilogue
+//     (proj -> norm2, cross proj -> norm3, fc2 -> next block's norm1 or the
+//     final norm), so no standalone norm runs inside the block stack;
 //   * the cross-attention K/V projection runs once per inference
 //     (sf_rdt_set_condition) instead of in every block call
 //     (dit_block.cu:288-293);
@@ -107,6 +110,8 @@ struct sf_rdt {
     std::vector<uint16_t*> ck, cv; // per-layer cross K/V cache [B, H, Sc, 64]
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
+    void* gemm_ws = nullptr;       // split-K partial sums, shared by the stream's GEMMs
+    size_t gemm_ws_bytes = 0;
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -226,6 +231,39 @@ int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, i
     d.ldc = ldc;
     d.c_dtype = c_dtype;
     d.accumulate = accumulate ? 1 : 0;
+    d.workspace = m->gemm_ws;
+    d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
+    return sf_gemm(&d, s);
+}
+
+// x += A W^T + b (fp32 residual m->x), then m->n = rmsnorm(x) * gamma (bf16).
+int linear_add_norm(sf_rdt* m, const void* A, int M, int w_idx, int b_idx, int gamma_idx,
+                    hipStream_t s) {
+    const Param& W = m->params[w_idx];
+    const int D = m->cfg.hidden;
+    sf_gemm_desc d{};
+    d.M = M;
+    d.N = (int32_t)W.shape[0];
+    d.K = (int32_t)W.shape[1];
+    d.A = A;
+    d.lda = W.shape[1];
+    d.a_dtype = SF_BF16;
+    d.W = W.data;
+    d.ldw = W.shape[1];
+    d.w_dtype = W.dtype;
+    d.w_scale = W.scale;
+    d.bias = pf(m, b_idx);
+    d.epilogue = SF_EPI_ADD_NORM;
+    d.C = m->x;
+    d.ldc = D;
+    d.c_dtype = SF_F32;
+    d.eps = m->cfg.eps;
+    d.norm_gamma = pf(m, gamma_idx);
+    d.norm_out = m->n;
+    d.norm_ldo = D;
+    d.norm_dtype = SF_BF16;
+    d.workspace = m->gemm_ws;
+    d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
     return sf_gemm(&d, s);
 }
 
@@ -257,6 +295,8 @@ int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
         d.head_stride[j][1] = (int64_t)S * 64;
         d.head_stride[j][2] = 64;
     }
+    d.workspace = m->gemm_ws;
+    d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
     return sf_gemm(&d, s);
 }
 
@@ -272,6 +312,24 @@ int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v
     d.o_stride[1] = 64;
     d.o_stride[2] = c.hidden;
     return sf_attn_fwd(&d, q, k, v, out, m->attn_ws, m->attn_ws_bytes, s);
+}
+
+// Largest split-K workspace over the step's GEMMs (rows B*S, B*T, B or 1).
+size_t gemm_ws_for(const sf_rdt* m) {
+    const sf_rdt_config& c = m->cfg;
+    const int rows[4] = {c.batch * (c.horizon + 3), c.batch * c.horizon, c.batch, 1};
+    size_t best = 0;
+    for (const Param& p : m->params) {
+        if (p.shape.size() != 2 || p.dtype == SF_F32) continue;
+        for (int M : rows) {
+            sf_gemm_desc d{};
+            d.M = M;
+            d.N = (int32_t)p.shape[0];
+            d.K = (int32_t)p.shape[1];
+            best = std::max(best, sf_gemm_workspace_bytes(&d));
+        }
+    }
+    return best;
 }
 
 size_t attn_ws_for(const sf_rdt_config& c, int Sk) {
@@ -293,32 +351,44 @@ int timestep_embed(sf_rdt* m, const int* idx4, int step, float* out, hipStream_t
                   false, s);
 }
 
-// RDTBlock::forward (dit_block.cu:349-387) on the fp32 residual m->x.
+// Gamma of the RMSNorm that follows block i: the next block's norm1, or the
+// final layer's norm after the last block.
+int next_norm(const sf_rdt* m, int i) {
+    return i + 1 < m->cfg.layers ? m->layers[i + 1].norm1 : m->fnorm;
+}
+
+// RDTBlock::forward (dit_block.cu:349-387) on the fp32 residual m->x, with
+// m->n holding norm1(x) on entry; on exit m->n holds the next norm of x.
 int block_forward(sf_rdt* m, int i, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const LayerIdx& L = m->layers[i];
     const int D = c.hidden, S = c.horizon + 3, M = c.batch * S;
     // self-attention branch
-    SF_TRY(sf_rmsnorm(m->x, SF_F32, D, pf(m, L.norm1), m->n, SF_BF16, D, M, D, c.eps, s));
     uint16_t* qkv[3] = {m->q, m->k, m->v};
     const int qk_g[3] = {L.q_norm, L.k_norm, -1};
     SF_TRY(linear_heads(m, m->n, M, S, L.qkv_w, L.qkv_b, qkv, qk_g, 3, s));
     SF_TRY(attention(m, m->q, m->k, m->v, S, nullptr, m->a, s));
-    SF_TRY(linear(m, m->a, D, M, L.proj_w, L.proj_b, SF_ACT_NONE, m->x, D, SF_F32, true, s));
+    SF_TRY(linear_add_norm(m, m->a, M, L.proj_w, L.proj_b, L.norm2, s));
     // cross-attention branch: even blocks attend to language, odd to image
     // (dit_block.cu:369)
-    SF_TRY(sf_rmsnorm(m->x, SF_F32, D, pf(m, L.norm2), m->n, SF_BF16, D, M, D, c.eps, s));
     uint16_t* cq[1] = {m->q};
     const int cq_g[1] = {L.cq_norm};
     SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s));
     const bool lang = (i % 2) == 0;
     SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? c.lang_max : c.img_len,
                      lang ? m->lang_len : nullptr, m->a, s));
-    SF_TRY(linear(m, m->a, D, M, L.cproj_w, L.cproj_b, SF_ACT_NONE, m->x, D, SF_F32, true, s));
+    SF_TRY(linear_add_norm(m, m->a, M, L.cproj_w, L.cproj_b, L.norm3, s));
     // FFN branch (Mlp::forward, dit_block.cu:143-163)
-    SF_TRY(sf_rmsnorm(m->x, SF_F32, D, pf(m, L.norm3), m->n, SF_BF16, D, M, D, c.eps, s));
     SF_TRY(linear(m, m->n, D, M, L.fc1_w, L.fc1_b, SF_ACT_GELU_TANH, m->h, D, SF_BF16, false, s));
-    return linear(m, m->h, D, M, L.fc2_w, L.fc2_b, SF_ACT_NONE, m->x, D, SF_F32, true, s);
+    return linear_add_norm(m, m->h, M, L.fc2_w, L.fc2_b, next_norm(m, i), s);
+}
+
+// m->n = first norm applied to the residual m->x before block `first`.
+int entry_norm(sf_rdt* m, int first, hipStream_t s) {
+    const sf_rdt_config& c = m->cfg;
+    const int D = c.hidden, M = c.batch * (c.horizon + 3);
+    const int g = first < c.layers ? m->layers[first].norm1 : m->fnorm;
+    return sf_rmsnorm(m->x, SF_F32, D, pf(m, g), m->n, SF_BF16, D, M, D, c.eps, s);
 }
 
 // RDT1BModel::denoise_step up to the final layer: velocity rows [B*S, A].
@@ -339,9 +409,9 @@ int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s) {
     SF_TRY(timestep_embed(m, m->te, t_int, m->t_emb, s));
     SF_TRY(sf_assemble_tokens(m->x, m->t_emb, m->f_emb, m->state_tok, m->act_out, pf(m, m->xpos),
                               c.batch, T, D, s));
+    SF_TRY(entry_norm(m, 0, s));
     for (int i = 0; i < c.layers; ++i) SF_TRY(block_forward(m, i, s));
-    // FinalLayer (dit_block.cu:407-412)
-    SF_TRY(sf_rmsnorm(m->x, SF_F32, D, pf(m, m->fnorm), m->n, SF_BF16, D, M, D, c.eps, s));
+    // FinalLayer (dit_block.cu:407-412); m->n = norm_final(x) from the last block
     SF_TRY(linear(m, m->n, D, M, m->f1w, m->f1b, SF_ACT_GELU_TANH, m->h, D, SF_BF16, false, s));
     return linear(m, m->h, D, M, m->f2w, m->f2b, SF_ACT_NONE, m->vel_rows, A, SF_F32, false, s);
 }
@@ -468,6 +538,8 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     m->attn_ws_bytes = std::max(attn_ws_for(c, c.lang_max), attn_ws_for(c, c.img_len));
     m->attn_ws_bytes = std::max(m->attn_ws_bytes, attn_ws_for(c, (int)S));
     bufs.push_back({&m->attn_ws, std::max<size_t>(m->attn_ws_bytes, 256)});
+    m->gemm_ws_bytes = gemm_ws_for(m);
+    bufs.push_back({&m->gemm_ws, std::max<size_t>(m->gemm_ws_bytes, 256)});
     std::vector<size_t> boff(bufs.size());
     for (size_t i = 0; i < bufs.size(); ++i) {
         boff[i] = off;
@@ -642,6 +714,7 @@ extern "C" int sf_rdt_run_blocks(sf_rdt* m, float* x, int32_t first, int32_t cou
     hipStream_t s = pick_stream(m, stream);
     const size_t nbytes = (size_t)c.batch * (c.horizon + 3) * c.hidden * 4;
     SF_HIP(hipMemcpyAsync(m->x, x, nbytes, hipMemcpyDeviceToDevice, s));
+    SF_TRY(entry_norm(m, first, s));
     for (int i = first; i < first + count; ++i) SF_TRY(block_forward(m, i, s));
     SF_HIP(hipMemcpyAsync(x, m->x, nbytes, hipMemcpyDeviceToDevice, s));
     return SF_OK;

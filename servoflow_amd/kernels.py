@@ -20,46 +20,79 @@ def _p(t):
     return None if t is None else t.data_ptr()
 
 
+def _desc(a, w, bias, act, w_scale):
+    M, K = a.shape
+    d = abi.GemmDesc()
+    d.M, d.N, d.K = M, w.shape[0], K
+    d.A, d.lda, d.a_dtype = a.data_ptr(), a.stride(0), _DT[a.dtype]
+    d.W, d.ldw, d.w_dtype = w.data_ptr(), w.stride(0), _DT[w.dtype]
+    d.w_scale = _p(w_scale)
+    d.bias = _p(bias)
+    d.act = act
+    return d
+
+
+def _run(d, a, workspace):
+    """workspace: "auto" allocates what the split-K path needs, None runs the
+    single-pass path, a tensor is used as given."""
+    if isinstance(workspace, str):
+        nbytes = abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d))
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=a.device) if nbytes else None
+    if workspace is not None:
+        d.workspace, d.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    abi.check(abi.lib().sf_gemm(ctypes.byref(d), _stream(a)), "sf_gemm")
+
+
+def workspace_bytes(a, w):
+    d = _desc(a, w, None, 0, None)
+    return abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d))
+
+
 def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat16,
-         accumulate=False, w_scale=None):
+         accumulate=False, w_scale=None, workspace="auto"):
     """out[M,N] = act(a[M,K] w[N,K]^T + bias) (bf16 a; bf16 or int8 w with
     per-row fp32 w_scale).  accumulate adds into an fp32 `out`."""
     M, K = a.shape
     N = w.shape[0]
     if out is None:
         out = torch.empty(M, N, dtype=out_dtype, device=a.device)
-    d = abi.GemmDesc()
-    d.M, d.N, d.K = M, N, K
-    d.A, d.lda, d.a_dtype = a.data_ptr(), a.stride(0), _DT[a.dtype]
-    d.W, d.ldw, d.w_dtype = w.data_ptr(), w.stride(0), _DT[w.dtype]
-    d.w_scale = _p(w_scale)
-    d.bias = _p(bias)
-    d.act = act
+    d = _desc(a, w, bias, act, w_scale)
     d.epilogue = abi.SF_EPI_PLAIN
     d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), _DT[out.dtype]
     d.accumulate = 1 if accumulate else 0
-    abi.check(abi.lib().sf_gemm(ctypes.byref(d), _stream(a)), "sf_gemm")
+    _run(d, a, workspace)
     return out
 
 
-def gemm_heads(a, w, bias, S, H, outs, gammas=(None, None, None), eps=1e-6, w_scale=None):
+def gemm_add_norm(a, w, bias, residual, gamma, eps=1e-6, act=abi.SF_ACT_NONE, w_scale=None,
+                  norm_dtype=torch.bfloat16, workspace="auto"):
+    """residual (fp32 [M,N]) += act(a w^T + bias); returns
+    rmsnorm(residual) * gamma in norm_dtype."""
+    M = a.shape[0]
+    N = w.shape[0]
+    out = torch.empty(M, N, dtype=norm_dtype, device=a.device)
+    d = _desc(a, w, bias, act, w_scale)
+    d.epilogue = abi.SF_EPI_ADD_NORM
+    d.C, d.ldc, d.c_dtype = residual.data_ptr(), residual.stride(0), abi.SF_F32
+    d.eps = eps
+    d.norm_gamma, d.norm_out = gamma.data_ptr(), out.data_ptr()
+    d.norm_ldo, d.norm_dtype = out.stride(0), _DT[norm_dtype]
+    _run(d, a, workspace)
+    return out
+
+
+def gemm_heads(a, w, bias, S, H, outs, gammas=(None, None, None), eps=1e-6, w_scale=None,
+               workspace="auto"):
     """Projection whose N columns are sections of H*64, written per head to
     outs[j] ([B,H,S,64] bf16 views) with optional per-head RMSNorm."""
-    M, K = a.shape
-    N = w.shape[0]
-    d = abi.GemmDesc()
-    d.M, d.N, d.K = M, N, K
-    d.A, d.lda, d.a_dtype = a.data_ptr(), a.stride(0), _DT[a.dtype]
-    d.W, d.ldw, d.w_dtype = w.data_ptr(), w.stride(0), _DT[w.dtype]
-    d.w_scale = _p(w_scale)
-    d.bias = _p(bias)
+    d = _desc(a, w, bias, abi.SF_ACT_NONE, w_scale)
     d.epilogue = abi.SF_EPI_HEADS
     d.H, d.S, d.eps = H, S, eps
     for j, o in enumerate(outs):
         d.head_out[j] = o.data_ptr()
         d.head_gamma[j] = _p(gammas[j])
         d.head_stride[j][:] = (o.stride(0), o.stride(1), o.stride(2))
-    abi.check(abi.lib().sf_gemm(ctypes.byref(d), _stream(a)), "sf_gemm")
+    _run(d, a, workspace)
     return outs
 
 

@@ -3,7 +3,8 @@ against the CPU oracle (bf16-rounded inputs shared by both sides).
 
 GEMM inputs are bf16, so products are exact and only the fp32 summation
 order differs from the oracle: fp32 outputs are held to max-abs <= 2e-2 and
-mean-rel <= 1e-4.  The int8 unpack and indexing are bit-exact (dequant
+mean-rel <= 1e-4.  GEMM tests run both kernels of sf_gemm: the split-K path
+(workspace given, M <= 160) and the single-pass path (workspace NULL).  The int8 unpack and indexing are bit-exact (dequant
 kernel vs oracle, all 256 codes, the reference's KATs)."""
 import json
 import os
@@ -42,39 +43,87 @@ def close(got, ref, what, rel=1e-4):
     assert mx <= 2e-2 and mr <= rel, f"{what}: max-abs {mx:.3e} mean-rel {mr:.3e}"
 
 
+PATHS = ["auto", None]     # split-K with a workspace, single-pass without
+
+
 @pytest.mark.parametrize("M,N,K", [(67, 2048, 2048), (1, 2048, 256), (80, 6144, 2048),
-                                   (81, 100, 1152), (200, 48, 64), (64, 2048, 256), (16, 128, 2048)])
+                                   (81, 100, 1152), (200, 48, 64), (64, 2048, 256), (16, 128, 2048),
+                                   (134, 2048, 1152), (3, 64, 4096), (160, 96, 2080)])
 @pytest.mark.parametrize("act", [abi.SF_ACT_NONE, abi.SF_ACT_GELU_TANH, abi.SF_ACT_SILU])
-def test_gemm_bias_act_f32_out(M, N, K, act):
+@pytest.mark.parametrize("ws", PATHS)
+def test_gemm_bias_act_f32_out(M, N, K, act, ws):
     a, w = rounded(1 + M, (M, K)), rounded(2 + N, (N, K), 0.02)
     b = O.randn(3, (N,), 0.02)
-    got = host(K_gemm(a, w, b, act))
+    got = host(K_gemm(a, w, b, act, workspace=ws))
     ref = O.linear(a, w, b, act=act)
     close(got, ref, f"gemm {M}x{N}x{K} act {act}")
 
 
-def K_gemm(a, w, b, act, out_dtype=torch.float32):
+def K_gemm(a, w, b, act, out_dtype=torch.float32, workspace="auto"):
     return K.gemm(dev(a), dev(w), dev(b, torch.float32) if b is not None else None, act,
-                  out_dtype=out_dtype)
+                  out_dtype=out_dtype, workspace=workspace)
 
 
-def test_gemm_bf16_out_is_rounded_f32():
+def test_gemm_split_path_is_used_and_deterministic():
+    a, w = rounded(5, (67, 2048)), rounded(6, (2048, 2048), 0.02)
+    assert K.workspace_bytes(dev(a), dev(w)) > 0
+    r1 = host(K_gemm(a, w, None, 0))
+    r2 = host(K_gemm(a, w, None, 0))
+    assert np.array_equal(r1, r2)
+    big = rounded(7, (161, 2048))
+    assert K.workspace_bytes(dev(big), dev(w)) == 0      # M > 160: single-pass only
+
+
+def test_gemm_workspace_too_small_is_an_error():
+    a, w = dev(rounded(8, (67, 2048))), dev(rounded(9, (2048, 2048), 0.02))
+    small = torch.empty(1024, dtype=torch.uint8, device=DEV)
+    with pytest.raises(abi.SfError, match="workspace"):
+        K.gemm(a, w, workspace=small)
+
+
+@pytest.mark.parametrize("ws", PATHS)
+def test_gemm_bf16_out_is_rounded_f32(ws):
     a, w = rounded(11, (67, 2048)), rounded(12, (2048, 2048), 0.02)
-    f32 = host(K_gemm(a, w, None, 0))
-    b16 = host(K_gemm(a, w, None, 0, torch.bfloat16))
+    f32 = host(K_gemm(a, w, None, 0, workspace=ws))
+    b16 = host(K_gemm(a, w, None, 0, torch.bfloat16, workspace=ws))
     assert np.array_equal(b16, O.bf16_round(f32))
 
 
-def test_gemm_accumulate_into_residual():
+@pytest.mark.parametrize("ws", PATHS)
+def test_gemm_accumulate_into_residual(ws):
     a, w = rounded(21, (67, 2048)), rounded(22, (2048, 2048), 0.02)
     b = O.randn(23, (2048,), 0.02)
     x = O.randn(24, (67, 2048))
     xd = dev(x, torch.float32)
-    K.gemm(dev(a), dev(w), dev(b, torch.float32), out=xd, accumulate=True)
+    K.gemm(dev(a), dev(w), dev(b, torch.float32), out=xd, accumulate=True, workspace=ws)
     close(host(xd), x + O.linear(a, w, b), "residual add", rel=1e-5)
 
 
-def test_gemm_heads_qkv_with_qk_norm():
+@pytest.mark.parametrize("M", [67, 134, 300])
+@pytest.mark.parametrize("ws", PATHS)
+@pytest.mark.parametrize("norm_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_add_norm(M, ws, norm_dtype):
+    """x += a w^T + b; n = rmsnorm(x) * gamma (the branch add and the next
+    block norm, fused_add_rms_norm, norm.cuh:130-171)."""
+    a, w = rounded(25 + M, (M, 2048)), rounded(26, (2048, 2048), 0.02)
+    b = O.randn(27, (2048,), 0.02)
+    g = 1.0 + O.randn(28, (2048,), 0.1)
+    x = O.randn(29, (M, 2048))
+    xd = dev(x, torch.float32)
+    n = K.gemm_add_norm(dev(a), dev(w), dev(b, torch.float32), xd, dev(g, torch.float32),
+                        norm_dtype=norm_dtype, workspace=ws)
+    x_ref = x + O.linear(a, w, b)
+    n_ref = O.rms_norm(x_ref, g)
+    close(host(xd), x_ref, "residual", rel=1e-5)
+    got = host(n)
+    if norm_dtype == torch.float32:
+        close(got, n_ref, "norm", rel=1e-4)
+    else:
+        assert np.all(np.abs(got - n_ref) <= np.abs(n_ref) * 2.0 ** -7 + 1e-4)
+
+
+@pytest.mark.parametrize("ws", PATHS)
+def test_gemm_heads_qkv_with_qk_norm(ws):
     B, S, H, D = 2, 67, 32, 64
     a = rounded(31, (B * S, 2048))
     w = rounded(32, (3 * H * D, 2048), 0.02)
@@ -83,7 +132,7 @@ def test_gemm_heads_qkv_with_qk_norm():
     gk = 1.0 + O.randn(35, (64,), 0.1)
     outs = [torch.empty(B, H, S, D, device=DEV, dtype=torch.bfloat16) for _ in range(3)]
     K.gemm_heads(dev(a), dev(w), dev(b, torch.float32), S, H, outs,
-                 (dev(gq, torch.float32), dev(gk, torch.float32), None))
+                 (dev(gq, torch.float32), dev(gk, torch.float32), None), workspace=ws)
     qkv = O.linear(a, w, b).reshape(B, S, 3 * H * D)
     Q, Kh, V = O.split_qkv(qkv, H, D)
     Q = O.rms_norm(Q, gq)
@@ -110,13 +159,15 @@ def test_gemm_heads_kv_strided_output():
         assert mean_rel(host(got), ref) < 3e-3
 
 
-def test_gemm_int8_weights():
-    a = rounded(51, (67, 2048))
+@pytest.mark.parametrize("M", [67, 134])
+@pytest.mark.parametrize("ws", PATHS)
+def test_gemm_int8_weights(M, ws):
+    a = rounded(51, (M, 2048))
     wf = O.randn(52, (2048, 2048), 0.02)
     q, s = O.quantize_int8_rows(wf)
     b = O.randn(53, (2048,), 0.02)
     got = host(K.gemm(dev(a), dev(q, torch.int8), dev(b, torch.float32), out_dtype=torch.float32,
-                      w_scale=dev(s, torch.float32)))
+                      w_scale=dev(s, torch.float32), workspace=ws))
     ref = O.linear(a, O.dequant_int8(q, s), b)
     close(got, ref, "int8 gemm")
 
