@@ -373,29 +373,43 @@ struct EpiArgs {
 };
 
 // Sum of the K-slice partials for C[m][n..n+3], slices in ascending order,
-// then scale, bias and activation.  All NS loads are issued before the
-// first add (indices past `splits` re-read the last slice and are masked),
-// so the sum costs one memory round trip.
+// then scale, bias and activation.  Every load (all NS slices -- indices past
+// `splits` re-read the last slice and are masked -- plus the bias and scale
+// quads) is issued before the first add, so the epilogue costs one memory
+// round trip.
 template <int NS>
-__device__ __forceinline__ f32x4 finish4(const EpiArgs& e, int m, int n) {
+struct Quad {
+    f32x4 part[NS];
+    f32x4 bias, scale;
+};
+
+template <int NS>
+__device__ __forceinline__ void load_quad(const EpiArgs& e, int m, int n, Quad<NS>& q) {
     const float* p = e.part + (int64_t)m * e.N + n;
     const int64_t stride = (int64_t)e.M * e.N;
-    f32x4 part[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s)
-        part[s] = *reinterpret_cast<const f32x4*>(p + min(s, e.splits - 1) * stride);
-    f32x4 v = part[0];
+        q.part[s] = *reinterpret_cast<const f32x4*>(p + min(s, e.splits - 1) * stride);
+    q.bias = e.bias ? *reinterpret_cast<const f32x4*>(e.bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+    q.scale = e.w_scale ? *reinterpret_cast<const f32x4*>(e.w_scale + n) : f32x4{1.f, 1.f, 1.f, 1.f};
+}
+
+template <int NS>
+__device__ __forceinline__ f32x4 finish_quad(const EpiArgs& e, const Quad<NS>& q) {
+    f32x4 v = q.part[0];
 #pragma unroll
     for (int s = 1; s < NS; ++s)
-        if (s < e.splits) v += part[s];
+        if (s < e.splits) v += q.part[s];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float x = v[j];
-        if (e.w_scale) x *= e.w_scale[n + j];
-        if (e.bias) x += e.bias[n + j];
-        v[j] = apply_act(e.act, x);
-    }
+    for (int j = 0; j < 4; ++j) v[j] = apply_act(e.act, v[j] * q.scale[j] + q.bias[j]);
     return v;
+}
+
+template <int NS>
+__device__ __forceinline__ f32x4 finish4(const EpiArgs& e, int m, int n) {
+    Quad<NS> q;
+    load_quad<NS>(e, m, n, q);
+    return finish_quad<NS>(e, q);
 }
 
 __device__ __forceinline__ uint2 pack_bf16x4(f32x4 v) {
@@ -435,13 +449,14 @@ __global__ __launch_bounds__(256) void reduce_heads_kernel(const EpiArgs e) {
     const int d = n % 64;
     const float* gamma = e.head_gamma[sec];
     if (gamma) {
+        const f32x4 gq = *reinterpret_cast<const f32x4*>(gamma + d);
         // rms_norm_kernel_impl over the 64 head dims (norm.cuh:89-122)
         float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
 #pragma unroll
         for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 64);
         const float inv_rms = 1.f / sqrtf(ss / 64.f + e.eps);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = v[j] * inv_rms * gamma[d + j];
+        for (int j = 0; j < 4; ++j) v[j] = v[j] * inv_rms * gq[j];
     }
     const int b = m / e.S;
     const int s = m % e.S;
@@ -449,42 +464,56 @@ __global__ __launch_bounds__(256) void reduce_heads_kernel(const EpiArgs e) {
     *reinterpret_cast<uint2*>(o) = pack_bf16x4(v);
 }
 
-// One workgroup per row: x[m] += result[m]; out[m] = rmsnorm(x[m]) * gamma.
-constexpr int kAddNormMaxChunks = 4;   // N <= 4 * 256 * 4 = 4096
+// One workgroup of 512 threads per row: x[m] += result[m];
+// out[m] = rmsnorm(x[m]) * gamma.
+constexpr int kAddNormThreads = 512;
+constexpr int kAddNormMaxChunks = 2;   // N <= 2 * 512 * 4 = 4096
 template <int NS>
-__global__ __launch_bounds__(256) void reduce_addnorm_kernel(const EpiArgs e) {
-    __shared__ float red[4];
+__global__ __launch_bounds__(kAddNormThreads) void reduce_addnorm_kernel(const EpiArgs e) {
+    __shared__ float red[kAddNormThreads / 64];
     const int m = blockIdx.x;
     const int n4 = e.N / 4;
     float* x = static_cast<float*>(e.c) + (int64_t)m * e.ldc;
-    f32x4 xv[kAddNormMaxChunks];
+    // every load of the row first (partials and residual), then the stores:
+    // a store to x between them would keep later loads from issuing early
+    const int nch = min(kAddNormMaxChunks, (n4 - (int)threadIdx.x + kAddNormThreads - 1) / kAddNormThreads);
+    Quad<NS> q[kAddNormMaxChunks];
+    f32x4 xv[kAddNormMaxChunks], gv[kAddNormMaxChunks];
+#pragma unroll
+    for (int i = 0; i < kAddNormMaxChunks; ++i) {
+        const int c = (int)threadIdx.x + kAddNormThreads * i;
+        if (i < nch) {
+            load_quad<NS>(e, m, 4 * c, q[i]);
+            xv[i] = *reinterpret_cast<const f32x4*>(x + 4 * c);
+            gv[i] = *reinterpret_cast<const f32x4*>(e.norm_gamma + 4 * c);
+        }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < kAddNormMaxChunks; ++i) {
-        const int c = threadIdx.x + 256 * i;
-        xv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (c < n4) {
-            f32x4 v = finish4<NS>(e, m, 4 * c);
-            f32x4* xp = reinterpret_cast<f32x4*>(x + 4 * c);
-            v += *xp;
-            *xp = v;
-            xv[i] = v;
-            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        if (i < nch) {
+            xv[i] += finish_quad<NS>(e, q[i]);
+            ss += xv[i][0] * xv[i][0] + xv[i][1] * xv[i][1] + xv[i][2] * xv[i][2] + xv[i][3] * xv[i][3];
         }
     }
+#pragma unroll
+    for (int i = 0; i < kAddNormMaxChunks; ++i)
+        if (i < nch) *reinterpret_cast<f32x4*>(x + 4 * ((int)threadIdx.x + kAddNormThreads * i)) = xv[i];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
-    const float total = red[0] + red[1] + red[2] + red[3];
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAddNormThreads / 64; ++w) total += red[w];
     const float inv_rms = 1.f / sqrtf(total / (float)e.N + e.eps);
 #pragma unroll
     for (int i = 0; i < kAddNormMaxChunks; ++i) {
-        const int c = threadIdx.x + 256 * i;
-        if (c < n4) {
+        const int c = threadIdx.x + kAddNormThreads * i;
+        if (i < nch) {
             f32x4 o;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o[j] = xv[i][j] * inv_rms * e.norm_gamma[4 * c + j];
+            for (int j = 0; j < 4; ++j) o[j] = xv[i][j] * inv_rms * gv[i][j];
             const int64_t off = (int64_t)m * e.norm_ldo + 4 * c;
             if (e.norm_f32)
                 *reinterpret_cast<f32x4*>(static_cast<float*>(e.norm_out) + off) = o;
@@ -504,7 +533,10 @@ struct SkPlan {
 // a 2048 x 2048 weight becomes 256 workgroups of 32 KB each and the
 // 6144-row QKV weight 768 (three per CU: LDS <= 42 KB each, so the whole
 // grid is resident at once).  Slices of 512 only when 256 would need more
-// than 16 slices or more workgroups than fit on the chip at once.
+// than 16 slices or more workgroups than fit on the chip at once for one
+// 80-row tile.  The slicing depends on (N, K) only, never on M, so each
+// row's sums are added in the same order whatever the batch: a row's result
+// does not depend on how many rows share the call.
 constexpr int kSkResident = 256 * 3;
 inline SkPlan plan_splitk(int M, int N, int K) {
     SkPlan p;
@@ -515,7 +547,7 @@ inline SkPlan plan_splitk(int M, int N, int K) {
     p.ntiles = (N + 16 * p.nw - 1) / (16 * p.nw);
     p.kt = 256;
     p.splits = (K + 255) / 256;
-    if ((int64_t)p.ntiles * p.mtiles * p.splits > kSkResident || p.splits > kSkMaxSplits) {
+    if ((int64_t)p.ntiles * p.splits > kSkResident || p.splits > kSkMaxSplits) {
         p.kt = 512;
         p.splits = (K + 511) / 512;
     }
@@ -560,7 +592,7 @@ void launch_reduce(const sf_gemm_desc* d, const EpiArgs& e, hipStream_t s) {
     if (d->epilogue == SF_EPI_HEADS)
         hipLaunchKernelGGL(reduce_heads_kernel<NS>, dim3(blocks), dim3(256), 0, s, e);
     else if (d->epilogue == SF_EPI_ADD_NORM)
-        hipLaunchKernelGGL(reduce_addnorm_kernel<NS>, dim3(d->M), dim3(256), 0, s, e);
+        hipLaunchKernelGGL(reduce_addnorm_kernel<NS>, dim3(d->M), dim3(kAddNormThreads), 0, s, e);
     else
         hipLaunchKernelGGL(reduce_plain_kernel<NS>, dim3(blocks), dim3(256), 0, s, e);
 }
@@ -643,9 +675,16 @@ int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
     return SF_OK;
 }
 
-// The split path needs 16-byte rows for its vector epilogue stores.
+// The split path reads bias / scale / gamma and writes its outputs as
+// 16-byte quads.
 bool splittable(const sf_gemm_desc* d) {
-    if (d->epilogue == SF_EPI_HEADS) return true;
+    if (!al16(d->bias) || (d->w_dtype == SF_I8 && !al16(d->w_scale))) return false;
+    if (d->epilogue == SF_EPI_HEADS) {
+        for (int j = 0; j < 3; ++j)
+            if (!al16(d->head_gamma[j])) return false;
+        return true;
+    }
+    if (d->epilogue == SF_EPI_ADD_NORM && !al16(d->norm_gamma)) return false;
     if ((d->ldc & 3) || !(d->c_dtype == SF_F32 ? al16(d->C) : al8(d->C))) return false;
     if (d->epilogue == SF_EPI_ADD_NORM &&
         ((d->norm_ldo & 3) || !(d->norm_dtype == SF_F32 ? al16(d->norm_out) : al8(d->norm_out))))

@@ -74,6 +74,17 @@ def test_gemm_split_path_is_used_and_deterministic():
     assert K.workspace_bytes(dev(big), dev(w)) == 0      # M > 160: single-pass only
 
 
+@pytest.mark.parametrize("N", [2048, 6144])
+def test_gemm_split_rows_independent_of_batch(N):
+    """A row's result does not depend on how many rows share the call (the
+    split-K slicing depends on N and K only)."""
+    w = rounded(10, (N, 2048), 0.02)
+    a = rounded(11, (150, 2048))
+    full = host(K_gemm(a, w, None, 0))
+    for M in (1, 67, 80, 81, 134):
+        assert np.array_equal(host(K_gemm(a[:M], w, None, 0)), full[:M]), M
+
+
 def test_gemm_workspace_too_small_is_an_error():
     a, w = dev(rounded(8, (67, 2048))), dev(rounded(9, (2048, 2048), 0.02))
     small = torch.empty(1024, dtype=torch.uint8, device=DEV)
