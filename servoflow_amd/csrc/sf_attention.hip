@@ -6,8 +6,9 @@
 // (src/backend/cuda/ops/attention.cu:183-197), whose arithmetic is the
 // online-softmax loop of naive_attention_kernel (attention.cu:90-139).
 //
-// Design (one kernel family serves the 67x67 self-attention and the
-// 67 x 4374 / 67 x <=1024 cross-attention):
+// Design (the split kernel serves the 67 x 4374 / 67 x <=1024
+// cross-attention; attn_short_kernel below serves key sets of <= 128, the
+// 67 x 67 self-attention):
 //   * grid = (splits x query-chunks, H, B); a workgroup of 4 waves owns one
 //     (b, h, query chunk of 80 rows, key split).  Splitting the keys
 //     (flash-decoding) is what fills 256 CUs when B*H = 32.
@@ -461,6 +462,161 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     store_out(a, b, h, q, lane, o);
 }
 
+// ---------------------------------------------------------------------------
+// Short key sets (Sk <= 128: the 67 x 67 self-attention of every block, short
+// language conditions): one wave per (b, h, 16-query block), all of K, V and
+// the query block loaded at once (one memory round trip), a single-pass
+// softmax over the whole key set (no running max, no split, no cross-wave
+// merge), and the result stored straight from the accumulators.
+//
+// S^T = K.Q^T with K fragments loaded from global directly in MFMA operand
+// layout.  V is staged in LDS in its natural [key][d] layout and read back as
+// the V^T operand with ds_read_b64_tr_b16: within each 16-lane group, lane j
+// receives element j%4 of the 8-byte rows addressed by lanes 4k + j/4,
+// k = 0..3, so lane i of group g addressing V[k0 + i/4][d0 + 4(i%4)] gives
+// lane j the four keys k0..k0+3 of head dim d0 + j -- the V^T fragment whose
+// key order matches the P^T slots the S^T accumulator provides.
+// ---------------------------------------------------------------------------
+constexpr int kShortMaxKeys = 128;
+constexpr int kVPitch = 80;   // LDS row pitch of V (bf16): 160 B keeps the four rows of a read apart
+
+typedef short v4i16 __attribute__((__vector_size__(8)));
+
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+    const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(p));
+    return __builtin_bit_cast(uint2, v);
+}
+
+template <int KB>   // 16-key blocks covering Sk (even, <= 8)
+__global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
+    constexpr int KROWS = 16 * KB;
+    __shared__ __attribute__((aligned(16))) uint16_t vl[KROWS * kVPitch];
+    const int lane = threadIdx.x;
+    const int g = lane >> 4;
+    const int r = lane & 15;
+    const int q0 = 16 * blockIdx.x;
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
+
+    int valid = a.Sk;
+    if (a.valid_len) {
+        const int vl_ = a.valid_len[b];
+        valid = vl_ < 0 ? 0 : (vl_ > a.Sk ? a.Sk : vl_);
+    }
+    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+    // rows outside [0, Sq) / [0, valid) read as zeros
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qp, (uint32_t)(a.Sq * a.q_ss * 2));
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, (uint32_t)(valid * a.k_ss * 2));
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vp, (uint32_t)(valid * a.v_ss * 2));
+
+    // every load of the wave up front
+    u32x4 vv[2 * KB];
+#pragma unroll
+    for (int j = 0; j < 2 * KB; ++j) {
+        const int c = lane + 64 * j;          // 16-byte chunk: key c/8, dims 8(c%8)..
+        vv[j] = buffer_load16(vrs, (uint32_t)(((c >> 3) * a.v_ss + (c & 7) * 8) * 2));
+    }
+    bf16x8 kf[KB][2];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+            kf[kb][hh] = __builtin_bit_cast(
+                bf16x8, buffer_load16(krs, (uint32_t)(((16 * kb + r) * a.k_ss + 32 * hh + 8 * g) * 2)));
+    }
+    bf16x8 qf[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+        qf[hh] = __builtin_bit_cast(
+            bf16x8, buffer_load16(qrs, (uint32_t)(((q0 + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
+#pragma unroll
+    for (int j = 0; j < 2 * KB; ++j) {
+        const int c = lane + 64 * j;
+        *reinterpret_cast<u32x4*>(vl + (c >> 3) * kVPitch + (c & 7) * 8) = vv[j];
+    }
+    asm volatile("" ::: "memory");
+
+    // S^T blocks: lane holds keys 16kb + 4g + i of query q0 + r (raw scores)
+    f32x4 s[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        z = mfma16x16x32(kf[kb][0], qf[0], z);
+        s[kb] = mfma16x16x32(kf[kb][1], qf[1], z);
+    }
+    const int qrow = q0 + r;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = 16 * kb + 4 * g + i;
+            const bool dead = key >= valid || (a.causal && key > qrow);
+            s[kb][i] = dead ? -INFINITY : s[kb][i];
+            mx = fmaxf(mx, s[kb][i]);
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float nm = mx == -INFINITY ? 0.f : -mx * a.scale_log2;
+
+    // P^T as bf16 (hi, lo) pairs, O^T += V^T . P^T per 32-key step
+    f32x4 acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ls = 0.f;
+#pragma unroll
+    for (int j = 0; j < KB / 2; ++j) {
+        uint32_t pb[8], lb[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float p = fast_exp2(fmaf(s[2 * j + (t >> 2)][t & 3], a.scale_log2, nm));
+            ls += p;
+            pb[t] = __float_as_uint(p);
+            lb[t] = __float_as_uint(p - __uint_as_float(pb[t] & 0xffff0000u));
+        }
+        const bf16x8 ph = u32x4_as_bf16x8(u32x4{__builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u),
+                                                __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
+                                                __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u),
+                                                __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)});
+        const bf16x8 pl = u32x4_as_bf16x8(u32x4{__builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u),
+                                                __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u),
+                                                __builtin_amdgcn_perm(lb[5], lb[4], 0x07060302u),
+                                                __builtin_amdgcn_perm(lb[7], lb[6], 0x07060302u)});
+        // keys 32j + 4g + (0..3) and 32j + 16 + 4g + (0..3): the P^T slot order
+        const uint16_t* vrow = vl + (32 * j + 4 * g + (r >> 2)) * kVPitch + 4 * (r & 3);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const uint2 lo4 = lds_read_tr16(vrow + 16 * db);
+            const uint2 hi4 = lds_read_tr16(vrow + 16 * kVPitch + 16 * db);
+            const bf16x8 vf = u32x4_as_bf16x8(u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
+            acc[db] = mfma16x16x32(vf, ph, acc[db]);
+            acc[db] = mfma16x16x32(vf, pl, acc[db]);
+        }
+    }
+    ls += __shfl_xor(ls, 16, 64);
+    ls += __shfl_xor(ls, 32, 64);
+    if (qrow >= a.Sq) return;
+    const float inv = ls > 0.f ? 1.f / ls : 0.f;
+    // O^T lane layout: head dims 16db + 4g + i of query qrow
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        const f32x4 o = acc[db] * inv;
+        const int64_t off = b * a.o_sb + h * a.o_sh + qrow * a.o_ss + 16 * db + 4 * g;
+        if (a.out_f32) {
+            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.o) + off) = o;
+        } else {
+            uint2 pk2;
+            pk2.x = pack_bf16x2(o[0], o[1]);
+            pk2.y = pack_bf16x2(o[2], o[3]);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.o) + off) = pk2;
+        }
+    }
+}
+
 }  // namespace sfk
 
 // ---------------------------------------------------------------------------
@@ -534,11 +690,13 @@ extern "C" void sf_attn_desc_init_bhsd(sf_attn_desc* d, int32_t B, int32_t H, in
 
 extern "C" int32_t sf_attn_num_splits(const sf_attn_desc* d) {
     if (validate(d) != SF_OK) return 0;
+    if (d->Sk <= sfk::kShortMaxKeys && d->num_splits <= 1) return 1;
     return choose_splits(d);
 }
 
 extern "C" size_t sf_attn_workspace_bytes(const sf_attn_desc* d) {
     if (validate(d) != SF_OK) return 0;
+    if (d->Sk <= sfk::kShortMaxKeys && d->num_splits <= 1) return 0;
     const int ns = choose_splits(d);
     if (ns <= 1) return 0;
     const size_t rows = (size_t)d->B * d->H * ns * d->Sq;
@@ -554,7 +712,8 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return SF_EINVAL;
     if (d->B > 65535 || d->H > 65535) return SF_ENOTSUP;
 
-    const int ns = choose_splits(d);
+    const bool short_keys = d->Sk <= sfk::kShortMaxKeys && d->num_splits <= 1;
+    const int ns = short_keys ? 1 : choose_splits(d);
     const int nqc = query_chunks(d);
     sfk::AttnArgs a{};
     a.q = static_cast<const uint16_t*>(q);
@@ -582,6 +741,15 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     if ((long)ns * nqc > 0x7fffffffL) return SF_ENOTSUP;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (short_keys) {
+        const dim3 grid((d->Sq + 15) / 16, d->H, d->B);
+        const int kb = ((d->Sk + 31) / 32) * 2;
+        if (kb <= 2) hipLaunchKernelGGL(sfk::attn_short_kernel<2>, grid, dim3(64), 0, s, a);
+        else if (kb <= 4) hipLaunchKernelGGL(sfk::attn_short_kernel<4>, grid, dim3(64), 0, s, a);
+        else if (kb <= 6) hipLaunchKernelGGL(sfk::attn_short_kernel<6>, grid, dim3(64), 0, s, a);
+        else hipLaunchKernelGGL(sfk::attn_short_kernel<8>, grid, dim3(64), 0, s, a);
+        return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+    }
     hipLaunchKernelGGL(sfk::attn_split_kernel, dim3(ns * nqc, d->H, d->B), dim3(sfk::kThreads), 0,
                        s, a);
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;

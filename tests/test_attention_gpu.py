@@ -203,3 +203,45 @@ def test_workspace_reuse_across_calls():
     torch.cuda.synchronize()
     assert_close_bf16(ref.cpu().numpy(), O.attention_f32(*(x.float().cpu().numpy() for x in (q, k, v))),
                       "reuse")
+
+
+@pytest.mark.parametrize("Sq,Sk,causal,vl", [(67, 67, False, None), (67, 128, False, [128, 5, 0]),
+                                            (200, 100, True, None), (16, 2, False, [1, 2, 2]),
+                                            (1, 97, False, [97, 96, 33]), (67, 64, True, [64, 40, 1])])
+def test_short_key_path(Sq, Sk, causal, vl):
+    """Sk <= 128 runs the one-wave short-key kernel (single-pass softmax, V
+    read through LDS transpose loads); it must agree with the oracle and with
+    the split kernel (forced by num_splits=2) on the same inputs."""
+    B, H = 3, 2
+    q, k, v = rounded(241, (B, H, Sq, 64)), rounded(242, (B, H, Sk, 64)), rounded(243, (B, H, Sk, 64))
+    kw = dict(is_causal=causal)
+    vld = None
+    if vl is not None:
+        vld = np.asarray(vl, np.int32)
+        kw["valid_len"] = to_dev(vld, torch.int32)
+    got = run(q, k, v, **kw)
+    ref = O.attention_f32(q, k, v, causal=causal, valid_len=vld)
+    assert_close_bf16(got, ref, f"short {Sq}x{Sk} causal={causal} vl={vl}")
+    split = run(q, k, v, num_splits=2, **kw)
+    assert np.abs(split - got).max() < 1e-4
+    if vl is not None and 0 in vl:
+        assert np.all(got[list(vl).index(0)] == 0)
+
+
+def test_short_key_path_strided_output_and_graph():
+    q = to_dev(rounded(251, (2, 32, 67, 64)))
+    k, v = to_dev(rounded(252, (2, 32, 67, 64))), to_dev(rounded(253, (2, 32, 67, 64)))
+    bhsd = attention(q, k, v, out_dtype=torch.bfloat16)
+    seq = torch.empty(2, 67, 32, 64, device=DEV, dtype=torch.bfloat16)   # [B, S, H*64] as the block uses
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            attention(q, k, v, out=seq.permute(0, 2, 1, 3))
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(3):
+        seq.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(seq.permute(0, 2, 1, 3), bhsd), f"replay {i}"
