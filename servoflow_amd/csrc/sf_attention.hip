@@ -10,11 +10,14 @@
 // cross-attention; attn_short_kernel below serves key sets of <= 128, the
 // 67 x 67 self-attention):
 //   * grid = (splits x query-chunks, H, B); a workgroup of 4 waves owns one
-//     (b, h, query chunk of 80 rows, key split).  Splitting the keys
-//     (flash-decoding) is what fills 256 CUs when B*H = 32.
-//   * K/V tiles of 128 keys are streamed HBM -> VGPR -> LDS with 16-byte
-//     coalesced loads, double-buffered so the next tile's loads are in
-//     flight while the current tile is contracted.
+//     (b, h, query chunk of 80 rows, key split), two workgroups per CU.
+//     Splitting the keys (flash-decoding) is what fills 256 CUs when
+//     B*H = 32.
+//   * K/V tiles of 128 keys are streamed HBM -> LDS by buffer_load ... lds
+//     (16-byte, coalesced, no VGPR staging) into a two-stage ring, so the
+//     next tile's loads are in flight while the current one is contracted;
+//     V stays in its [key][d] layout and is read as V^T with
+//     ds_read_b64_tr_b16.
 //   * Each wave contracts 32 keys of the tile against all 80 query rows with
 //     v_mfma_f32_16x16x32_bf16: S^T = K.Q^T, then O^T += V^T.P^T.  The S^T
 //     accumulator layout (lane = query, 4 consecutive keys per lane) is
@@ -35,8 +38,6 @@
 namespace sfk {
 
 constexpr int kKT = 128;    // keys per tile per workgroup (4 waves x 32)
-constexpr int kRow = 72;    // K tile pitch in bf16 elements (144 B, bank-skewed)
-constexpr int kVRow = 136;  // transposed V tile pitch in bf16 elements (272 B)
 constexpr int kD = 64;      // head dim this kernel family is built for
 constexpr int kQB = 5;      // 16-row query blocks per workgroup (80 rows >= 67)
 constexpr int kThreads = 256;
@@ -72,277 +73,43 @@ __device__ __forceinline__ void store_out(const AttnArgs& a, int b, int h, int q
     }
 }
 
-// One (b, h, query chunk, key split) per workgroup.
-//
-// LDS: K tile row-major [128 keys][72] (144-byte pitch), V tile transposed
-// [64 d][136] (272-byte pitch), so both MFMA operands are read with 16- and
-// 8-byte loads, plus the resident Q tile [80][72]: 47,360 bytes, small
-// enough for two workgroups per CU.  The next tile is prefetched into VGPRs
-// while the current one is contracted.
-__global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(const AttnArgs a) {
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element
+// j%4 of the 8-byte rows addressed by lanes 4k + j/4, k = 0..3.  Lane i of a
+// group addressing V[k0 + i/4][d0 + 4(i%4)] therefore gives lane j the four
+// keys k0..k0+3 of head dim d0 + j: a V^T operand fragment read from V in
+// its natural [key][d] layout.
+typedef short v4i16 __attribute__((__vector_size__(8)));
+
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+    const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(p));
+    return __builtin_bit_cast(uint2, v);
+}
+
+// Shared epilogue of the split kernels: row sums, then the four waves'
+// (m, l, O) merge through LDS (xo_base: >= 43.5 KB of LDS no longer in use),
+// then the normalised output (one split) or the split's partials.
+__device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo_base,
+                                                    f32x4 (&acc)[kQB][4], float (&m)[kQB],
+                                                    float (&l)[kQB], int w, int g, int r, int lane,
+                                                    int b, int h, int q0, int split, int nsplit,
+                                                    bool l_per_lane = true) {
     constexpr int QR = 16 * kQB;
-    constexpr int kKElems = kKT * kRow;          // 9216
-    constexpr int kVElems = kD * kVRow;          // 8704
-    constexpr int kBufElems = kKElems + kVElems;
-    constexpr int kQElems = QR * kRow;           // 5760
-    __shared__ __attribute__((aligned(16))) uint16_t lds[kBufElems + kQElems];
-    uint16_t* const qs = lds + kBufElems;        // Q tile [80][72], resident
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int w = tid >> 6;
-    const int g = lane >> 4;
-    const int r = lane & 15;
-    const int nsplit = a.nsplit;
-    const int split = blockIdx.x % nsplit;
-    const int qc = blockIdx.x / nsplit;
-    const int h = blockIdx.y;
-    const int b = blockIdx.z;
-    const int q0 = qc * QR;
-
-    int valid = a.Sk;
-    if (a.valid_len) {
-        const int vl = a.valid_len[b];
-        valid = vl < 0 ? 0 : (vl > a.Sk ? a.Sk : vl);
-    }
-    // Key range of this split: equal shares of the VALID keys, 32-key granular.
-    int per = (valid + nsplit - 1) / nsplit;
-    per = (per + 31) & ~31;
-    const int kbeg = split * per;
-    int kend = min(valid, kbeg + per);
-    if (a.causal) kend = min(kend, min(a.Sq, q0 + QR));
-    const int ntiles = kend > kbeg ? (kend - kbeg + kKT - 1) / kKT : 0;
-
-    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
-
-    // Buffer resources: rows outside [0, Sq) / [0, kend) read as zeros from
-    // the hardware's range check, so loads need no branches or clamping.
-    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qp, (uint32_t)(a.Sq * a.q_ss * 2));
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, (uint32_t)(kend * a.k_ss * 2));
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vp, (uint32_t)(kend * a.v_ss * 2));
-
-    // Global -> register prefetch of one tile.  K: 1024 16-byte chunks, four
-    // per thread, 8 threads per 128-byte key row.  V: thread (kg = tid/8,
-    // c = tid%8) loads keys 4kg..4kg+3, head dims 8c..8c+7, so it can write
-    // four consecutive keys of one head dim into the transposed tile.
-    u32x4 pk[4], pv[4];
-    const int vkg = tid >> 3;
-    const int vc = tid & 7;
-    auto gload = [&](int kt) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = tid + kThreads * j;
-            const int key = kt + (c >> 3);
-            pk[j] = buffer_load16(krs, (uint32_t)((key * a.k_ss + (c & 7) * 8) * 2));
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int key = kt + 4 * vkg + j;
-            pv[j] = buffer_load16(vrs, (uint32_t)((key * a.v_ss + vc * 8) * 2));
-        }
-    };
-    auto lstore = [&]() {
-        uint16_t* kl = lds;
-        uint16_t* vt = kl + kKElems;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = tid + kThreads * j;
-            *reinterpret_cast<u32x4*>(kl + (c >> 3) * kRow + (c & 7) * 8) = pk[j];
-        }
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const uint32_t x0 = pv[0][p], x1 = pv[1][p], x2 = pv[2][p], x3 = pv[3][p];
-            uint2 ev, od;
-            ev.x = (x0 & 0xffffu) | (x1 << 16);
-            ev.y = (x2 & 0xffffu) | (x3 << 16);
-            od.x = (x0 >> 16) | (x1 & 0xffff0000u);
-            od.y = (x2 >> 16) | (x3 & 0xffff0000u);
-            const int d = vc * 8 + 2 * p;
-            *reinterpret_cast<uint2*>(vt + d * kVRow + 4 * vkg) = ev;
-            *reinterpret_cast<uint2*>(vt + (d + 1) * kVRow + 4 * vkg) = od;
-        }
-    };
-
-    // Q tile -> LDS (rows >= Sq read as zeros).  Its loads overlap tile 0's.
-    u32x4 pq[3];
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int c = tid + kThreads * j;          // 640 chunks of 16 bytes
-        const int row = c >> 3;
-        pq[j] = c < QR * 8 ? buffer_load16(qrs, (uint32_t)(((q0 + row) * a.q_ss + (c & 7) * 8) * 2))
-                           : u32x4{0u, 0u, 0u, 0u};
-    }
-    if (ntiles > 0) gload(kbeg);
-    // Retire Q and tile 0 here so the loop's prefetch loads are only ever
-    // waited for where they are stored to LDS.
-    __builtin_amdgcn_s_waitcnt(0);
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int c = tid + kThreads * j;
-        if (c < QR * 8) *reinterpret_cast<u32x4*>(qs + (c >> 3) * kRow + (c & 7) * 8) = pq[j];
-    }
-    if (ntiles > 0) lstore();
-    __syncthreads();
-
-    f32x4 acc[kQB][4];   // O^T blocks: lane holds d = 16db + 4g + i, q = 16qb + r
-    float m[kQB], l[kQB];
-#pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
-        m[qb] = -INFINITY;
-        l[qb] = 0.f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) acc[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    for (int t = 0; t < ntiles; ++t) {
-        const int kt = kbeg + t * kKT;
-        if (t + 1 < ntiles) gload(kt + kKT);
-
-        const uint16_t* kl = lds;
-        const uint16_t* vt = kl + kKElems;
-        const int wkey = 32 * w;   // this wave's first key inside the tile
-
-        // ---- Operand fragments shared by the five query blocks: K rows of
-        //      the wave's two 16-key blocks (A of S^T = K.Q^T) and V^T rows
-        //      (A of O^T += V^T.P^T) holding the 8 keys {4g..4g+3,
-        //      16+4g..16+4g+3}, the key order the S^T accumulator gives P^T.
-        bf16x8 kf[2][2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const uint16_t* krow = kl + (wkey + 16 * kb + r) * kRow + 8 * g;
-            kf[kb][0] = load_bf16x8(krow);
-            kf[kb][1] = load_bf16x8(krow + 32);
-        }
-        bf16x8 vf[4];
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const uint16_t* vrow = vt + (16 * db + r) * kVRow + wkey + 4 * g;
-            const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow);
-            const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + 16);
-            vf[db] = u32x4_as_bf16x8(u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
-        }
-        const bool need_mask = a.causal || kt + kKT > kend;
-
-        // ---- S^T for all five query blocks (lane: query 16qb + r, keys
-        //      16kb + 4g + i), raw (unscaled) scores.  Q is the B operand:
-        //      row 16qb + r, head dims [32dc + 8g, +8).  Each phase below is
-        //      straight-line over the five blocks so their MFMA, shuffle and
-        //      exp latencies overlap.
-        f32x4 s[kQB][2];
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
-            const uint16_t* qrow_l = qs + (16 * qb + r) * kRow + 8 * g;
-            const bf16x8 qf0 = load_bf16x8(qrow_l);
-            const bf16x8 qf1 = load_bf16x8(qrow_l + 32);
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                z = mfma16x16x32(kf[kb][0], qf0, z);
-                s[qb][kb] = mfma16x16x32(kf[kb][1], qf1, z);
-            }
-        }
-        // Keys past the split end (and future keys when causal) drop out.
-        if (need_mask) {
-#pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
-                const int qrow = q0 + 16 * qb + r;
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int key = kt + wkey + 16 * kb + 4 * g + i;
-                        const bool dead = key >= kend || (a.causal && key > qrow);
-                        s[qb][kb][i] = dead ? -INFINITY : s[qb][kb][i];
-                    }
-                }
-            }
-        }
-        // Row maxima in log2 units (scale_log2 > 0, so the max of the raw
-        // scores scales): 8 keys per lane, then the 4 lane groups of a query.
-        float mx[kQB];
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
-            const f32x4 u = s[qb][0], v = s[qb][1];
-            mx[qb] = fmaxf(fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3])),
-                           fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
-        }
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) mx[qb] = fmaxf(mx[qb], __shfl_xor(mx[qb], 16, 64));
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb)
-            mx[qb] = fmaxf(mx[qb], __shfl_xor(mx[qb], 32, 64)) * a.scale_log2;
-        // Lazy rescale (one vote per tile): keep each row's reference max
-        // unless it grew by more than 2^8; P = exp2(x - m) then stays <= 256.
-        bool grow = false;
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) grow |= mx[qb] > m[qb] + 8.f;
-        if (__any(grow)) {
-#pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
-                const float mnew = fmaxf(m[qb], mx[qb]);
-                const float alpha = fast_exp2(m[qb] - (mnew == -INFINITY ? 0.f : mnew));
-                m[qb] = mnew;
-                l[qb] *= alpha;
-#pragma unroll
-                for (int db = 0; db < 4; ++db) acc[qb][db] *= alpha;
-            }
-        }
-        // P = exp2(s * scale_log2 - m) as a bf16 (hi, lo) pair: hi is the
-        // truncated top half of P, lo the bf16 of the exact remainder.  Then
-        // O^T += V^T . P^T for both halves.
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
-            const float nmuse = m[qb] == -INFINITY ? 0.f : -m[qb];
-            float ls = l[qb];
-            uint32_t pb[8], lb[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float p = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nmuse));
-                ls += p;
-                pb[j] = __float_as_uint(p);
-                lb[j] = __float_as_uint(p - __uint_as_float(pb[j] & 0xffff0000u));
-            }
-            l[qb] = ls;
-            // perm selector 0x07060302: high halves of (second, first).
-            const u32x4 phw = {__builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u),
-                               __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
-                               __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u),
-                               __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)};
-            const u32x4 plw = {__builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u),
-                               __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u),
-                               __builtin_amdgcn_perm(lb[5], lb[4], 0x07060302u),
-                               __builtin_amdgcn_perm(lb[7], lb[6], 0x07060302u)};
-            const bf16x8 ph8 = u32x4_as_bf16x8(phw);
-            const bf16x8 pl8 = u32x4_as_bf16x8(plw);
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                acc[qb][db] = mfma16x16x32(vf[db], ph8, acc[qb][db]);
-                acc[qb][db] = mfma16x16x32(vf[db], pl8, acc[qb][db]);
-            }
-        }
-
-        if (t + 1 < ntiles) {
-            __syncthreads();   // every wave is done reading the tile
-            lstore();
-        }
-        __syncthreads();
-    }
-
     // ---- Row sums: each lane summed its own 8 keys per tile; add the four
     //      lane groups that share a query.
+    if (l_per_lane) {
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
-        l[qb] += __shfl_xor(l[qb], 16, 64);
-        l[qb] += __shfl_xor(l[qb], 32, 64);
+        for (int qb = 0; qb < kQB; ++qb) {
+            l[qb] += __shfl_xor(l[qb], 16, 64);
+            l[qb] += __shfl_xor(l[qb], 32, 64);
+        }
     }
 
     // ---- Merge the four waves' (m, l, O).  Wave w owns head dims
     //      [16w, 16w + 16); the other waves hand it their partial sums for
     //      that d-block through LDS in two rounds (owners 0,1 then 2,3), so
     //      each output element is summed once and stored as a 4-vector.
-    float* xo = reinterpret_cast<float*>(lds);          // [4 w][2 slot][kQB][64 lanes][4]
+    float* xo = xo_base;                                 // [4 w][2 slot][kQB][64 lanes][4]
     float* sm = xo + 4 * 2 * kQB * 64 * 4;               // [4][QR]
     float* sl = sm + 4 * QR;                             // [4][QR]
     if (g == 0) {
@@ -420,7 +187,258 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(const AttnArgs 
         }
         if (round == 0) __syncthreads();
     }
+}
 
+// ---------------------------------------------------------------------------
+// Split kernel, ring-pipelined (the cross-attention path).
+//
+// One (b, h, query chunk, key split) per workgroup of 4 waves, two
+// workgroups per CU (two waves per SIMD: the softmax is VALU-issue bound and
+// one wave alone issues VALU at half the SIMD's rate); the splits are chosen
+// so B*H*splits ~ 512.  K and V tiles of 128 keys go HBM -> LDS directly
+// (buffer_load ... lds, no VGPR staging) into a 2-stage ring per workgroup,
+// a tile's loads issued as soon as its stage is free.  Rows
+// sit in LDS in their natural [key][64] layout with the 16-byte chunks of
+// key row k XOR-swizzled by (k >> 1) & 7, which makes both the K fragment
+// reads (16 rows x 16 B) and the V^T transpose reads (4 rows x 8 B per
+// 16-lane group) bank-conflict free.  Q fragments live in registers.  The
+// arithmetic (S^T = K.Q^T, lazy-rescaled log2 softmax, P as a bf16 hi/lo
+// pair, O^T += V^T.P^T, 4-wave LDS merge) is the split kernel's, except that
+// the row sums come from the MFMA pipe: a constant V^T fragment whose first
+// row is all ones turns P^T into l, so the VALU does no per-element adds and
+// l sums exactly the (hi + lo) weights the numerator uses.
+// ---------------------------------------------------------------------------
+constexpr int kRingStages = 2;
+constexpr int kTileBytes = kKT * kD * 2;          // 16 KB per K (or V) tile
+constexpr int kStageBytes = 2 * kTileBytes;       // K then V
+
+__device__ __forceinline__ int ring_swz(int key) { return (key >> 1) & 7; }
+
+// Wait until at most n of this wave's vector-memory ops are outstanding,
+// then barrier.  n is 0, 8, 16 or 24 (tiles still in flight x 8).
+__device__ __forceinline__ void ring_wait_barrier(int n) {
+    if (n >= 24) asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
+    else if (n >= 16) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    else if (n >= 8) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a) {
+    constexpr int QR = 16 * kQB;
+    __shared__ __attribute__((aligned(16))) char ring[kRingStages * kStageBytes];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int g = lane >> 4;
+    const int r = lane & 15;
+    const int nsplit = a.nsplit;
+    const int split = blockIdx.x % nsplit;
+    const int qc = blockIdx.x / nsplit;
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
+    const int q0 = qc * QR;
+
+    int valid = a.Sk;
+    if (a.valid_len) {
+        const int vl = a.valid_len[b];
+        valid = vl < 0 ? 0 : (vl > a.Sk ? a.Sk : vl);
+    }
+    // Key range of this split: equal shares of the VALID keys, 32-key granular.
+    int per = (valid + nsplit - 1) / nsplit;
+    per = (per + 31) & ~31;
+    const int kbeg = split * per;
+    int kend = min(valid, kbeg + per);
+    if (a.causal) kend = min(kend, min(a.Sq, q0 + QR));
+    const int ntiles = kend > kbeg ? (kend - kbeg + kKT - 1) / kKT : 0;
+
+    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qp, (uint32_t)(a.Sq * a.q_ss * 2));
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, (uint32_t)(max(kend, 0) * a.k_ss * 2));
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vp, (uint32_t)(max(kend, 0) * a.v_ss * 2));
+
+    // Q fragments (B operand of S^T = K.Q^T): row 16qb + r, dims 32hh + 8g..
+    bf16x8 qf[kQB][2];
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+            qf[qb][hh] = __builtin_bit_cast(
+                bf16x8, buffer_load16(qrs, (uint32_t)(((q0 + 16 * qb + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
+
+    // DMA of one tile into a stage: wave w, op j fills LDS chunks
+    // (4w + j) * 64 + lane = key * 8 + slot of K (and of V), loading global
+    // chunk slot ^ swz(key) of that key.  Keys past kend read as zeros.
+    int chunk_key[4], chunk_col[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int p = (4 * w + j) * 64 + lane;
+        chunk_key[j] = p >> 3;
+        chunk_col[j] = ((p & 7) ^ ring_swz(p >> 3)) * 8;
+    }
+    auto issue = [&](int t) {
+        const int kt = kbeg + t * kKT;
+        char* st = ring + (t % kRingStages) * kStageBytes;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t koff = (uint32_t)(((kt + chunk_key[j]) * a.k_ss + chunk_col[j]) * 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                krs, (__attribute__((address_space(3))) void*)(st + (4 * w + j) * 1024), 16, koff, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t voff = (uint32_t)(((kt + chunk_key[j]) * a.v_ss + chunk_col[j]) * 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                vrs, (__attribute__((address_space(3))) void*)(st + kTileBytes + (4 * w + j) * 1024), 16,
+                voff, 0, 0, 0);
+        }
+    };
+    const int first = min(ntiles, kRingStages);
+    for (int t = 0; t < first; ++t) issue(t);
+
+    f32x4 acc[kQB][4];   // O^T blocks: lane holds d = 16db + 4g + i, q = 16qb + r
+    f32x4 accl[kQB];     // row sums: element 0 of lanes 0..15 holds l of query 16qb + r
+    float m[kQB], l[kQB];
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+        m[qb] = -INFINITY;
+        accl[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // A operand whose row 0 is all ones (rows 1..15 zero)
+    const uint32_t one2 = r == 0 ? 0x3f803f80u : 0u;
+    const bf16x8 ones = u32x4_as_bf16x8(u32x4{one2, one2, one2, one2});
+
+    const int wkey = 32 * w;   // this wave's first key inside a tile
+    // per-lane LDS byte offsets inside a stage (swizzled rows)
+    int koffs[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        const int key = wkey + 16 * kb + r;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) koffs[kb][hh] = key * 128 + (((g + 4 * hh) ^ ring_swz(key)) * 16);
+    }
+    int voffs[2][4];   // [key half][db]: V^T transpose-read addresses
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        const int key = wkey + 16 * hf + 4 * g + (r >> 2);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = 16 * db + 4 * (r & 3);
+            voffs[hf][db] = kTileBytes + key * 128 + (((d >> 3) ^ ring_swz(key)) * 16) + (d & 7) * 2;
+        }
+    }
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int kt = kbeg + t * kKT;
+        ring_wait_barrier(8 * min(kRingStages - 1, ntiles - 1 - t));
+        const char* st = ring + (t % kRingStages) * kStageBytes;
+        if (kt + wkey < kend && !(a.causal && kt + wkey > q0 + QR - 1)) {
+            bf16x8 kf[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+                    kf[kb][hh] = *reinterpret_cast<const bf16x8*>(st + koffs[kb][hh]);
+            bf16x8 vf[4];
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const uint2 lo4 = lds_read_tr16(reinterpret_cast<const uint16_t*>(st + voffs[0][db]));
+                const uint2 hi4 = lds_read_tr16(reinterpret_cast<const uint16_t*>(st + voffs[1][db]));
+                vf[db] = u32x4_as_bf16x8(u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
+            }
+            const bool need_mask = a.causal || kt + kKT > kend;
+            f32x4 s[kQB][2];
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    z = mfma16x16x32(kf[kb][0], qf[qb][0], z);
+                    s[qb][kb] = mfma16x16x32(kf[kb][1], qf[qb][1], z);
+                }
+            }
+            if (need_mask) {
+#pragma unroll
+                for (int qb = 0; qb < kQB; ++qb) {
+                    const int qrow = q0 + 16 * qb + r;
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int key = kt + wkey + 16 * kb + 4 * g + i;
+                            const bool dead = key >= kend || (a.causal && key > qrow);
+                            s[qb][kb][i] = dead ? -INFINITY : s[qb][kb][i];
+                        }
+                    }
+                }
+            }
+            float mx[kQB];
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+                const f32x4 u = s[qb][0], v = s[qb][1];
+                mx[qb] = fmaxf(fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3])),
+                               fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+            }
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) mx[qb] = fmaxf(mx[qb], __shfl_xor(mx[qb], 16, 64));
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb)
+                mx[qb] = fmaxf(mx[qb], __shfl_xor(mx[qb], 32, 64)) * a.scale_log2;
+            bool grow = false;
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) grow |= mx[qb] > m[qb] + 8.f;
+            if (__any(grow)) {
+#pragma unroll
+                for (int qb = 0; qb < kQB; ++qb) {
+                    const float mnew = fmaxf(m[qb], mx[qb]);
+                    const float alpha = fast_exp2(m[qb] - (mnew == -INFINITY ? 0.f : mnew));
+                    m[qb] = mnew;
+                    accl[qb] *= alpha;
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) acc[qb][db] *= alpha;
+                }
+            }
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+                const float nmuse = m[qb] == -INFINITY ? 0.f : -m[qb];
+                uint32_t pb[8], lb[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nmuse));
+                    pb[j] = __float_as_uint(p);
+                    lb[j] = __float_as_uint(p - __uint_as_float(pb[j] & 0xffff0000u));
+                }
+                const u32x4 phw = {__builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u),
+                                   __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
+                                   __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u),
+                                   __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)};
+                const u32x4 plw = {__builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u),
+                                   __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u),
+                                   __builtin_amdgcn_perm(lb[5], lb[4], 0x07060302u),
+                                   __builtin_amdgcn_perm(lb[7], lb[6], 0x07060302u)};
+                const bf16x8 ph8 = u32x4_as_bf16x8(phw);
+                const bf16x8 pl8 = u32x4_as_bf16x8(plw);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    acc[qb][db] = mfma16x16x32(vf[db], ph8, acc[qb][db]);
+                    acc[qb][db] = mfma16x16x32(vf[db], pl8, acc[qb][db]);
+                }
+                accl[qb] = mfma16x16x32(ones, ph8, accl[qb]);
+                accl[qb] = mfma16x16x32(ones, pl8, accl[qb]);
+            }
+        }   // live keys
+        // every wave is done with this stage before it is refilled
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (t + kRingStages < ntiles) issue(t + kRingStages);
+    }
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) l[qb] = __shfl(accl[qb][0], r, 64);
+    attn_split_epilogue(a, reinterpret_cast<float*>(ring), acc, m, l, w, g, r, lane, b, h, q0,
+                        split, nsplit, false);
 }
 
 // Log-sum-exp merge of the split partials.  One wave per output row
@@ -435,12 +453,19 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     if (q >= a.Sq) return;
     const int ns = a.nsplit;
     const size_t row0 = ((size_t)b * a.H + h) * ns * (size_t)a.Sq + q;   // split 0's row
+    // every load first: this lane's split (m, l) and head dim `lane` of the
+    // first kMergeBatch splits' partial outputs
+    constexpr int kMergeBatch = 16;
     float ms = -INFINITY, ls = 0.f;
     if (lane < ns) {
         const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (row0 + (size_t)lane * a.Sq) * 2);
         ms = ml.x;
         ls = ml.y;
     }
+    float v0[kMergeBatch];
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j)
+        v0[j] = a.part_o[(row0 + (size_t)min(j, ns - 1) * a.Sq) * kD + lane];
     float M = ms;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
@@ -451,7 +476,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
     wgt *= L > 0.f ? 1.f / L : 0.f;
     float o = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j)
+        if (j < ns) o += __shfl(wgt, j, 64) * v0[j];
+    for (int s0 = kMergeBatch; s0 < ns; s0 += 8) {
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
@@ -479,14 +507,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kShortMaxKeys = 128;
 constexpr int kVPitch = 80;   // LDS row pitch of V (bf16): 160 B keeps the four rows of a read apart
-
-typedef short v4i16 __attribute__((__vector_size__(8)));
-
-__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
-    const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) v4i16*)(p));
-    return __builtin_bit_cast(uint2, v);
-}
 
 template <int KB>   // 16-key blocks covering Sk (even, <= 8)
 __global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
@@ -628,9 +648,9 @@ using sfk::kMaxSplits;
 
 int query_chunks(const sf_attn_desc* d) { return (d->Sq + 16 * sfk::kQB - 1) / (16 * sfk::kQB); }
 
-// MI355X has 256 CUs and the split kernel fits two workgroups per CU (two
-// waves per SIMD).  Splits are chosen so the grid is one round of
-// workgroups, each split covering at least 256 keys.
+// MI355X has 256 CUs and the ring kernel runs two workgroups per CU (64 KB
+// LDS ring each).  Splits are chosen so the grid is one round of
+// workgroups, each split covering at least one 128-key tile.
 constexpr long kNumCUs = 256;
 constexpr long kWgPerCU = 2;
 
@@ -639,7 +659,7 @@ int choose_splits(const sf_attn_desc* d) {
     const long base = (long)d->B * d->H * query_chunks(d);
     if (base <= 0) return 1;
     long ns = kNumCUs * kWgPerCU / base;
-    const long cap = d->Sk / 256;
+    const long cap = d->Sk / 128;
     if (ns > cap) ns = cap;
     if (ns < 1) ns = 1;
     if (ns > kMaxSplits) ns = kMaxSplits;
@@ -750,7 +770,7 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         else hipLaunchKernelGGL(sfk::attn_short_kernel<8>, grid, dim3(64), 0, s, a);
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
     }
-    hipLaunchKernelGGL(sfk::attn_split_kernel, dim3(ns * nqc, d->H, d->B), dim3(sfk::kThreads), 0,
+    hipLaunchKernelGGL(sfk::attn_ring_kernel, dim3(ns * nqc, d->H, d->B), dim3(sfk::kThreads), 0,
                        s, a);
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     if (ns > 1) {
