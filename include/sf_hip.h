@@ -67,6 +67,14 @@ typedef enum sf_dtype {
  * kv_valid_len: NULL (every key valid) or a DEVICE pointer to B int32
  * lengths; keys [valid_len[b], Sk) of batch b are ignored.  Lengths are
  * clamped to [0, Sk] on the device; a row with no valid key yields zeros.
+ * kv_mask: NULL or a DEVICE pointer to a boolean key-padding mask, one byte
+ * per key (nonzero = attend), batch b's row at kv_mask + b * kv_mask_stride
+ * bytes (4-byte aligned, stride a multiple of 4, each row readable for Sk
+ * rounded up to 4 bytes; bytes past Sk are ignored); combined with
+ * kv_valid_len by AND.  This is the [B, Sk] key-padding form the RDT block
+ * header documents (include/servoflow/models/rdt1b/dit_block.h:141) and the
+ * mask argument of IBackend::attention (backend.h:104) that the reference
+ * implementations ignore.
  * num_splits: 0 chooses the split-K factor automatically; n > 0 forces n
  * (at most 64).
  * scale must be >= 0 (SF_ENOTSUP otherwise).
@@ -86,6 +94,8 @@ typedef struct sf_attn_desc {
     int64_t k_stride[3];
     int64_t v_stride[3];
     int64_t o_stride[3];
+    const uint8_t* kv_mask;
+    int64_t kv_mask_stride;
 } sf_attn_desc;
 
 /* Fills a descriptor for contiguous [B,H,S,D] tensors (the layout

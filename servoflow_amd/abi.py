@@ -45,6 +45,8 @@ class AttnDesc(ctypes.Structure):
         ("k_stride", ctypes.c_int64 * 3),
         ("v_stride", ctypes.c_int64 * 3),
         ("o_stride", ctypes.c_int64 * 3),
+        ("kv_mask", ctypes.c_void_p),
+        ("kv_mask_stride", ctypes.c_int64),
     ]
 
 

@@ -23,7 +23,7 @@ def _strides3(t: torch.Tensor):
     return (t.stride(0), t.stride(1), t.stride(2))
 
 
-def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_splits=0):
+def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_splits=0, kv_mask=None):
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     if k.shape != (B, H, Sk, D) or v.shape != (B, H, Sk, D) or out.shape != (B, H, Sq, D):
@@ -40,6 +40,12 @@ def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_spli
         if valid_len.dtype != torch.int32 or valid_len.numel() != B or not valid_len.is_cuda:
             raise ValueError("valid_len must be a device int32 tensor of B elements")
         d.kv_valid_len = valid_len.data_ptr()
+    if kv_mask is not None:
+        if kv_mask.dtype not in (torch.bool, torch.uint8) or kv_mask.dim() != 2 or \
+                kv_mask.shape[0] != B or kv_mask.shape[1] != Sk or kv_mask.stride(1) != 1 or not kv_mask.is_cuda:
+            raise ValueError("kv_mask must be a device bool/uint8 tensor [B, Sk] with contiguous rows")
+        d.kv_mask = kv_mask.data_ptr()
+        d.kv_mask_stride = kv_mask.stride(0)
     for name, t in (("q_stride", q), ("k_stride", k), ("v_stride", v), ("o_stride", out)):
         getattr(d, name)[:] = _strides3(t)
     return d
@@ -50,16 +56,17 @@ def workspace_bytes(desc) -> int:
 
 
 def attention(q, k, v, out=None, scale=0.0, is_causal=False, valid_len=None, num_splits=0,
-              out_dtype=None, workspace=None, stream=None):
-    """Runs sf_attn_fwd on torch's current stream (or `stream`) and returns `out`."""
+              out_dtype=None, workspace=None, stream=None, kv_mask=None):
+    """Runs sf_attn_fwd on torch's current stream (or `stream`) and returns `out`.
+    kv_mask: optional device bool [B, Sk] key-padding mask (True = attend);
+    its rows must be readable for Sk rounded up to 4 bytes."""
     if out is None:
         od = out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=od, device=q.device)
-    desc = make_desc(q, k, v, out, scale, is_causal, valid_len, num_splits)
+    desc = make_desc(q, k, v, out, scale, is_causal, valid_len, num_splits, kv_mask)
     need = workspace_bytes(desc)
     if need and workspace is None:
-        # Zero-filled once: the split-K tickets at its head must start at 0.
-        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)   # needs no init
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_n = workspace.numel() * workspace.element_size() if workspace is not None else 0
     s = stream if stream is not None else torch.cuda.current_stream(q.device)

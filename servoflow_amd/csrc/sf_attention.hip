@@ -51,6 +51,8 @@ struct AttnArgs {
     float* part_o;    // [B*H][nsplit][Sq][64] unnormalised outputs
     float* part_ml;   // [B*H][nsplit][Sq][2]  (running max in log2 units, sum)
     const int32_t* valid_len;
+    const uint8_t* kv_mask;   // [B][kv_mask_stride] bytes, nonzero = attend
+    int64_t kv_mask_stride;
     int64_t q_sb, q_sh, q_ss;
     int64_t k_sb, k_sh, k_ss;
     int64_t v_sb, v_sh, v_ss;
@@ -214,6 +216,13 @@ constexpr int kStageBytes = 2 * kTileBytes;       // K then V
 
 __device__ __forceinline__ int ring_swz(int key) { return (key >> 1) & 7; }
 
+// Key-padding mask bytes of keys k..k+3 (k a multiple of 4) as a 32-bit
+// word.  The buffer range is Sk rounded up to 4 bytes: words past it read as
+// 0, and bytes of keys >= Sk are never used (those keys are out of range).
+__device__ __forceinline__ uint32_t mask_word(__amdgpu_buffer_rsrc_t mrs, int key) {
+    return __builtin_amdgcn_raw_buffer_load_b32(mrs, (uint32_t)key, 0, 0);
+}
+
 // Wait until at most n of this wave's vector-memory ops are outstanding,
 // then barrier.  n is 0, 8, 16 or 24 (tiles still in flight x 8).
 __device__ __forceinline__ void ring_wait_barrier(int n) {
@@ -258,6 +267,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a
     const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qp, (uint32_t)(a.Sq * a.q_ss * 2));
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, (uint32_t)(max(kend, 0) * a.k_ss * 2));
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vp, (uint32_t)(max(kend, 0) * a.v_ss * 2));
+    const __amdgpu_buffer_rsrc_t mrs =
+        make_rsrc(a.kv_mask ? static_cast<const void*>(a.kv_mask + b * a.kv_mask_stride) : static_cast<const void*>(a.q),
+                  a.kv_mask ? (uint32_t)((a.Sk + 3) & ~3) : 0u);
 
     // Q fragments (B operand of S^T = K.Q^T): row 16qb + r, dims 32hh + 8g..
     bf16x8 qf[kQB][2];
@@ -350,7 +362,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a
                 const uint2 hi4 = lds_read_tr16(reinterpret_cast<const uint16_t*>(st + voffs[1][db]));
                 vf[db] = u32x4_as_bf16x8(u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
             }
-            const bool need_mask = a.causal || kt + kKT > kend;
+            const bool need_mask = a.causal || kt + kKT > kend || a.kv_mask;
+            uint32_t mw[2] = {0xffffffffu, 0xffffffffu};
+            if (a.kv_mask) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) mw[kb] = mask_word(mrs, kt + wkey + 16 * kb + 4 * g);
+            }
             f32x4 s[kQB][2];
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb) {
@@ -370,7 +387,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int key = kt + wkey + 16 * kb + 4 * g + i;
-                            const bool dead = key >= kend || (a.causal && key > qrow);
+                            const bool dead = key >= kend || (a.causal && key > qrow) ||
+                                              ((mw[kb] >> (8 * i)) & 0xffu) == 0;
                             s[qb][kb][i] = dead ? -INFINITY : s[qb][kb][i];
                         }
                     }
@@ -531,6 +549,9 @@ __global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
     const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qp, (uint32_t)(a.Sq * a.q_ss * 2));
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, (uint32_t)(valid * a.k_ss * 2));
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vp, (uint32_t)(valid * a.v_ss * 2));
+    const __amdgpu_buffer_rsrc_t mrs =
+        make_rsrc(a.kv_mask ? static_cast<const void*>(a.kv_mask + b * a.kv_mask_stride) : static_cast<const void*>(a.q),
+                  a.kv_mask ? (uint32_t)((a.Sk + 3) & ~3) : 0u);
 
     // every load of the wave up front
     u32x4 vv[2 * KB];
@@ -568,13 +589,16 @@ __global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
         s[kb] = mfma16x16x32(kf[kb][1], qf[1], z);
     }
     const int qrow = q0 + r;
+    uint32_t mw[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) mw[kb] = a.kv_mask ? mask_word(mrs, 16 * kb + 4 * g) : 0xffffffffu;
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int key = 16 * kb + 4 * g + i;
-            const bool dead = key >= valid || (a.causal && key > qrow);
+            const bool dead = key >= valid || (a.causal && key > qrow) || ((mw[kb] >> (8 * i)) & 0xffu) == 0;
             s[kb][i] = dead ? -INFINITY : s[kb][i];
             mx = fmaxf(mx, s[kb][i]);
         }
@@ -683,6 +707,9 @@ int validate(const sf_attn_desc* d) {
     for (int j = 0; j < 3; ++j)
         if (d->o_stride[j] < 0) return SF_EINVAL;
     if (d->Sk == 0 && d->B > 0 && d->H > 0 && d->Sq > 0) return SF_EINVAL;
+    if (d->kv_mask && ((reinterpret_cast<uintptr_t>(d->kv_mask) & 3) || (d->kv_mask_stride & 3) ||
+                       (d->B > 1 && d->kv_mask_stride < d->Sk)))
+        return SF_EINVAL;
     // Per-head byte ranges are addressed with 32-bit buffer offsets.
     if ((int64_t)d->Sq * d->q_stride[2] * 2 > 0x7fffffffLL ||
         (int64_t)d->Sk * d->k_stride[2] * 2 > 0x7fffffffLL ||
@@ -741,6 +768,8 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     a.v = static_cast<const uint16_t*>(v);
     a.o = out;
     a.valid_len = d->kv_valid_len;
+    a.kv_mask = d->kv_mask;
+    a.kv_mask_stride = d->kv_mask_stride;
     a.q_sb = d->q_stride[0]; a.q_sh = d->q_stride[1]; a.q_ss = d->q_stride[2];
     a.k_sb = d->k_stride[0]; a.k_sh = d->k_stride[1]; a.k_ss = d->k_stride[2];
     a.v_sb = d->v_stride[0]; a.v_sh = d->v_stride[1]; a.v_ss = d->v_stride[2];

@@ -245,3 +245,41 @@ def test_short_key_path_strided_output_and_graph():
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(seq.permute(0, 2, 1, 3), bhsd), f"replay {i}"
+
+
+def _masked_reference(q, k, v, mask):
+    """Key-padding mask == attention over the kept keys only (per batch)."""
+    B, H, Sq, D = q.shape
+    ref = np.zeros((B, H, Sq, D), np.float32)
+    for b in range(B):
+        keep = np.flatnonzero(mask[b])
+        if keep.size:
+            ref[b:b + 1] = O.attention_f32(q[b:b + 1], np.ascontiguousarray(k[b:b + 1][:, :, keep]),
+                                           np.ascontiguousarray(v[b:b + 1][:, :, keep]))
+    return ref
+
+
+@pytest.mark.parametrize("Sk", [67, 130, 1000, 4374])
+def test_key_padding_mask(Sk):
+    """A boolean key mask [B, Sk] (the key-padding form of dit_block.h:141)
+    equals attention over the kept keys; combined with valid_len by AND; a
+    row with nothing kept yields zeros."""
+    B, H, Sq = 3, 2, 67
+    q, k, v = rounded(261, (B, H, Sq, 64)), rounded(262, (B, H, Sk, 64)), rounded(263, (B, H, Sk, 64))
+    rng = np.random.default_rng(Sk)
+    mask = rng.random((B, Sk)) < 0.6
+    mask[2] = False
+    stride = (Sk + 3) // 4 * 4
+    md = torch.zeros(B, stride, dtype=torch.uint8, device=DEV)
+    md[:, :Sk] = torch.from_numpy(mask.astype(np.uint8)).to(DEV)
+    got = run(q, k, v, kv_mask=md[:, :Sk])
+    ref = _masked_reference(q, k, v, mask)
+    assert_close_bf16(got, ref, f"key mask Sk={Sk}")
+    assert np.all(got[2] == 0)
+    # AND with valid lengths
+    vl = np.array([Sk // 2, Sk, 5], np.int32)
+    got2 = run(q, k, v, kv_mask=md[:, :Sk], valid_len=to_dev(vl, torch.int32))
+    m2 = mask.copy()
+    for b in range(B):
+        m2[b, vl[b]:] = False
+    assert_close_bf16(got2, _masked_reference(q, k, v, m2), f"key mask & valid Sk={Sk}")
