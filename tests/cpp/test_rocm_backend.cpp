@@ -1,0 +1,342 @@
+// Tests of RocmBackend::attention (servoflow_amd/host/rocm_backend.h), the
+// IBackend::attention-shaped layer (include/servoflow/backend/backend.h:105-110),
+// written in the style of the reference's C++ tests (tests/test_*.cpp): one
+// function per case, inputs from a fixed seed, results checked against the
+// CPU oracle (oracle/sf_oracle.h, test infrastructure only).
+//
+// Tolerances as the Python parity tests: fp32 output within max-abs 2e-2 and
+// sum|d| / sum|ref| 1e-3 of the fp32 oracle on the same bf16-rounded inputs.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "rocm_backend.h"
+extern "C" {
+#include "sf_oracle.h"
+}
+
+using sf_amd::DType;
+using sf_amd::RocmBackend;
+using sf_amd::TensorRef;
+
+namespace {
+
+int g_failed = 0;
+
+#define CHECK(cond, msg)                                                              \
+    do {                                                                              \
+        if (!(cond)) throw std::runtime_error(std::string("check failed: ") + (msg)); \
+    } while (0)
+
+#define HIP_OK(expr) CHECK((expr) == hipSuccess, #expr)
+
+void run_case(const char* name, const std::function<void()>& fn) {
+    try {
+        fn();
+        std::printf("[ OK   ] %s\n", name);
+    } catch (const std::exception& e) {
+        std::printf("[ FAIL ] %s: %s\n", name, e.what());
+        ++g_failed;
+    }
+    std::fflush(stdout);
+}
+
+uint16_t to_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return (uint16_t)(u >> 16);   // inputs are already bf16-rounded: exact
+}
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    explicit DevBuf(size_t bytes) : n(bytes) {
+        if (hipMalloc(&p, bytes) != hipSuccess) throw std::runtime_error("hipMalloc");
+    }
+    ~DevBuf() { (void)hipFree(p); }
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+};
+
+// N(0,1) from the oracle's generator, rounded to bf16; host fp32 copy + device bf16.
+struct Bf16Tensor {
+    std::vector<float> host;
+    DevBuf dev;
+    std::vector<int64_t> shape;
+    Bf16Tensor(uint64_t seed, std::vector<int64_t> shp)
+        : host(numel(shp)), dev(numel(shp) * 2), shape(shp) {
+        sfo_randn(seed, (int64_t)host.size(), 1.f, host.data());
+        sfo_bf16_round_array(host.data(), (int64_t)host.size());
+        std::vector<uint16_t> b(host.size());
+        for (size_t i = 0; i < host.size(); ++i) b[i] = to_bf16(host[i]);
+        if (hipMemcpy(dev.p, b.data(), b.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
+            throw std::runtime_error("hipMemcpy");
+    }
+    static size_t numel(const std::vector<int64_t>& s) {
+        size_t n = 1;
+        for (int64_t x : s) n *= (size_t)x;
+        return n;
+    }
+    TensorRef ref() const { return TensorRef::contiguous(dev.p, DType::BFloat16, shape); }
+};
+
+std::vector<float> download_f32(const DevBuf& b, size_t n) {
+    std::vector<float> h(n);
+    if (hipMemcpy(h.data(), b.p, n * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        throw std::runtime_error("hipMemcpy D2H");
+    return h;
+}
+
+void expect_close(const std::vector<float>& got, const std::vector<float>& ref, const char* what) {
+    CHECK(got.size() == ref.size(), what);
+    double sd = 0, sr = 0, mx = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        CHECK(std::isfinite(got[i]), what);
+        const double d = std::fabs((double)got[i] - ref[i]);
+        sd += d;
+        sr += std::fabs((double)ref[i]);
+        if (d > mx) mx = d;
+    }
+    const double mr = sr > 0 ? sd / sr : sd;
+    if (!(mx <= 2e-2 && mr <= 1e-3)) {
+        char buf[160];
+        std::snprintf(buf, sizeof buf, "%s: max-abs %.3e mean-rel %.3e", what, mx, mr);
+        throw std::runtime_error(buf);
+    }
+}
+
+// The oracle over a subset of keys of one batch element (key-padding mask).
+std::vector<float> oracle_kept(const Bf16Tensor& q, const Bf16Tensor& k, const Bf16Tensor& v,
+                               const std::vector<std::vector<uint8_t>>& keep) {
+    const int B = (int)q.shape[0], H = (int)q.shape[1], S = (int)q.shape[2], D = (int)q.shape[3];
+    const int Sk = (int)k.shape[2];
+    std::vector<float> out((size_t)B * H * S * D, 0.f);
+    for (int b = 0; b < B; ++b) {
+        std::vector<int> idx;
+        for (int j = 0; j < Sk; ++j)
+            if (keep[b][j]) idx.push_back(j);
+        if (idx.empty()) continue;
+        const int n = (int)idx.size();
+        std::vector<float> kk((size_t)H * n * D), vv((size_t)H * n * D), o((size_t)H * S * D);
+        for (int h = 0; h < H; ++h)
+            for (int j = 0; j < n; ++j)
+                for (int d = 0; d < D; ++d) {
+                    const size_t src = (((size_t)b * H + h) * Sk + idx[j]) * D + d;
+                    kk[((size_t)h * n + j) * D + d] = k.host[src];
+                    vv[((size_t)h * n + j) * D + d] = v.host[src];
+                }
+        sfo_attention_f32(q.host.data() + (size_t)b * H * S * D, kk.data(), vv.data(), o.data(), 1, H,
+                          S, n, D, 0.f, 0, nullptr);
+        std::memcpy(out.data() + (size_t)b * H * S * D, o.data(), o.size() * 4);
+    }
+    return out;
+}
+
+void test_self_attention_matches_oracle() {
+    RocmBackend be;
+    Bf16Tensor q(11, {1, 32, 67, 64}), k(12, {1, 32, 67, 64}), v(13, {1, 32, 67, 64});
+    DevBuf ob((size_t)32 * 67 * 64 * 4);
+    TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {1, 32, 67, 64});
+    be.attention(q.ref(), k.ref(), v.ref(), out);
+    HIP_OK(hipDeviceSynchronize());
+    std::vector<float> ref(q.host.size());
+    sfo_attention_f32(q.host.data(), k.host.data(), v.host.data(), ref.data(), 1, 32, 67, 67, 64, 0.f,
+                      0, nullptr);
+    expect_close(download_f32(ob, ref.size()), ref, "self 1x32x67x67");
+}
+
+void test_int32_mask_is_valid_lengths() {
+    RocmBackend be;
+    const int B = 2, H = 4, S = 67, Sk = 4374;
+    Bf16Tensor q(21, {B, H, S, 64}), k(22, {B, H, Sk, 64}), v(23, {B, H, Sk, 64});
+    const int32_t lens[B] = {4000, 517};
+    DevBuf lb(sizeof lens);
+    HIP_OK(hipMemcpy(lb.p, lens, sizeof lens, hipMemcpyHostToDevice));
+    TensorRef mask = TensorRef::contiguous(lb.p, DType::Int32, {B});
+    DevBuf ob((size_t)B * H * S * 64 * 4);
+    TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {B, H, S, 64});
+    be.attention(q.ref(), k.ref(), v.ref(), out, &mask);
+    HIP_OK(hipDeviceSynchronize());
+    std::vector<float> ref(q.host.size());
+    sfo_attention_f32(q.host.data(), k.host.data(), v.host.data(), ref.data(), B, H, S, Sk, 64, 0.f, 0,
+                      lens);
+    expect_close(download_f32(ob, ref.size()), ref, "Int32 lengths");
+}
+
+void test_bool_key_padding_mask_both_shapes() {
+    RocmBackend be;
+    const int B = 2, H = 2, S = 67, Sk = 300, pitch = 300;
+    Bf16Tensor q(31, {B, H, S, 64}), k(32, {B, H, Sk, 64}), v(33, {B, H, Sk, 64});
+    std::vector<std::vector<uint8_t>> keep(B, std::vector<uint8_t>(pitch, 0));
+    std::vector<float> u(B * Sk);
+    sfo_randn(34, (int64_t)u.size(), 1.f, u.data());
+    for (int b = 0; b < B; ++b)
+        for (int j = 0; j < Sk; ++j) keep[b][j] = u[b * Sk + j] > -0.3f ? 1 : 0;
+    DevBuf mb((size_t)B * pitch);
+    for (int b = 0; b < B; ++b)
+        HIP_OK(hipMemcpy(static_cast<char*>(mb.p) + b * pitch, keep[b].data(), pitch, hipMemcpyHostToDevice));
+    const std::vector<float> ref = oracle_kept(q, k, v, keep);
+    for (int form = 0; form < 2; ++form) {
+        TensorRef mask = form == 0 ? TensorRef::contiguous(mb.p, DType::Bool, {B, Sk})
+                                   : TensorRef::contiguous(mb.p, DType::Bool, {B, 1, 1, Sk});
+        DevBuf ob((size_t)B * H * S * 64 * 4);
+        TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {B, H, S, 64});
+        be.attention(q.ref(), k.ref(), v.ref(), out, &mask);
+        HIP_OK(hipDeviceSynchronize());
+        expect_close(download_f32(ob, ref.size()), ref, form == 0 ? "Bool [B,Sk]" : "Bool [B,1,1,Sk]");
+    }
+}
+
+void test_strided_output_and_explicit_scale() {
+    RocmBackend be;
+    const int B = 1, H = 8, S = 67, Sk = 1024;
+    Bf16Tensor q(41, {B, H, S, 64}), k(42, {B, H, Sk, 64}), v(43, {B, H, Sk, 64});
+    // out as a [B, S, H, D] buffer viewed as [B, H, S, D] (the block's layout)
+    DevBuf ob((size_t)B * S * H * 64 * 4);
+    TensorRef out;
+    out.data = ob.p;
+    out.dtype = DType::Float32;
+    out.shape = {B, H, S, 64};
+    out.strides = {(int64_t)S * H * 64 * 4, 64 * 4, (int64_t)H * 64 * 4, 4};
+    out.on_device = true;
+    be.attention(q.ref(), k.ref(), v.ref(), out, nullptr, 0.3f);
+    HIP_OK(hipDeviceSynchronize());
+    std::vector<float> ref(q.host.size());
+    sfo_attention_f32(q.host.data(), k.host.data(), v.host.data(), ref.data(), B, H, S, Sk, 64, 0.3f, 0,
+                      nullptr);
+    std::vector<float> seq = download_f32(ob, ref.size()), got(ref.size());
+    for (int h = 0; h < H; ++h)
+        for (int s = 0; s < S; ++s)
+            for (int d = 0; d < 64; ++d)
+                got[((size_t)h * S + s) * 64 + d] = seq[((size_t)s * H + h) * 64 + d];
+    expect_close(got, ref, "BSHD view, scale 0.3");
+}
+
+void test_causal() {
+    RocmBackend be;
+    Bf16Tensor q(51, {1, 4, 67, 64}), k(52, {1, 4, 67, 64}), v(53, {1, 4, 67, 64});
+    DevBuf ob((size_t)4 * 67 * 64 * 4);
+    TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {1, 4, 67, 64});
+    be.attention(q.ref(), k.ref(), v.ref(), out, nullptr, 0.f, true);
+    HIP_OK(hipDeviceSynchronize());
+    std::vector<float> ref(q.host.size());
+    sfo_attention_f32(q.host.data(), k.host.data(), v.host.data(), ref.data(), 1, 4, 67, 67, 64, 0.f, 1,
+                      nullptr);
+    expect_close(download_f32(ob, ref.size()), ref, "causal");
+}
+
+template <class E>
+void expect_throw(const std::function<void()>& fn, const char* what) {
+    try {
+        fn();
+    } catch (const E&) {
+        return;
+    } catch (const std::exception& e) {
+        throw std::runtime_error(std::string(what) + ": wrong exception type: " + e.what());
+    }
+    throw std::runtime_error(std::string(what) + ": no exception");
+}
+
+void test_errors_use_reference_exception_types() {
+    RocmBackend be;
+    Bf16Tensor q(61, {1, 2, 8, 64}), k(62, {1, 2, 300, 64});
+    DevBuf ob((size_t)2 * 8 * 64 * 4);
+    TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {1, 2, 8, 64});
+    TensorRef qf = q.ref();
+    qf.dtype = DType::Float32;   // wrong dtype
+    expect_throw<std::invalid_argument>([&] { be.attention(qf, k.ref(), k.ref(), out); }, "fp32 inputs");
+    TensorRef qh = q.ref();
+    qh.on_device = false;        // host tensor (cuda_backend.cu:156-161)
+    expect_throw<std::invalid_argument>([&] { be.attention(qh, k.ref(), k.ref(), out); }, "host tensor");
+    DevBuf fm((size_t)8 * 300 * 4);
+    TensorRef additive = TensorRef::contiguous(fm.p, DType::Float32, {1, 1, 8, 300});
+    expect_throw<std::invalid_argument>([&] { be.attention(q.ref(), k.ref(), k.ref(), out, &additive); },
+                                        "additive float mask");
+    DevBuf bm((size_t)8 * 300);
+    TensorRef per_query = TensorRef::contiguous(bm.p, DType::Bool, {1, 1, 8, 300});
+    expect_throw<std::invalid_argument>([&] { be.attention(q.ref(), k.ref(), k.ref(), out, &per_query); },
+                                        "per-query Bool mask");
+    Bf16Tensor q128(63, {1, 1, 4, 128});
+    DevBuf ob128((size_t)4 * 128 * 4);
+    TensorRef out128 = TensorRef::contiguous(ob128.p, DType::Float32, {1, 1, 4, 128});
+    expect_throw<std::invalid_argument>([&] { be.attention(q128.ref(), q128.ref(), q128.ref(), out128); },
+                                        "head dim 128");
+    TensorRef bad_shape = k.ref();
+    bad_shape.shape[3] = 32;
+    expect_throw<std::invalid_argument>([&] { be.attention(q.ref(), bad_shape, k.ref(), out); }, "shape mismatch");
+}
+
+void test_graph_capture_with_reserved_workspace() {
+    const int B = 1, H = 32, S = 67, Sk = 4374;
+    Bf16Tensor q(71, {B, H, S, 64}), k(72, {B, H, Sk, 64}), v(73, {B, H, Sk, 64});
+    DevBuf ob((size_t)B * H * S * 64 * 4), eb((size_t)B * H * S * 64 * 4);
+    TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {B, H, S, 64});
+    TensorRef eager = TensorRef::contiguous(eb.p, DType::Float32, {B, H, S, 64});
+    hipStream_t st;
+    HIP_OK(hipStreamCreate(&st));
+    {
+        // capture without a reserved workspace: refused with runtime_error
+        RocmBackend fresh;
+        HIP_OK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        bool threw = false;
+        try {
+            fresh.attention(q.ref(), k.ref(), v.ref(), out, nullptr, 0.f, false, st);
+        } catch (const std::runtime_error&) {
+            threw = true;
+        }
+        hipGraph_t g0 = nullptr;
+        (void)hipStreamEndCapture(st, &g0);
+        if (g0) (void)hipGraphDestroy(g0);
+        CHECK(threw, "capture without reserve must throw std::runtime_error");
+    }
+    RocmBackend be;
+    be.reserve_attention_workspace(RocmBackend::attention_workspace_bytes(q.ref(), k.ref()));
+    be.attention(q.ref(), k.ref(), v.ref(), eager, nullptr, 0.f, false, st);
+    HIP_OK(hipStreamSynchronize(st));
+    hipGraph_t g;
+    hipGraphExec_t ge;
+    HIP_OK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    be.attention(q.ref(), k.ref(), v.ref(), out, nullptr, 0.f, false, st);
+    HIP_OK(hipStreamEndCapture(st, &g));
+    HIP_OK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    const std::vector<float> ref = download_f32(eb, (size_t)B * H * S * 64);
+    for (int rep = 0; rep < 3; ++rep) {
+        HIP_OK(hipMemsetAsync(ob.p, 0xff, ob.n, st));   // NaN fill, outside the graph
+        HIP_OK(hipGraphLaunch(ge, st));
+        HIP_OK(hipStreamSynchronize(st));
+        const std::vector<float> got = download_f32(ob, ref.size());
+        CHECK(std::memcmp(got.data(), ref.data(), ref.size() * 4) == 0, "graph replay == eager");
+    }
+    (void)hipGraphExecDestroy(ge);
+    (void)hipGraphDestroy(g);
+    (void)hipStreamDestroy(st);
+}
+
+}  // namespace
+
+int main() {
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+        std::printf("no HIP device\n");
+        return 2;
+    }
+    run_case("self_attention_matches_oracle", test_self_attention_matches_oracle);
+    run_case("int32_mask_is_valid_lengths", test_int32_mask_is_valid_lengths);
+    run_case("bool_key_padding_mask_both_shapes", test_bool_key_padding_mask_both_shapes);
+    run_case("strided_output_and_explicit_scale", test_strided_output_and_explicit_scale);
+    run_case("causal", test_causal);
+    run_case("errors_use_reference_exception_types", test_errors_use_reference_exception_types);
+    run_case("graph_capture_with_reserved_workspace", test_graph_capture_with_reserved_workspace);
+    if (g_failed) {
+        std::printf("%d case(s) failed\n", g_failed);
+        return 1;
+    }
+    std::printf("ALL PASSED\n");
+    return 0;
+}
