@@ -34,6 +34,12 @@ sys.path.insert(0, ROOT)
 
 METRIC = "RDT-1B denoise-loop latency ms (bs=1) + cross-attn HBM GB/s vs roofline"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per roofline op measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# (x2.0 / x1.0, scales read off a 256 MiB copy kernel) on `bench.py
+# --profile-roofline`: ring kernel 38.32 MB read + 9.07 MB written, merge
+# 10.11 MB read + 0.27 MB written (profiles/cross_attention_b1_image_roofline.md).
+# Re-measured whenever the attention kernels change.
+TRAFFIC_B1_IMAGE_BYTES = 57779046
 
 
 def attn_bytes(B, H, Sq, Sk_valid_total, D=64, eb=2):
@@ -251,6 +257,37 @@ def cpu_baseline(budget_s=25.0):
     }
 
 
+def profile_roofline(iters=50):
+    """Runs only what the roofline profiles measure: the batch-1 image
+    cross-attention op (attn_ring_kernel + attn_merge_kernel) `iters` times,
+    then a plain 256 MiB device-to-device copy `iters` times -- the
+    calibration kernel whose FETCH_SIZE / WRITE_SIZE per dispatch give the
+    counter's scale (256 MiB read, 256 MiB written).  Eager launches, so each
+    dispatch is one kernel-trace / PMC record."""
+    import torch
+
+    from servoflow_amd.attention import attention, make_desc, workspace_bytes
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1235)
+    q = torch.randn(1, 32, 67, 64, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 32, 4374, 64, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, 32, 4374, 64, device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty(1, 67, 32, 64, device=dev, dtype=torch.bfloat16).permute(0, 2, 1, 3)
+    ws = torch.empty(max(workspace_bytes(make_desc(q, k, v, out)), 16), dtype=torch.uint8, device=dev)
+    for _ in range(iters):
+        attention(q, k, v, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    print(f"profile: {iters} cross-attention ops 1x32x67x4374x64 done", flush=True)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"profile: {iters} copies of 256 MiB done", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +295,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline and roofline only")
+    ap.add_argument("--profile-roofline", action="store_true",
+                    help="run only the roofline op and the copy calibration kernel (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -268,6 +307,9 @@ def main():
     import torch
 
     torch.cuda.init()
+    if args.profile_roofline:
+        profile_roofline()
+        return
     extra = {}
     # ---- headline: batch-1 loop (config 4)
     m1, enc1 = make_model(1)
@@ -329,7 +371,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(img1["frac"], 4),
-            "traffic": None,
+            "traffic": TRAFFIC_B1_IMAGE_BYTES,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE on bench.py --profile-roofline, "
+                              "profiles/cross_attention_b1_image_roofline.md",
             "kernel": "cross-attention op (attn_split_kernel + attn_merge_kernel), 1x32x67x4374x64 "
                       f"bf16, {img1['bytes']} algorithmic bytes per launch, {img1['us']:.2f} us",
         },
