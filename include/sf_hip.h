@@ -146,12 +146,15 @@ int sf_attn_fwd(const sf_attn_desc* desc, const void* q, const void* k,
  * K a multiple of 32; bias, w_scale, head_gamma, norm_gamma are fp32;
  * head_out must be 8-byte aligned with strides that are multiples of 4.
  *
- * workspace: fp32 scratch of sf_gemm_workspace_bytes() for the split-K
- * path (M <= 160, N a multiple of 16), which spreads one weight matrix over
- * all CUs.  With workspace == NULL (or a shape outside that range) a
- * single-pass kernel runs instead and nothing beyond A, W and the outputs is
- * touched.  A non-NULL workspace that is too small is SF_EWORKSPACE.  Calls
- * that may run concurrently need separate workspaces.
+ * workspace: scratch of sf_gemm_workspace_bytes().  M <= 160 (N a multiple
+ * of 16): fp32 split-K partial sums, which spread one weight matrix over all
+ * CUs.  M > 160: the library path -- hipBLASLt writes the fp32 product in
+ * chunks of <= 8192 rows into the workspace (plus a bf16 copy of int8
+ * weights and hipBLASLt's own scratch) and the epilogue kernels read it.
+ * With workspace == NULL a single-pass kernel runs instead and nothing
+ * beyond A, W and the outputs is touched.  A non-NULL workspace that is too
+ * small is SF_EWORKSPACE.  Calls that may run concurrently need separate
+ * workspaces.
  * ------------------------------------------------------------------------- */
 typedef enum sf_act { SF_ACT_NONE = 0, SF_ACT_GELU_TANH = 1, SF_ACT_SILU = 2 } sf_act;
 typedef enum sf_epilogue { SF_EPI_PLAIN = 0, SF_EPI_HEADS = 1, SF_EPI_ADD_NORM = 2 } sf_epilogue;
@@ -190,6 +193,11 @@ typedef struct sf_gemm_desc {
 size_t sf_gemm_workspace_bytes(const sf_gemm_desc* desc);
 
 int sf_gemm(const sf_gemm_desc* desc, void* stream);
+
+/* Host-side setup of the library path for this shape (algorithm selection,
+ * once per shape and process; no device work).  sf_gemm does it on first
+ * use; call this before capturing a graph that contains the call. */
+int sf_gemm_prepare(const sf_gemm_desc* desc);
 
 /* ---------------------------------------------------------------------------
  * Normalisation and dequant.

@@ -31,13 +31,24 @@
 //   waves, and writes fp32 partial sums; a reduce kernel sums the K slices in
 //   a fixed order (deterministic) and applies the epilogue, including the
 //   residual add + RMSNorm that follows a block branch.
-//   single-pass path (no workspace, or M > 160): one workgroup of 8 waves per
-//   16 or 64 weight rows over all of K, reduced in LDS, epilogue in place.
+//   library path (M > 160, caller workspace): at those sizes the product is
+//   MFMA-bound, a plain library GEMM: hipBLASLt computes the fp32 product
+//   chunk by chunk (<= 8192 rows) into the workspace and the same reduce
+//   kernels apply the epilogue.  int8 weights are first widened to bf16
+//   (exactly, without the scale) in the workspace, so the row scale is
+//   applied in the epilogue as in the other paths.
+//   single-pass path (no workspace): one workgroup of 8 waves per 16 or 64
+//   weight rows over all of K, reduced in LDS, epilogue in place.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
 
+#include <hipblaslt/hipblaslt.h>
+
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 #include "sf_device.h"
 #include "sf_hip.h"
@@ -352,6 +363,7 @@ struct EpiArgs {
     const float* part;     // [splits][M][N]
     int splits;
     int M, N;
+    int64_t m_off;         // row of the outputs that partial row 0 belongs to
     const float* w_scale;  // [N] or null
     const float* bias;     // [N] or null
     int act;
@@ -424,7 +436,7 @@ __global__ __launch_bounds__(256) void reduce_plain_kernel(const EpiArgs e) {
     const int m = (int)(idx / n4);
     const int n = 4 * (int)(idx % n4);
     f32x4 v = finish4<NS>(e, m, n);
-    const int64_t off = (int64_t)m * e.ldc + n;
+    const int64_t off = (e.m_off + m) * e.ldc + n;
     if (e.c_f32) {
         f32x4* cp = reinterpret_cast<f32x4*>(static_cast<float*>(e.c) + off);
         if (e.accumulate) v += *cp;
@@ -458,8 +470,9 @@ __global__ __launch_bounds__(256) void reduce_heads_kernel(const EpiArgs e) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = v[j] * inv_rms * gq[j];
     }
-    const int b = m / e.S;
-    const int s = m % e.S;
+    const int64_t mg = e.m_off + m;
+    const int64_t b = mg / e.S;
+    const int64_t s = mg % e.S;
     uint16_t* o = e.head_out[sec] + b * e.head_sb[sec] + h * e.head_sh[sec] + s * e.head_ss[sec] + d;
     *reinterpret_cast<uint2*>(o) = pack_bf16x4(v);
 }
@@ -473,7 +486,7 @@ __global__ __launch_bounds__(kAddNormThreads) void reduce_addnorm_kernel(const E
     __shared__ float red[kAddNormThreads / 64];
     const int m = blockIdx.x;
     const int n4 = e.N / 4;
-    float* x = static_cast<float*>(e.c) + (int64_t)m * e.ldc;
+    float* x = static_cast<float*>(e.c) + (e.m_off + m) * e.ldc;
     // every load of the row first (partials and residual), then the stores:
     // a store to x between them would keep later loads from issuing early
     const int nch = min(kAddNormMaxChunks, (n4 - (int)threadIdx.x + kAddNormThreads - 1) / kAddNormThreads);
@@ -514,13 +527,25 @@ __global__ __launch_bounds__(kAddNormThreads) void reduce_addnorm_kernel(const E
             f32x4 o;
 #pragma unroll
             for (int j = 0; j < 4; ++j) o[j] = xv[i][j] * inv_rms * gv[i][j];
-            const int64_t off = (int64_t)m * e.norm_ldo + 4 * c;
+            const int64_t off = (e.m_off + m) * e.norm_ldo + 4 * c;
             if (e.norm_f32)
                 *reinterpret_cast<f32x4*>(static_cast<float*>(e.norm_out) + off) = o;
             else
                 *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.norm_out) + off) = pack_bf16x4(o);
         }
     }
+}
+
+// int8 weight codes -> bf16 (exact), row-major [N][K] out of [N][ldw].
+__global__ __launch_bounds__(256) void widen_int8_kernel(const int8_t* __restrict__ q, int64_t ldw,
+                                                         uint16_t* __restrict__ out, int N, int K) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;   // 8 codes per thread
+    const int k8 = K / 8;
+    if (idx >= (int64_t)N * k8) return;
+    const int64_t n = idx / k8;
+    const int k = 8 * (int)(idx % k8);
+    const uint2 raw = *reinterpret_cast<const uint2*>(q + n * ldw + k);
+    *reinterpret_cast<bf16x8*>(out + n * K + k) = i8x8_to_bf16x8(raw);
 }
 
 struct SkPlan {
@@ -587,12 +612,12 @@ inline void launch_splitk(const SkArgs& a, const SkPlan& p, bool w8, hipStream_t
 
 template <int NS>
 void launch_reduce(const sf_gemm_desc* d, const EpiArgs& e, hipStream_t s) {
-    const int64_t quads = (int64_t)d->M * d->N / 4;
+    const int64_t quads = (int64_t)e.M * e.N / 4;
     const unsigned blocks = (unsigned)((quads + 255) / 256);
     if (d->epilogue == SF_EPI_HEADS)
         hipLaunchKernelGGL(reduce_heads_kernel<NS>, dim3(blocks), dim3(256), 0, s, e);
     else if (d->epilogue == SF_EPI_ADD_NORM)
-        hipLaunchKernelGGL(reduce_addnorm_kernel<NS>, dim3(d->M), dim3(kAddNormThreads), 0, s, e);
+        hipLaunchKernelGGL(reduce_addnorm_kernel<NS>, dim3(e.M), dim3(kAddNormThreads), 0, s, e);
     else
         hipLaunchKernelGGL(reduce_plain_kernel<NS>, dim3(blocks), dim3(256), 0, s, e);
 }
@@ -610,6 +635,95 @@ hipError_t launch_smallm(const GemmArgs& g, int mb, dim3 grid, hipStream_t s) {
 }
 
 }  // namespace sfk
+
+// ---------------------------------------------------------------------------
+// library path (hipBLASLt)
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kLibMinRows = 161;       // M above the split-K range
+constexpr int kLibChunkRows = 8192;    // rows of fp32 product staged at once
+constexpr size_t kLibLtBytes = 32u << 20;
+
+size_t up256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+struct LibPlan {
+    bool ok = false;
+    int chunk = 0;
+    size_t c_bytes = 0, w_bytes = 0, total = 0;
+};
+
+LibPlan plan_library(int M, int N, int K, bool w8) {
+    LibPlan p;
+    if (M < kLibMinRows || N <= 0 || (N & 15) || K <= 0 || (K & 31)) return p;
+    p.chunk = std::min(M, kLibChunkRows);
+    p.c_bytes = up256((size_t)p.chunk * N * 4);
+    p.w_bytes = w8 ? up256((size_t)N * K * 2) : 0;
+    p.total = p.c_bytes + p.w_bytes + kLibLtBytes;
+    p.ok = true;
+    return p;
+}
+
+// One hipBLASLt handle per device and one (descriptor, layouts, algorithm)
+// per GEMM shape, created on first use and kept for the process.
+struct LtShape {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    bool ok = false;
+};
+
+std::mutex g_lt_mu;
+std::map<int, hipblasLtHandle_t> g_lt_handles;
+std::map<std::tuple<int, int, int, int, int64_t, int64_t>, LtShape> g_lt_shapes;
+
+// D (fp32 [rows][N]) = A_act (bf16 [rows][lda]) . W (bf16 [N][ldw])^T, in
+// hipBLASLt's column-major terms: D (N x rows) = op_T(W: K x N, ld ldw) .
+// (A_act: K x rows, ld lda).
+int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, hipblasLtHandle_t* h, const LtShape** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return SF_EDEVICE;
+    std::lock_guard<std::mutex> lock(g_lt_mu);
+    auto hit = g_lt_handles.find(dev);
+    if (hit == g_lt_handles.end()) {
+        hipblasLtHandle_t nh = nullptr;
+        if (hipblasLtCreate(&nh) != HIPBLAS_STATUS_SUCCESS) return SF_EDEVICE;
+        hit = g_lt_handles.emplace(dev, nh).first;
+    }
+    *h = hit->second;
+    const auto key = std::make_tuple(dev, N, K, rows, lda, ldw);
+    auto it = g_lt_shapes.find(key);
+    if (it == g_lt_shapes.end()) {
+        LtShape sh;
+        bool ok = hipblasLtMatmulDescCreate(&sh.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+        const hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
+        ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof opT) ==
+                       HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof opN) ==
+                       HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&sh.a, HIP_R_16BF, K, N, ldw) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&sh.b, HIP_R_16BF, K, rows, lda) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&sh.d, HIP_R_32F, N, rows, N) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulPreference_t pref = nullptr;
+        ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+        const uint64_t wsmax = kLibLtBytes;
+        ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax,
+                                                         sizeof wsmax) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulHeuristicResult_t res[1];
+        int nres = 0;
+        ok = ok && hipblasLtMatmulAlgoGetHeuristic(*h, sh.desc, sh.a, sh.b, sh.d, sh.d, pref, 1, res, &nres) ==
+                       HIPBLAS_STATUS_SUCCESS;
+        ok = ok && nres > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= kLibLtBytes;
+        if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
+        if (ok) sh.algo = res[0].algo;
+        sh.ok = ok;
+        it = g_lt_shapes.emplace(key, sh).first;
+    }
+    *out = &it->second;
+    return it->second.ok ? SF_OK : SF_ENOTSUP;
+}
+
+}  // namespace
 
 // ---------------------------------------------------------------------------
 // C-ABI
@@ -742,7 +856,24 @@ int gemm_single_pass(const sf_gemm_desc* d, const sfk::EpiArgs& e, hipStream_t s
 extern "C" size_t sf_gemm_workspace_bytes(const sf_gemm_desc* d) {
     if (!d) return 0;
     const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K);
-    return p.split ? p.ws_bytes : 0;
+    if (p.split) return p.ws_bytes;
+    const LibPlan lp = plan_library(d->M, d->N, d->K, d->w_dtype == SF_I8);
+    return lp.ok ? lp.total : 0;
+}
+
+extern "C" int sf_gemm_prepare(const sf_gemm_desc* d) {
+    if (!d) return SF_EINVAL;
+    const LibPlan lp = plan_library(d->M, d->N, d->K, d->w_dtype == SF_I8);
+    if (!lp.ok) return SF_OK;   // split-K and single-pass paths need no setup
+    const int64_t ldw = d->w_dtype == SF_I8 ? d->K : d->ldw;
+    hipblasLtHandle_t h;
+    const LtShape* sh = nullptr;
+    for (int rows : {lp.chunk, d->M % lp.chunk}) {
+        if (rows <= 0) continue;
+        const int st = lt_lookup(d->N, d->K, rows, d->lda, ldw, &h, &sh);
+        if (st != SF_OK) return st;
+    }
+    return SF_OK;
 }
 
 extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
@@ -753,6 +884,47 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     SF_CHECK_OK(validate(d, e));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K);
+    if (d->workspace && !p.split && splittable(d)) {
+        const bool w8 = d->w_dtype == SF_I8;
+        const LibPlan lp = plan_library(d->M, d->N, d->K, w8);
+        if (lp.ok) {
+            if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < lp.total) return SF_EWORKSPACE;
+            if (!al16(d->workspace)) return SF_EINVAL;
+            char* ws = static_cast<char*>(d->workspace);
+            float* cbuf = reinterpret_cast<float*>(ws);
+            void* ltws = ws + lp.c_bytes + lp.w_bytes;
+            const void* W = d->W;
+            int64_t ldw = d->ldw;
+            if (w8) {
+                uint16_t* wb = reinterpret_cast<uint16_t*>(ws + lp.c_bytes);
+                const int64_t n8 = (int64_t)d->N * (d->K / 8);
+                hipLaunchKernelGGL(sfk::widen_int8_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s,
+                                   static_cast<const int8_t*>(d->W), d->ldw, wb, d->N, d->K);
+                if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
+                W = wb;
+                ldw = d->K;
+            }
+            const float one = 1.f, zero = 0.f;
+            for (int m0 = 0; m0 < d->M; m0 += lp.chunk) {
+                const int rows = std::min(lp.chunk, d->M - m0);
+                hipblasLtHandle_t h;
+                const LtShape* sh = nullptr;
+                SF_CHECK_OK(lt_lookup(d->N, d->K, rows, d->lda, ldw, &h, &sh));
+                const uint16_t* Ac = static_cast<const uint16_t*>(d->A) + (int64_t)m0 * d->lda;
+                if (hipblasLtMatmul(h, sh->desc, &one, W, sh->a, Ac, sh->b, &zero, cbuf, sh->d, cbuf, sh->d,
+                                    &sh->algo, ltws, kLibLtBytes, s) != HIPBLAS_STATUS_SUCCESS)
+                    return SF_ELAUNCH;
+                sfk::EpiArgs ec = e;
+                ec.part = cbuf;
+                ec.splits = 1;
+                ec.M = rows;
+                ec.m_off = m0;
+                sfk::launch_reduce<1>(d, ec, s);
+                if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
+            }
+            return SF_OK;
+        }
+    }
     if (!d->workspace || !p.split || !splittable(d)) return gemm_single_pass(d, e, s);
     if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < p.ws_bytes) return SF_EWORKSPACE;
     if (!al16(d->workspace)) return SF_EINVAL;

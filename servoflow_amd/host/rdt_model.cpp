@@ -314,10 +314,14 @@ int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v
     return sf_attn_fwd(&d, q, k, v, out, m->attn_ws, m->attn_ws_bytes, s);
 }
 
-// Largest split-K workspace over the step's GEMMs (rows B*S, B*T, B or 1).
-size_t gemm_ws_for(const sf_rdt* m) {
+// Every GEMM the runtime issues: each matrix at each row count it is used
+// with (step rows B*S, B*T, B, 1; condition rows B*lang_max, B*img_len).
+// Returns the largest workspace; with prepare, also selects the library
+// path's algorithms now, outside any graph capture.
+size_t gemm_ws_for(const sf_rdt* m, bool prepare, int* status) {
     const sf_rdt_config& c = m->cfg;
-    const int rows[4] = {c.batch * (c.horizon + 3), c.batch * c.horizon, c.batch, 1};
+    const int rows[6] = {c.batch * (c.horizon + 3), c.batch * c.horizon, c.batch, 1,
+                         c.batch * c.lang_max, c.batch * c.img_len};
     size_t best = 0;
     for (const Param& p : m->params) {
         if (p.shape.size() != 2 || p.dtype == SF_F32) continue;
@@ -326,7 +330,11 @@ size_t gemm_ws_for(const sf_rdt* m) {
             d.M = M;
             d.N = (int32_t)p.shape[0];
             d.K = (int32_t)p.shape[1];
+            d.lda = d.K;
+            d.ldw = d.K;
+            d.w_dtype = p.dtype;
             best = std::max(best, sf_gemm_workspace_bytes(&d));
+            if (prepare && status && *status == SF_OK) *status = sf_gemm_prepare(&d);
         }
     }
     return best;
@@ -538,7 +546,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     m->attn_ws_bytes = std::max(attn_ws_for(c, c.lang_max), attn_ws_for(c, c.img_len));
     m->attn_ws_bytes = std::max(m->attn_ws_bytes, attn_ws_for(c, (int)S));
     bufs.push_back({&m->attn_ws, std::max<size_t>(m->attn_ws_bytes, 256)});
-    m->gemm_ws_bytes = gemm_ws_for(m);
+    m->gemm_ws_bytes = gemm_ws_for(m, false, nullptr);
     bufs.push_back({&m->gemm_ws, std::max<size_t>(m->gemm_ws_bytes, 256)});
     std::vector<size_t> boff(bufs.size());
     for (size_t i = 0; i < bufs.size(); ++i) {
@@ -583,6 +591,12 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     if (hipMemcpy(m->sincos, tab.data(), tab.size() * 2, hipMemcpyHostToDevice) != hipSuccess) {
         sf_rdt_destroy(m);
         return SF_EDEVICE;
+    }
+    int prep = SF_OK;
+    (void)gemm_ws_for(m, true, &prep);
+    if (prep != SF_OK) {
+        sf_rdt_destroy(m);
+        return prep;
     }
     *out = m;
     return SF_OK;

@@ -71,7 +71,7 @@ def test_gemm_split_path_is_used_and_deterministic():
     r2 = host(K_gemm(a, w, None, 0))
     assert np.array_equal(r1, r2)
     big = rounded(7, (161, 2048))
-    assert K.workspace_bytes(dev(big), dev(w)) == 0      # M > 160: single-pass only
+    assert K.workspace_bytes(dev(big), dev(w)) > 0        # M > 160: the library path
 
 
 @pytest.mark.parametrize("N", [2048, 6144])
@@ -229,3 +229,53 @@ def test_gemm_rejects_bad_shapes():
     with pytest.raises(abi.SfError) as e:
         K.gemm(a, w)
     assert e.value.status == abi.SF_ENOTSUP
+
+
+@pytest.mark.parametrize("M,N,Kd,w8", [(1072, 2048, 2048, False), (161, 6144, 2048, True),
+                                      (2144, 2048, 2048, True), (9000, 64, 256, False)])
+def test_gemm_library_path(M, N, Kd, w8):
+    """M > 160 with a workspace: hipBLASLt product + the reduce epilogues
+    (chunks of 8192 rows; int8 weights widened exactly, scale in the
+    epilogue)."""
+    a = rounded(81 + M, (M, Kd))
+    b = O.randn(83, (N,), 0.02)
+    if w8:
+        q, s = O.quantize_int8_rows(O.randn(82, (N, Kd), 0.02))
+        w, wdev, sdev = O.dequant_int8(q, s), dev(q, torch.int8), dev(s, torch.float32)
+    else:
+        w = rounded(82, (N, Kd), 0.02)
+        wdev, sdev = dev(w), None
+    assert K.workspace_bytes(dev(a), wdev) > 0
+    got = host(K.gemm(dev(a), wdev, dev(b, torch.float32), abi.SF_ACT_GELU_TANH, out_dtype=torch.float32,
+                      w_scale=sdev))
+    ref = O.linear(a, w, b, act=abi.SF_ACT_GELU_TANH)
+    close(got, ref, f"library gemm {M}x{N}x{Kd} w8={w8}")
+
+
+def test_gemm_library_heads_and_add_norm():
+    """The condition K/V projection shape (rows B*4374, K|V heads, k_norm) and
+    a batch-16 residual add + RMSNorm through the library path."""
+    B, S, H = 1, 4374, 32
+    a = rounded(91, (B * S, 2048))
+    w = rounded(92, (2 * H * 64, 2048), 0.02)
+    b = O.randn(93, (2 * H * 64,), 0.02)
+    gk = 1.0 + O.randn(94, (64,), 0.1)
+    outs = [torch.empty(B, H, S, 64, device=DEV, dtype=torch.bfloat16) for _ in range(2)]
+    K.gemm_heads(dev(a), dev(w), dev(b, torch.float32), S, H, outs, (dev(gk, torch.float32), None))
+    kv = O.linear(a, w, b).reshape(B, S, 2 * H * 64)
+    Kh, V = O.split_kv(kv, H, 64)
+    Kh = O.rms_norm(Kh, gk)
+    for got, ref in zip(outs, (Kh, V)):
+        g = host(got)
+        assert np.all(np.abs(g - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-3)
+        assert mean_rel(g, ref) < 3e-3
+    M = 16 * 67
+    a2, w2 = rounded(95, (M, 2048)), rounded(96, (2048, 2048), 0.02)
+    b2, g2 = O.randn(97, (2048,), 0.02), 1.0 + O.randn(98, (2048,), 0.1)
+    x = O.randn(99, (M, 2048))
+    xd = dev(x, torch.float32)
+    n = K.gemm_add_norm(dev(a2), dev(w2), dev(b2, torch.float32), xd, dev(g2, torch.float32),
+                        norm_dtype=torch.float32)
+    x_ref = x + O.linear(a2, w2, b2)
+    close(host(xd), x_ref, "residual (library)", rel=1e-5)
+    close(host(n), O.rms_norm(x_ref, g2), "norm (library)", rel=1e-4)
