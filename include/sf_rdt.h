@@ -134,6 +134,44 @@ int sf_rdt_sample(sf_rdt* m, float* x, int32_t use_graph, void* stream);
 /* Cross-attention K or V cache of block `layer` ([B, H, S, 64] bf16). */
 void* sf_rdt_cache_ptr(sf_rdt* m, int32_t layer, int32_t which_v);
 
+/* ---- checkpoints (safetensors) ------------------------------------------- */
+
+/* One tensor of a safetensors file (SafeTensorsLoader::TensorMeta,
+ * include/servoflow/loader/safetensors.h; header format of
+ * src/loader/safetensors.cpp:75-105).  data_begin / data_end are absolute
+ * byte offsets in the file; dtype is an sf_dtype value or -1. */
+typedef struct sf_st_entry {
+    char name[256];
+    int32_t dtype;
+    int32_t ndim;
+    int64_t shape[8];
+    uint64_t data_begin, data_end;
+} sf_st_entry;
+
+/* Lists the tensors of a safetensors file (SafeTensorsLoader::inspect,
+ * safetensors.cpp:110-114): fills up to max_entries entries and sets *count
+ * to the number of tensors in the file.  Host only. */
+int sf_safetensors_inspect(const char* path, sf_st_entry* entries, int32_t max_entries,
+                           int32_t* count);
+
+#define SF_LOAD_PARTIAL 1   /* do not fail when a model parameter is absent */
+
+/* Loads a checkpoint into the parameter table (SafeTensorsLoader::load +
+ * load_weight_from_map, safetensors.cpp:117-190): names as the servoflow
+ * checkpoint keys, HuggingFace names accepted through remap_key
+ * (tools/convert/hf_to_servoflow.py:41-65: leading "model." dropped, EMA and
+ * optimizer entries skipped); F32 / F16 / BF16 tensors converted to the
+ * parameter's type (bf16 round-to-nearest-even, or int8 rows quantised
+ * scale = max|w| / 127 in int8 mode); shapes must match up to leading 1s.
+ * Keys the model does not have are ignored; a model parameter absent from
+ * the file is an error unless flags has SF_LOAD_PARTIAL.  *loaded = number of
+ * parameters written.  Synchronous (hipMemcpy); sf_rdt_last_error describes
+ * a failure. */
+int sf_rdt_load_safetensors(sf_rdt* m, const char* path, int32_t flags, int32_t* loaded);
+
+/* Message of the last failure of a call on m ("" if none). */
+const char* sf_rdt_last_error(const sf_rdt* m);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -1,0 +1,9 @@
+// Internal helpers shared by the translation units of libsf_rdt.so.
+#pragma once
+
+#include <string>
+
+#include "sf_rdt.h"
+
+// Records the message sf_rdt_last_error returns for this model.
+void sf_rdt_set_error(sf_rdt* m, const std::string& msg);

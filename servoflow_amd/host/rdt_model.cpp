@@ -32,6 +32,7 @@
 
 #include "sf_hip.h"
 #include "sf_rdt.h"
+#include "rdt_internal.h"
 
 namespace {
 
@@ -116,7 +117,15 @@ struct sf_rdt {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     hipStream_t graph_stream = nullptr;
+
+    std::string last_error;
 };
+
+void sf_rdt_set_error(sf_rdt* m, const std::string& msg) {
+    if (m) m->last_error = msg;
+}
+
+extern "C" const char* sf_rdt_last_error(const sf_rdt* m) { return m ? m->last_error.c_str() : ""; }
 
 namespace {
 

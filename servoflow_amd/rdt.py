@@ -24,6 +24,14 @@ class RdtConfig(ctypes.Structure):
         "ctrl_freq", "num_steps", "batch", "int8_weights")] + [("eps", ctypes.c_float)]
 
 
+class StEntry(ctypes.Structure):
+    """Mirror of `sf_st_entry`."""
+
+    _fields_ = [("name", ctypes.c_char * 256), ("dtype", ctypes.c_int32), ("ndim", ctypes.c_int32),
+                ("shape", ctypes.c_int64 * 8), ("data_begin", ctypes.c_uint64), ("data_end", ctypes.c_uint64)]
+
+
+SF_LOAD_PARTIAL = 1
 _lib = None
 
 
@@ -59,6 +67,10 @@ def lib():
     L.sf_rdt_denoise_step.argtypes = [vp, vp, ctypes.c_float, vp, vp]
     L.sf_rdt_sample.argtypes = [vp, vp, i32, vp]
     L.sf_rdt_run_blocks.argtypes = [vp, vp, i32, i32, vp]
+    L.sf_safetensors_inspect.argtypes = [ctypes.c_char_p, ctypes.POINTER(StEntry), i32, ctypes.POINTER(i32)]
+    L.sf_rdt_load_safetensors.argtypes = [vp, ctypes.c_char_p, i32, ctypes.POINTER(i32)]
+    L.sf_rdt_last_error.argtypes = [vp]
+    L.sf_rdt_last_error.restype = ctypes.c_char_p
     _lib = L
     return L
 
@@ -69,6 +81,18 @@ def default_config(**over) -> RdtConfig:
     for k, v in over.items():
         setattr(c, k, v)
     return c
+
+
+def inspect_safetensors(path):
+    """[(name, sf_dtype, shape, data_begin, data_end)] of a safetensors file."""
+    n = ctypes.c_int32()
+    abi.check(lib().sf_safetensors_inspect(os.fsencode(path), None, 0, ctypes.byref(n)),
+              "sf_safetensors_inspect")
+    arr = (StEntry * max(n.value, 1))()
+    abi.check(lib().sf_safetensors_inspect(os.fsencode(path), arr, n.value, ctypes.byref(n)),
+              "sf_safetensors_inspect")
+    return [(e.name.decode("utf-8"), e.dtype, tuple(e.shape[:e.ndim]), e.data_begin, e.data_end)
+            for e in arr[:n.value]]
 
 
 _hip = None
@@ -135,6 +159,24 @@ class RdtModel:
         q = _memcpy_d2h(np.empty(shape, np.int8), ptr)
         s = _memcpy_d2h(np.empty(shape[0], np.float32), lib().sf_rdt_param_scale(self.h, idx))
         return q.astype(np.float32) * s[:, None]
+
+    def param_int8(self, idx):
+        """(codes int8 [N, K], row scales fp32 [N]) of an int8 parameter."""
+        _, dt, shape = self.params()[idx]
+        assert dt == abi.SF_I8
+        q = _memcpy_d2h(np.empty(shape, np.int8), lib().sf_rdt_param_data(self.h, idx))
+        s = _memcpy_d2h(np.empty(shape[0], np.float32), lib().sf_rdt_param_scale(self.h, idx))
+        return q, s
+
+    def load_safetensors(self, path, partial=False):
+        """Loads a checkpoint (sf_rdt_load_safetensors); returns the number of
+        parameters written."""
+        n = ctypes.c_int32()
+        st = lib().sf_rdt_load_safetensors(self.h, os.fsencode(path), SF_LOAD_PARTIAL if partial else 0,
+                                           ctypes.byref(n))
+        if st != abi.SF_OK:
+            raise abi.SfError(st, "sf_rdt_load_safetensors: " + lib().sf_rdt_last_error(self.h).decode())
+        return n.value
 
     def state_dict(self):
         return {nm: self.param_numpy(i, dt, sh) for i, (nm, dt, sh) in enumerate(self.params())}

@@ -31,9 +31,9 @@ def test_header_declares_entry_points():
 
 
 def _owner_lib(name):
-    # sf_rdt_* (model runtime) live in libsf_rdt.so, everything else in
-    # libsf_hip_kernels.so
-    if name.startswith("sf_rdt_"):
+    # sf_rdt_* (model runtime) and sf_safetensors_* (checkpoint reader) live
+    # in libsf_rdt.so, everything else in libsf_hip_kernels.so
+    if name.startswith(("sf_rdt_", "sf_safetensors_")):
         from servoflow_amd import rdt
         return rdt.lib()
     return abi.lib()
@@ -110,3 +110,17 @@ def test_workspace_contract():
     d1.num_splits = 0
     d1.scale = -1.0
     assert _fwd(d1) == abi.SF_ENOTSUP
+
+
+def test_backend_library_loads_and_exports_the_operator():
+    """libsf_backend.so (the C++ RocmBackend over the C-ABI) loads on the host
+    and exports RocmBackend::attention."""
+    import ctypes
+    import os
+    import subprocess
+    path = os.path.join(os.path.dirname(abi.LIB_PATH), "libsf_backend.so")
+    abi.lib()
+    ctypes.CDLL(path)
+    syms = subprocess.run(["nm", "-DC", path], capture_output=True, text=True).stdout
+    assert "sf_amd::RocmBackend::attention(" in syms
+    assert "sf_amd::RocmBackend::reserve_attention_workspace(" in syms

@@ -27,6 +27,7 @@ import torch
 from _util import assert_close_bf16, mean_rel
 from oracle import oracle as O
 from oracle import rdt as OR
+from servoflow_amd import abi
 from servoflow_amd import rdt as R
 
 pytestmark = pytest.mark.gpu
@@ -237,3 +238,74 @@ def test_full_rdt1b_shape_graph_loop():
     assert torch.isfinite(xe).all()
     assert torch.equal(xe, xg) and torch.equal(xg, xg2)
     assert float((xe - torch.from_numpy(x0).to(DEV)).abs().max()) > 0
+
+
+def _hf_checkpoint(model, path, int8_as_fp32=False):
+    """Writes model's parameters with HuggingFace naming (blocks and final
+    layer under "model.", adaptors as-is) plus entries the loader must skip,
+    the way tools/convert/hf_to_servoflow.py:41-65 expects a checkpoint."""
+    from safetensors.torch import save_file
+    tensors = {}
+    for i, (nm, dt, sh) in enumerate(model.params()):
+        v = torch.from_numpy(np.ascontiguousarray(model.param_numpy(i, dt, sh)))
+        if dt == 2:
+            v = v.to(torch.bfloat16)
+        key = nm if nm.startswith(("lang_adaptor", "img_adaptor", "state_adaptor")) else "model." + nm
+        tensors[key] = v
+    tensors["ema_model.blocks.0.norm1.weight"] = torch.zeros(3)
+    tensors["optimizer.state.0"] = torch.zeros(2)
+    tensors["action_norm.mean"] = torch.zeros(128)
+    save_file(tensors, path)
+
+
+def test_safetensors_roundtrip_bf16_model(tmp_path):
+    """A checkpoint written from one model and loaded into another gives the
+    same parameters bit for bit and the same velocity."""
+    c = small_cfg(batch=1)
+    a, b = build(c, seed=11), build(c, seed=99)
+    path = str(tmp_path / "rdt.safetensors")
+    _hf_checkpoint(a, path)
+    n = b.load_safetensors(path)
+    assert n == len(a.params())
+    for i, (nm, dt, sh) in enumerate(a.params()):
+        assert np.array_equal(a.param_numpy(i, dt, sh), b.param_numpy(i, dt, sh)), nm
+    lang, ll, img, state = make_condition(c)
+    x_t = torch.from_numpy(O.randn(5, (1, c.horizon, c.action_dim))).to(DEV)
+    outs = []
+    for m in (a, b):
+        set_cond(m, lang, ll, img, state)
+        outs.append(m.denoise_step(x_t, 0.4).cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+
+
+def test_safetensors_int8_model_quantises_rows(tmp_path):
+    c8 = small_cfg(batch=1, int8_weights=1)
+    src = build(small_cfg(batch=1), seed=13)            # bf16 weights as the checkpoint
+    dst = build(c8, seed=1)
+    path = str(tmp_path / "rdt.safetensors")
+    _hf_checkpoint(src, path)
+    dst.load_safetensors(path)
+    sd = src.state_dict()
+    checked = 0
+    for i, (nm, dt, sh) in enumerate(dst.params()):
+        if dt != abi.SF_I8:
+            continue
+        q_ref, s_ref = O.quantize_int8_rows(sd[nm])
+        q, s = dst.param_int8(i)
+        assert np.array_equal(q, q_ref) and np.array_equal(s, s_ref), nm
+        checked += 1
+    assert checked == 7 * c8.layers
+
+
+def test_safetensors_errors(tmp_path):
+    from safetensors.torch import save_file
+    c = small_cfg(batch=1)
+    m = build(c)
+    path = str(tmp_path / "partial.safetensors")
+    save_file({"model.blocks.0.norm1.weight": torch.ones(c.hidden)}, path)
+    with pytest.raises(abi.SfError, match="missing key"):
+        m.load_safetensors(path)
+    assert m.load_safetensors(path, partial=True) == 1
+    save_file({"model.blocks.0.norm1.weight": torch.ones(c.hidden + 1)}, path)
+    with pytest.raises(abi.SfError, match="shape mismatch"):
+        m.load_safetensors(path, partial=True)
