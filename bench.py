@@ -374,7 +374,7 @@ def main():
             "traffic": TRAFFIC_B1_IMAGE_BYTES,
             "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE on bench.py --profile-roofline, "
                               "profiles/cross_attention_b1_image_roofline.md",
-            "kernel": "cross-attention op (attn_split_kernel + attn_merge_kernel), 1x32x67x4374x64 "
+            "kernel": "cross-attention op (attn_ring_kernel + attn_merge_kernel), 1x32x67x4374x64 "
                       f"bf16, {img1['bytes']} algorithmic bytes per launch, {img1['us']:.2f} us",
         },
         "cpu_baseline": cpu,

@@ -37,10 +37,8 @@
 
 namespace sfk {
 
-constexpr int kKT = 128;    // keys per tile per workgroup (4 waves x 32)
 constexpr int kD = 64;      // head dim this kernel family is built for
 constexpr int kQB = 5;      // 16-row query blocks per workgroup (80 rows >= 67)
-constexpr int kThreads = 256;
 constexpr int kMaxSplits = 64;
 
 struct AttnArgs {
@@ -86,6 +84,52 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
     const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (__attribute__((address_space(3))) v4i16*)(p));
     return __builtin_bit_cast(uint2, v);
+}
+
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+
+// Eight ds_read_b64_tr_b16 at LDS byte addresses addr[0..7], then a wait for
+// them.  Written as one asm block because the compiler treats the builtin
+// form as a possible alias of buffer_load ... lds writes still in flight and
+// puts an s_waitcnt vmcnt(0) in front of it, which in the ring kernel would
+// wait for the NEXT tile's loads before the current tile is contracted.  The
+// caller has already waited for the stage being read (ring_wait_barrier).
+// Early-clobber outputs: a result register must not double as an address
+// that a later read of the batch still has to send.
+__device__ __forceinline__ void lds_read_tr16_x8(u32x2v (&o)[8], const uint32_t (&addr)[8]) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %8\n\t"
+        "ds_read_b64_tr_b16 %1, %9\n\t"
+        "ds_read_b64_tr_b16 %2, %10\n\t"
+        "ds_read_b64_tr_b16 %3, %11\n\t"
+        "ds_read_b64_tr_b16 %4, %12\n\t"
+        "ds_read_b64_tr_b16 %5, %13\n\t"
+        "ds_read_b64_tr_b16 %6, %14\n\t"
+        "ds_read_b64_tr_b16 %7, %15\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]),
+          "=&v"(o[6]), "=&v"(o[7])
+        : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]),
+          "v"(addr[6]), "v"(addr[7])
+        : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)(p);
+}
+
+// max(x, x of lane ^ 16) and max(x, x of lane ^ 32) with the VALU lane swaps
+// of gfx950 (v_permlane16/32_swap with both operands x: the two results hold,
+// per lane, x of this row and of the partner row).  A ds_bpermute here would
+// be an LDS instruction, in front of which the compiler also waits for the
+// ring's in-flight DMA.
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 
 // Shared epilogue of the split kernels: row sums, then the four waves'
@@ -211,6 +255,7 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
 // l sums exactly the (hi + lo) weights the numerator uses.
 // ---------------------------------------------------------------------------
 constexpr int kRingStages = 2;
+constexpr int kKT = 128;                          // keys per tile (4 waves x 32)
 constexpr int kTileBytes = kKT * kD * 2;          // 16 KB per K (or V) tile
 constexpr int kStageBytes = 2 * kTileBytes;       // K then V
 
@@ -223,16 +268,15 @@ __device__ __forceinline__ uint32_t mask_word(__amdgpu_buffer_rsrc_t mrs, int ke
     return __builtin_amdgcn_raw_buffer_load_b32(mrs, (uint32_t)key, 0, 0);
 }
 
-// Wait until at most n of this wave's vector-memory ops are outstanding,
-// then barrier.  n is 0, 8, 16 or 24 (tiles still in flight x 8).
-__device__ __forceinline__ void ring_wait_barrier(int n) {
-    if (n >= 24) asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
-    else if (n >= 16) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-    else if (n >= 8) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+// Wait until at most one tile's loads (8 per wave) of this wave are still
+// outstanding, then barrier: every wave's share of the older tile has landed.
+// Vector loads complete in issue order, so this covers the tile being
+// waited for and every load issued before it (Q, mask words).
+__device__ __forceinline__ void ring_wait_barrier() {
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
 }
 
-__global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     constexpr int QR = 16 * kQB;
     __shared__ __attribute__((aligned(16))) char ring[kRingStages * kStageBytes];
 
@@ -307,8 +351,32 @@ __global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a
                 voff, 0, 0, 0);
         }
     };
-    const int first = min(ntiles, kRingStages);
-    for (int t = 0; t < first; ++t) issue(t);
+    // Key-padding mask words of tile t, loaded one tile ahead and always
+    // BEFORE the next tile's DMA is issued: vector loads complete in issue
+    // order, so the wait the compiler puts in front of their first use then
+    // never covers a tile still streaming in.
+    auto load_mask = [&](int t, uint32_t (&mw)[2]) {
+        const int kt = kbeg + t * kKT;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) mw[kb] = mask_word(mrs, kt + 32 * w + 16 * kb + 4 * g);
+    };
+    uint32_t mw_next[2] = {0xffffffffu, 0xffffffffu};
+    if (a.kv_mask) load_mask(0, mw_next);
+    // Exactly one tile is issued per stage use, whether or not it exists:
+    // tiles at or past ntiles lie beyond the buffer range and load zeros (no
+    // memory traffic).  With the issue unconditional, the compiler's own
+    // vmcnt bookkeeping sees the ring loads as always in flight behind Q and
+    // the mask words, and ring_wait_barrier waits for one tile at a time.
+    issue(0);
+    issue(1);
+    // Wait for the Q fragments here, behind the first tiles' loads.  Inside
+    // the tile loop the compiler would otherwise still count them as
+    // outstanding and wait for every in-flight ring load before the first
+    // S contraction of each tile.
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) asm volatile("" ::"v"(qf[qb][hh]));
 
     f32x4 acc[kQB][4];   // O^T blocks: lane holds d = 16db + 4g + i, q = 16qb + r
     f32x4 accl[kQB];     // row sums: element 0 of lanes 0..15 holds l of query 16qb + r
@@ -346,7 +414,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a
 
     for (int t = 0; t < ntiles; ++t) {
         const int kt = kbeg + t * kKT;
-        ring_wait_barrier(8 * min(kRingStages - 1, ntiles - 1 - t));
+        ring_wait_barrier();   // tile t has landed; tile t + 1 may still stream in
         const char* st = ring + (t % kRingStages) * kStageBytes;
         if (kt + wkey < kend && !(a.causal && kt + wkey > q0 + QR - 1)) {
             bf16x8 kf[2][2];
@@ -356,18 +424,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a
                 for (int hh = 0; hh < 2; ++hh)
                     kf[kb][hh] = *reinterpret_cast<const bf16x8*>(st + koffs[kb][hh]);
             bf16x8 vf[4];
+            {
+                const uint32_t sbase = lds_addr(st);
+                uint32_t va[8];
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const uint2 lo4 = lds_read_tr16(reinterpret_cast<const uint16_t*>(st + voffs[0][db]));
-                const uint2 hi4 = lds_read_tr16(reinterpret_cast<const uint16_t*>(st + voffs[1][db]));
-                vf[db] = u32x4_as_bf16x8(u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
+                for (int db = 0; db < 4; ++db) {
+                    va[2 * db] = sbase + voffs[0][db];
+                    va[2 * db + 1] = sbase + voffs[1][db];
+                }
+                u32x2v vt[8];
+                lds_read_tr16_x8(vt, va);
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+                    vf[db] = u32x4_as_bf16x8(u32x4{vt[2 * db][0], vt[2 * db][1], vt[2 * db + 1][0],
+                                                   vt[2 * db + 1][1]});
             }
             const bool need_mask = a.causal || kt + kKT > kend || a.kv_mask;
-            uint32_t mw[2] = {0xffffffffu, 0xffffffffu};
-            if (a.kv_mask) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) mw[kb] = mask_word(mrs, kt + wkey + 16 * kb + 4 * g);
-            }
+            const uint32_t mw[2] = {mw_next[0], mw_next[1]};
             f32x4 s[kQB][2];
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb) {
@@ -402,10 +475,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a
                                fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
             }
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) mx[qb] = fmaxf(mx[qb], __shfl_xor(mx[qb], 16, 64));
+            for (int qb = 0; qb < kQB; ++qb) mx[qb] = max_xor16(mx[qb]);
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb)
-                mx[qb] = fmaxf(mx[qb], __shfl_xor(mx[qb], 32, 64)) * a.scale_log2;
+            for (int qb = 0; qb < kQB; ++qb) mx[qb] = max_xor32(mx[qb]) * a.scale_log2;
             bool grow = false;
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb) grow |= mx[qb] > m[qb] + 8.f;
@@ -451,8 +523,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_ring_kernel(const AttnArgs a
         }   // live keys
         // every wave is done with this stage before it is refilled
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (t + kRingStages < ntiles) issue(t + kRingStages);
+        if (a.kv_mask) load_mask(t + 1, mw_next);
+        issue(t + kRingStages);
     }
+    // The loads issued past the last tile land in LDS that the epilogue
+    // reuses: every wave waits for its own, then all waves meet.
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) l[qb] = __shfl(accl[qb][0], r, 64);
     attn_split_epilogue(a, reinterpret_cast<float*>(ring), acc, m, l, w, g, r, lane, b, h, q0,
@@ -673,8 +749,10 @@ using sfk::kMaxSplits;
 int query_chunks(const sf_attn_desc* d) { return (d->Sq + 16 * sfk::kQB - 1) / (16 * sfk::kQB); }
 
 // MI355X has 256 CUs and the ring kernel runs two workgroups per CU (64 KB
-// LDS ring each).  Splits are chosen so the grid is one round of
-// workgroups, each split covering at least one 128-key tile.
+// LDS ring each).  When B*H*query-chunks alone fills the CUs the keys are not
+// split (no partials, no merge pass: measured faster at B = 8 and 16 than two
+// splits); otherwise splits make the grid one round of workgroups, each split
+// covering at least one 128-key tile.
 constexpr long kNumCUs = 256;
 constexpr long kWgPerCU = 2;
 
@@ -682,6 +760,7 @@ int choose_splits(const sf_attn_desc* d) {
     if (d->num_splits > 0) return d->num_splits < kMaxSplits ? d->num_splits : kMaxSplits;
     const long base = (long)d->B * d->H * query_chunks(d);
     if (base <= 0) return 1;
+    if (base >= kNumCUs) return 1;
     long ns = kNumCUs * kWgPerCU / base;
     const long cap = d->Sk / 128;
     if (ns > cap) ns = cap;
@@ -799,8 +878,7 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         else hipLaunchKernelGGL(sfk::attn_short_kernel<8>, grid, dim3(64), 0, s, a);
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
     }
-    hipLaunchKernelGGL(sfk::attn_ring_kernel, dim3(ns * nqc, d->H, d->B), dim3(sfk::kThreads), 0,
-                       s, a);
+    hipLaunchKernelGGL(sfk::attn_ring_kernel, dim3(ns * nqc, d->H, d->B), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     if (ns > 1) {
         hipLaunchKernelGGL(sfk::attn_merge_kernel, dim3((d->Sq + 3) / 4, d->H, d->B), dim3(256), 0,

@@ -98,6 +98,20 @@ def test_split_count_invariance(ns):
     assert_close_bf16(got, O.attention_f32(q, k, v), f"num_splits={ns}")
 
 
+@pytest.mark.parametrize("ns", [8, 9])
+def test_ring_variants_image_b1(ns):
+    """num_splits = 8 gives 256 workgroups (the 8-wave ring kernel, one per
+    CU), 9 gives 288 (the 4-wave kernel, two per CU); both against the
+    oracle, with and without valid lengths."""
+    q = rounded(155, (1, 32, 67, 64))
+    k, v = rounded(156, (1, 32, 4374, 64)), rounded(157, (1, 32, 4374, 64))
+    got = run(q, k, v, num_splits=ns)
+    assert_close_bf16(got, O.attention_f32(q, k, v), f"img B=1 num_splits={ns}")
+    vl = np.array([3001], np.int32)
+    got = run(q, k, v, num_splits=ns, valid_len=to_dev(vl, torch.int32))
+    assert_close_bf16(got, O.attention_f32(q, k, v, valid_len=vl), f"img B=1 num_splits={ns} valid=3001")
+
+
 def test_causal_matches_oracle():
     q, k, v = (rounded(s, (1, 4, 67, 64)) for s in (161, 162, 163))
     got = run(q, k, v, is_causal=True)
