@@ -85,7 +85,9 @@ def time_graph(fn, steps, warmup, reps=20):
     return start.elapsed_time(stop) / (steps * reps)
 
 
-def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32):
+def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=False):
+    """Graph-timed cross-attention op (exact_pv: the bf16 (hi, lo) P.V form
+    instead of the default fp16 one)."""
     import numpy as np
     import torch
 
@@ -104,7 +106,7 @@ def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32):
         vl = torch.from_numpy(np.asarray(valid, np.int32)).to(dev)
     desc = make_desc(q, k, v, out, valid_len=vl)
     ws = torch.zeros(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=dev)
-    fn = lambda: attention(q, k, v, out=out, valid_len=vl, workspace=ws)  # noqa: E731
+    fn = lambda: attention(q, k, v, out=out, valid_len=vl, workspace=ws, exact_pv=exact_pv)  # noqa: E731
     ms = time_graph(fn, steps, warmup)
     sk_total = B * Sk if valid is None else int(np.sum(valid))
     nbytes = attn_bytes(B, H, Sq, sk_total)

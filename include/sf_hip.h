@@ -77,6 +77,15 @@ typedef enum sf_dtype {
  * implementations ignore.
  * num_splits: 0 chooses the split-K factor automatically; n > 0 forces n
  * (at most 64).
+ * exact_pv: 0 (default) runs the key-split kernel's (Sk > 128) P.V
+ * contraction in fp16: V converted exactly (bf16's 8 significant bits fit
+ * fp16's 11 below 2^16) and P rounded toward zero to fp16, ~2.4e-4 mean
+ * relative error on the output.  V must then hold |v| < 2^16: a workgroup
+ * that meets a larger or infinite value writes NaN to its output rows (to
+ * its split's partials, which the merge turns into NaN rows) instead of a
+ * saturated result; a NaN in V propagates as in fp32 arithmetic.  1 keeps V
+ * in bf16 and P as a bf16 (hi, lo) pair (~1e-5) for any finite V, at ~15%
+ * more time per key tile.
  * scale must be >= 0 (SF_ENOTSUP otherwise).
  *
  * Supported: in_dtype SF_BF16, out_dtype SF_BF16 or SF_F32, D == 64,
@@ -96,6 +105,7 @@ typedef struct sf_attn_desc {
     int64_t o_stride[3];
     const uint8_t* kv_mask;
     int64_t kv_mask_stride;
+    int32_t exact_pv;
 } sf_attn_desc;
 
 /* Fills a descriptor for contiguous [B,H,S,D] tensors (the layout

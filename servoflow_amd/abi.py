@@ -47,6 +47,7 @@ class AttnDesc(ctypes.Structure):
         ("o_stride", ctypes.c_int64 * 3),
         ("kv_mask", ctypes.c_void_p),
         ("kv_mask_stride", ctypes.c_int64),
+        ("exact_pv", ctypes.c_int32),
     ]
 
 

@@ -23,7 +23,8 @@ def _strides3(t: torch.Tensor):
     return (t.stride(0), t.stride(1), t.stride(2))
 
 
-def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_splits=0, kv_mask=None):
+def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_splits=0, kv_mask=None,
+              exact_pv=False):
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     if k.shape != (B, H, Sk, D) or v.shape != (B, H, Sk, D) or out.shape != (B, H, Sq, D):
@@ -46,6 +47,7 @@ def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_spli
             raise ValueError("kv_mask must be a device bool/uint8 tensor [B, Sk] with contiguous rows")
         d.kv_mask = kv_mask.data_ptr()
         d.kv_mask_stride = kv_mask.stride(0)
+    d.exact_pv = 1 if exact_pv else 0
     for name, t in (("q_stride", q), ("k_stride", k), ("v_stride", v), ("o_stride", out)):
         getattr(d, name)[:] = _strides3(t)
     return d
@@ -56,14 +58,16 @@ def workspace_bytes(desc) -> int:
 
 
 def attention(q, k, v, out=None, scale=0.0, is_causal=False, valid_len=None, num_splits=0,
-              out_dtype=None, workspace=None, stream=None, kv_mask=None):
+              out_dtype=None, workspace=None, stream=None, kv_mask=None, exact_pv=False):
     """Runs sf_attn_fwd on torch's current stream (or `stream`) and returns `out`.
     kv_mask: optional device bool [B, Sk] key-padding mask (True = attend);
-    its rows must be readable for Sk rounded up to 4 bytes."""
+    its rows must be readable for Sk rounded up to 4 bytes.
+    exact_pv: bf16 V and P as a bf16 (hi, lo) pair instead of the fp16 P.V
+    contraction (which needs finite |V| < 2^16; see sf_attn_desc)."""
     if out is None:
         od = out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=od, device=q.device)
-    desc = make_desc(q, k, v, out, scale, is_causal, valid_len, num_splits, kv_mask)
+    desc = make_desc(q, k, v, out, scale, is_causal, valid_len, num_splits, kv_mask, exact_pv)
     need = workspace_bytes(desc)
     if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)   # needs no init

@@ -88,12 +88,13 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
 
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 
-// Eight ds_read_b64_tr_b16 at LDS byte addresses addr[0..7], then a wait for
-// them.  Written as one asm block because the compiler treats the builtin
-// form as a possible alias of buffer_load ... lds writes still in flight and
-// puts an s_waitcnt vmcnt(0) in front of it, which in the ring kernel would
-// wait for the NEXT tile's loads before the current tile is contracted.  The
-// caller has already waited for the stage being read (ring_wait_barrier).
+// LDS reads of the ring kernel are written as asm: the compiler treats the
+// builtin and plain forms as possible aliases of buffer_load ... lds writes
+// still in flight and puts an s_waitcnt vmcnt(0) in front of them, which
+// would wait for the NEXT tile's loads before the current tile is
+// contracted (the caller has already waited for the stage it reads).  The
+// asm reads do not wait: an explicit s_waitcnt asm that names them ties the wait for a batch of
+// them to their result registers, so no use can be scheduled before it.
 // Early-clobber outputs: a result register must not double as an address
 // that a later read of the batch still has to send.
 __device__ __forceinline__ void lds_read_tr16_x8(u32x2v (&o)[8], const uint32_t (&addr)[8]) {
@@ -105,8 +106,7 @@ __device__ __forceinline__ void lds_read_tr16_x8(u32x2v (&o)[8], const uint32_t 
         "ds_read_b64_tr_b16 %4, %12\n\t"
         "ds_read_b64_tr_b16 %5, %13\n\t"
         "ds_read_b64_tr_b16 %6, %14\n\t"
-        "ds_read_b64_tr_b16 %7, %15\n\t"
-        "s_waitcnt lgkmcnt(0)"
+        "ds_read_b64_tr_b16 %7, %15"
         : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]),
           "=&v"(o[6]), "=&v"(o[7])
         : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]),
@@ -116,6 +116,18 @@ __device__ __forceinline__ void lds_read_tr16_x8(u32x2v (&o)[8], const uint32_t 
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)(p);
+}
+
+// Four ds_read_b128 (the wave's K fragments of a ring stage), no wait.
+__device__ __forceinline__ void lds_read_b128_x4(u32x4 (&o)[4], const uint32_t (&addr)[4]) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %5\n\t"
+        "ds_read_b128 %2, %6\n\t"
+        "ds_read_b128 %3, %7"
+        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3])
+        : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3])
+        : "memory");
 }
 
 // max(x, x of lane ^ 16) and max(x, x of lane ^ 32) with the VALU lane swaps
@@ -139,7 +151,7 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
                                                     f32x4 (&acc)[kQB][4], float (&m)[kQB],
                                                     float (&l)[kQB], int w, int g, int r, int lane,
                                                     int b, int h, int q0, int split, int nsplit,
-                                                    bool l_per_lane = true) {
+                                                    bool l_per_lane = true, bool poison = false) {
     constexpr int QR = 16 * kQB;
     // ---- Row sums: each lane summed its own 8 keys per tile; add the four
     //      lane groups that share a query.
@@ -210,23 +222,31 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
                 }
                 const int q = q0 + 16 * qb + r;
                 if (q >= a.Sq) continue;
+                // poison: quiet-NaN bit patterns (written as integers: the
+                // kernels are compiled on the assumption of no NaN arithmetic)
+                constexpr uint32_t kNaN32 = 0x7fc00000u, kNaN16x2 = 0x7fc07fc0u;
                 if (nsplit == 1) {
                     const float inv = Lq[qb] > 0.f ? 1.f / Lq[qb] : 0.f;
                     o *= inv;
                     const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + d0;
                     if (a.out_f32) {
-                        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.o) + off) = o;
+                        u32x4 ob = __builtin_bit_cast(u32x4, o);
+                        if (poison) ob = u32x4{kNaN32, kNaN32, kNaN32, kNaN32};
+                        *reinterpret_cast<u32x4*>(reinterpret_cast<float*>(a.o) + off) = ob;
                     } else {
                         uint2 pk2;
-                        pk2.x = pack_bf16x2(o[0], o[1]);
-                        pk2.y = pack_bf16x2(o[2], o[3]);
+                        pk2.x = poison ? kNaN16x2 : pack_bf16x2(o[0], o[1]);
+                        pk2.y = poison ? kNaN16x2 : pack_bf16x2(o[2], o[3]);
                         *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.o) + off) = pk2;
                     }
                 } else {
-                    *reinterpret_cast<f32x4*>(a.part_o + (pbase + q) * kD + d0) = o;
+                    u32x4 ob = __builtin_bit_cast(u32x4, o);
+                    if (poison) ob = u32x4{kNaN32, kNaN32, kNaN32, kNaN32};
+                    *reinterpret_cast<u32x4*>(a.part_o + (pbase + q) * kD + d0) = ob;
                     if (w == 0 && g == 0) {
-                        a.part_ml[(pbase + q) * 2 + 0] = Mq[qb];
-                        a.part_ml[(pbase + q) * 2 + 1] = Lq[qb];
+                        uint32_t* ml = reinterpret_cast<uint32_t*>(a.part_ml + (pbase + q) * 2);
+                        ml[0] = poison ? kNaN32 : __float_as_uint(Mq[qb]);
+                        ml[1] = poison ? kNaN32 : __float_as_uint(Lq[qb]);
                     }
                 }
             }
@@ -276,6 +296,7 @@ __device__ __forceinline__ void ring_wait_barrier() {
     asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
 }
 
+template <bool kExactPV>   // false: P.V in fp16 (V exact below 2^16); true: bf16 V, P as (hi, lo)
 __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     constexpr int QR = 16 * kQB;
     __shared__ __attribute__((aligned(16))) char ring[kRingStages * kStageBytes];
@@ -391,6 +412,9 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     // A operand whose row 0 is all ones (rows 1..15 zero)
     const uint32_t one2 = r == 0 ? 0x3f803f80u : 0u;
     const bf16x8 ones = u32x4_as_bf16x8(u32x4{one2, one2, one2, one2});
+    const uint32_t oneh = r == 0 ? 0x3c003c00u : 0u;
+    const f16x8 ones_f16 = u32x4_as_f16x8(u32x4{oneh, oneh, oneh, oneh});
+    bool v_out_of_range = false;   // fp16 form: some |v| >= 2^16 (inf included)
 
     const int wkey = 32 * w;   // this wave's first key inside a tile
     // per-lane LDS byte offsets inside a stage (swizzled rows)
@@ -417,13 +441,16 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
         ring_wait_barrier();   // tile t has landed; tile t + 1 may still stream in
         const char* st = ring + (t % kRingStages) * kStageBytes;
         if (kt + wkey < kend && !(a.causal && kt + wkey > q0 + QR - 1)) {
-            bf16x8 kf[2][2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
-                    kf[kb][hh] = *reinterpret_cast<const bf16x8*>(st + koffs[kb][hh]);
-            bf16x8 vf[4];
+            // K fragments, then V^T: K is waited for before the S contraction,
+            // V^T only before P.V, so the transpose reads overlap S.
+            u32x4 kw[4];
+            {
+                const uint32_t sbase = lds_addr(st);
+                const uint32_t ka[4] = {sbase + koffs[0][0], sbase + koffs[0][1], sbase + koffs[1][0],
+                                        sbase + koffs[1][1]};
+                lds_read_b128_x4(kw, ka);
+            }
+            u32x2v vt[8];
             {
                 const uint32_t sbase = lds_addr(st);
                 uint32_t va[8];
@@ -432,13 +459,16 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                     va[2 * db] = sbase + voffs[0][db];
                     va[2 * db + 1] = sbase + voffs[1][db];
                 }
-                u32x2v vt[8];
                 lds_read_tr16_x8(vt, va);
-#pragma unroll
-                for (int db = 0; db < 4; ++db)
-                    vf[db] = u32x4_as_bf16x8(u32x4{vt[2 * db][0], vt[2 * db][1], vt[2 * db + 1][0],
-                                                   vt[2 * db + 1][1]});
+                // K landed (LDS reads return in order; no scalar loads are in
+                // flight in the loop, so the count is exact); V^T may not have
+                asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(kw[0]), "+v"(kw[1]), "+v"(kw[2]), "+v"(kw[3]) :: "memory");
             }
+            bf16x8 kf[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) kf[kb][hh] = u32x4_as_bf16x8(kw[2 * kb + hh]);
             const bool need_mask = a.causal || kt + kKT > kend || a.kv_mask;
             const uint32_t mw[2] = {mw_next[0], mw_next[1]};
             f32x4 s[kQB][2];
@@ -492,33 +522,77 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                     for (int db = 0; db < 4; ++db) acc[qb][db] *= alpha;
                 }
             }
+            // V^T fragments: bf16 as read (exact form), or converted to fp16,
+            // which is exact for |v| < 2^16 (bf16's 8 significant bits fit
+            // fp16's 11); the lane notes any larger value (a NaN, which the
+            // max ignores, propagates through the arithmetic instead).
+            bf16x8 vf[4];
+            f16x8 vh[4];
+            {
+                // V^T landed
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vt[0]), "+v"(vt[1]), "+v"(vt[2]), "+v"(vt[3]),
+                             "+v"(vt[4]), "+v"(vt[5]), "+v"(vt[6]), "+v"(vt[7]) :: "memory");
+                float vmax = 0.f;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const u32x4 vw = {vt[2 * db][0], vt[2 * db][1], vt[2 * db + 1][0], vt[2 * db + 1][1]};
+                    if constexpr (kExactPV) {
+                        vf[db] = u32x4_as_bf16x8(vw);
+                    } else {
+                        u32x4 hw;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float lo = __uint_as_float(vw[e] << 16);
+                            const float hi = __uint_as_float(vw[e] & 0xffff0000u);
+                            hw[e] = pack_f16x2_rtz(lo, hi);
+                            vmax = fmaxf(vmax, fmaxf(fabsf(lo), fabsf(hi)));
+                        }
+                        vh[db] = u32x4_as_f16x8(hw);
+                    }
+                }
+                if constexpr (!kExactPV) v_out_of_range |= !(vmax < 65536.f);
+            }
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb) {
                 const float nmuse = m[qb] == -INFINITY ? 0.f : -m[qb];
-                uint32_t pb[8], lb[8];
+                if constexpr (!kExactPV) {
+                    // P rounded toward zero to fp16 (P <= 2^8 by the lazy
+                    // rescale; ~2.4e-4 mean relative error on the output); l
+                    // sums the same rounded weights.
+                    float pf[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float p = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nmuse));
-                    pb[j] = __float_as_uint(p);
-                    lb[j] = __float_as_uint(p - __uint_as_float(pb[j] & 0xffff0000u));
-                }
-                const u32x4 phw = {__builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u),
-                                   __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
-                                   __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u),
-                                   __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)};
-                const u32x4 plw = {__builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u),
-                                   __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u),
-                                   __builtin_amdgcn_perm(lb[5], lb[4], 0x07060302u),
-                                   __builtin_amdgcn_perm(lb[7], lb[6], 0x07060302u)};
-                const bf16x8 ph8 = u32x4_as_bf16x8(phw);
-                const bf16x8 pl8 = u32x4_as_bf16x8(plw);
+                    for (int j = 0; j < 8; ++j) pf[j] = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nmuse));
+                    const f16x8 p8 = u32x4_as_f16x8(u32x4{pack_f16x2_rtz(pf[0], pf[1]), pack_f16x2_rtz(pf[2], pf[3]),
+                                                          pack_f16x2_rtz(pf[4], pf[5]), pack_f16x2_rtz(pf[6], pf[7])});
 #pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    acc[qb][db] = mfma16x16x32(vf[db], ph8, acc[qb][db]);
-                    acc[qb][db] = mfma16x16x32(vf[db], pl8, acc[qb][db]);
-                }
-                accl[qb] = mfma16x16x32(ones, ph8, accl[qb]);
-                accl[qb] = mfma16x16x32(ones, pl8, accl[qb]);
+                    for (int db = 0; db < 4; ++db) acc[qb][db] = mfma16x16x32_f16(vh[db], p8, acc[qb][db]);
+                    accl[qb] = mfma16x16x32_f16(ones_f16, p8, accl[qb]);
+                } else {
+                    uint32_t pb[8], lb[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float p = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nmuse));
+                        pb[j] = __float_as_uint(p);
+                        lb[j] = __float_as_uint(p - __uint_as_float(pb[j] & 0xffff0000u));
+                    }
+                    const u32x4 phw = {__builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u),
+                                       __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
+                                       __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u),
+                                       __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)};
+                    const u32x4 plw = {__builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u),
+                                       __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u),
+                                       __builtin_amdgcn_perm(lb[5], lb[4], 0x07060302u),
+                                       __builtin_amdgcn_perm(lb[7], lb[6], 0x07060302u)};
+                    const bf16x8 ph8 = u32x4_as_bf16x8(phw);
+                    const bf16x8 pl8 = u32x4_as_bf16x8(plw);
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) {
+                        acc[qb][db] = mfma16x16x32(vf[db], ph8, acc[qb][db]);
+                        acc[qb][db] = mfma16x16x32(vf[db], pl8, acc[qb][db]);
+                    }
+                    accl[qb] = mfma16x16x32(ones, ph8, accl[qb]);
+                    accl[qb] = mfma16x16x32(ones, pl8, accl[qb]);
+                            }
             }
         }   // live keys
         // every wave is done with this stage before it is refilled
@@ -531,8 +605,11 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) l[qb] = __shfl(accl[qb][0], r, 64);
+    // V outside the fp16 form's range anywhere in this workgroup's keys: its
+    // rows (or split partials) become NaN rather than silently saturated.
+    const bool poison = !kExactPV && __syncthreads_or(v_out_of_range);
     attn_split_epilogue(a, reinterpret_cast<float*>(ring), acc, m, l, w, g, r, lane, b, h, q0,
-                        split, nsplit, false);
+                        split, nsplit, false, poison);
 }
 
 // Log-sum-exp merge of the split partials.  One wave per output row
@@ -551,10 +628,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     // first kMergeBatch splits' partial outputs
     constexpr int kMergeBatch = 16;
     float ms = -INFINITY, ls = 0.f;
+    bool poisoned = false;   // a split marked its partials NaN (V out of range)
     if (lane < ns) {
         const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (row0 + (size_t)lane * a.Sq) * 2);
         ms = ml.x;
         ls = ml.y;
+        poisoned = (__float_as_uint(ml.y) & 0x7fffffffu) > 0x7f800000u;
     }
     float v0[kMergeBatch];
 #pragma unroll
@@ -580,6 +659,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
             v[j] = s0 + j < ns ? a.part_o[(row0 + (size_t)(s0 + j) * a.Sq) * kD + lane] : 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o += __shfl(wgt, s0 + j < ns ? s0 + j : 0, 64) * v[j];
+    }
+    if (__any(poisoned)) {   // NaN bits written as integers (no-NaN arithmetic assumed)
+        const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + lane;
+        if (a.out_f32) reinterpret_cast<uint32_t*>(a.o)[off] = 0x7fc00000u;
+        else reinterpret_cast<uint16_t*>(a.o)[off] = 0x7fc0u;
+        return;
     }
     store_out(a, b, h, q, lane, o);
 }
@@ -878,7 +963,10 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         else hipLaunchKernelGGL(sfk::attn_short_kernel<8>, grid, dim3(64), 0, s, a);
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
     }
-    hipLaunchKernelGGL(sfk::attn_ring_kernel, dim3(ns * nqc, d->H, d->B), dim3(256), 0, s, a);
+    if (d->exact_pv)
+        hipLaunchKernelGGL(sfk::attn_ring_kernel<true>, dim3(ns * nqc, d->H, d->B), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(sfk::attn_ring_kernel<false>, dim3(ns * nqc, d->H, d->B), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     if (ns > 1) {
         hipLaunchKernelGGL(sfk::attn_merge_kernel, dim3((d->Sq + 3) / 4, d->H, d->B), dim3(256), 0,

@@ -51,6 +51,23 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f16x8 u32x4_as_f16x8(u32x4 v) {
+    return __builtin_bit_cast(f16x8, v);
+}
+
+// Two fp32 -> packed fp16x2 (low half = a), rounded toward zero
+// (v_cvt_pkrtz_f16_f32); values beyond the fp16 range saturate to +-65504.
+__device__ __forceinline__ uint32_t pack_f16x2_rtz(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
+// The fp16 form of mfma16x16x32, same operand layout.
+__device__ __forceinline__ f32x4 mfma16x16x32_f16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 // Raw buffer resource over [base, base + bytes): loads past `bytes` return 0.
 // Word 3 = 0x00020000 is the raw-buffer format for the gfx9 family (gfx950).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
