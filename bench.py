@@ -37,9 +37,10 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per roofline op measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (x2.0 / x1.0, scales read off a 256 MiB copy kernel) on `bench.py
 # --profile-roofline`: ring kernel 38.32 MB read + 9.07 MB written, merge
-# 10.11 MB read + 0.27 MB written (profiles/cross_attention_b1_image_roofline.md).
+# 10.11 MB read + 0.27 MB written (profiles/cross_attention_image_roofline.md).
 # Re-measured whenever the attention kernels change.
-TRAFFIC_B1_IMAGE_BYTES = 57779046
+TRAFFIC_B1_IMAGE_BYTES = 57821027
+TRAFFIC_B8_IMAGE_BYTES = 291360997   # same profile, batch-8 op (no key split)
 
 
 def attn_bytes(B, H, Sq, Sk_valid_total, D=64, eb=2):
@@ -262,6 +263,7 @@ def cpu_baseline(budget_s=25.0):
 def profile_roofline(iters=50):
     """Runs only what the roofline profiles measure: the batch-1 image
     cross-attention op (attn_ring_kernel + attn_merge_kernel) `iters` times,
+    the batch-8 one (attn_ring_kernel alone: no key split) `iters` times,
     then a plain 256 MiB device-to-device copy `iters` times -- the
     calibration kernel whose FETCH_SIZE / WRITE_SIZE per dispatch give the
     counter's scale (256 MiB read, 256 MiB written).  Eager launches, so each
@@ -282,6 +284,15 @@ def profile_roofline(iters=50):
         attention(q, k, v, out=out, workspace=ws)
     torch.cuda.synchronize()
     print(f"profile: {iters} cross-attention ops 1x32x67x4374x64 done", flush=True)
+    q8 = torch.randn(8, 32, 67, 64, device=dev, generator=g).to(torch.bfloat16)
+    k8 = torch.randn(8, 32, 4374, 64, device=dev, generator=g).to(torch.bfloat16)
+    v8 = torch.randn(8, 32, 4374, 64, device=dev, generator=g).to(torch.bfloat16)
+    out8 = torch.empty(8, 67, 32, 64, device=dev, dtype=torch.bfloat16).permute(0, 2, 1, 3)
+    ws8 = torch.empty(max(workspace_bytes(make_desc(q8, k8, v8, out8)), 16), dtype=torch.uint8, device=dev)
+    for _ in range(iters):
+        attention(q8, k8, v8, out=out8, workspace=ws8)
+    torch.cuda.synchronize()
+    print(f"profile: {iters} cross-attention ops 8x32x67x4374x64 done", flush=True)
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(iters):
@@ -333,10 +344,19 @@ def main():
         lang8 = bench_attention(8, 1024, att_steps, args.warmup, valid=lv8)
         lang1 = bench_attention(1, 1024, att_steps, args.warmup, valid=[517])
         self1 = bench_attention(1, 67, att_steps, args.warmup)
+        img16 = bench_attention(16, 4374, att_steps, args.warmup)
+        img1x = bench_attention(1, 4374, att_steps, args.warmup, exact_pv=True)
+        img8x = bench_attention(8, 4374, att_steps, args.warmup, exact_pv=True)
         extra.update({
             "cross_img_b8_us": round(img8["us"], 3),
             "cross_img_b8_GBps": round(img8["GBps"], 1),
             "cross_img_b8_frac": round(img8["frac"], 4),
+            "cross_img_b8_traffic": TRAFFIC_B8_IMAGE_BYTES,
+            "cross_img_b16_us": round(img16["us"], 3),
+            "cross_img_b16_frac": round(img16["frac"], 4),
+            "cross_img_b1_exact_pv_us": round(img1x["us"], 3),
+            "cross_img_b8_exact_pv_us": round(img8x["us"], 3),
+            "cross_img_b8_exact_pv_frac": round(img8x["frac"], 4),
             "cross_lang_b8_us": round(lang8["us"], 3),
             "cross_lang_b8_GBps": round(lang8["GBps"], 1),
             "cross_lang_b1_L517_us": round(lang1["us"], 3),
@@ -375,8 +395,8 @@ def main():
             "frac": round(img1["frac"], 4),
             "traffic": TRAFFIC_B1_IMAGE_BYTES,
             "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE on bench.py --profile-roofline, "
-                              "profiles/cross_attention_b1_image_roofline.md",
-            "kernel": "cross-attention op (attn_ring_kernel + attn_merge_kernel), 1x32x67x4374x64 "
+                              "profiles/cross_attention_image_roofline.md",
+            "kernel": "cross-attention op (attn_ring_kernel, fp16 P.V form, + attn_merge_kernel), 1x32x67x4374x64 "
                       f"bf16, {img1['bytes']} algorithmic bytes per launch, {img1['us']:.2f} us",
         },
         "cpu_baseline": cpu,
