@@ -264,15 +264,17 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Workgroup (blockIdx.x, blockIdx.y, blockIdx.z) = (16*NW-row weight tile,
-// KT-wide K slice, 16*MB-row activation tile); NW waves share the LDS copy
-// of the activation slice.  Lane (g4 = lane/16, r = lane%16) of wave w
-// supplies weight row 16w + r and activation row 16mb + r, k = 32t + 8g4
-// .. +7 of MFMA step t; its accumulator holds C^T[16w + 4g4 + i][16mb + r].
-template <int MB, int KT, int NW, bool W8>
+// Workgroup (blockIdx.x, blockIdx.y, blockIdx.z) = (16*NW*NB-row weight
+// tile, KT-wide K slice, 16*MB-row activation tile); NW waves share the LDS
+// copy of the activation slice, and each wave contracts NB 16-row weight
+// blocks against every activation fragment it reads from LDS.  Lane
+// (g4 = lane/16, r = lane%16) of wave w supplies weight rows
+// 16(NB w + nb) + r and activation row 16mb + r, k = 32t + 8g4 .. +7 of MFMA
+// step t; accumulator [nb][mb] holds C^T[16(NB w + nb) + 4g4 + i][16mb + r].
+template <int MB, int KT, int NW, bool W8, int NB>
 __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
     constexpr int kSkThreads = 64 * NW;
-    constexpr int kSkRows = 16 * NW;
+    constexpr int kSkRows = 16 * NW * NB;     // weight rows (output columns) per workgroup
     constexpr int MR = 16 * MB;
     constexpr int PITCH = 2 * KT + 16;       // bytes per LDS activation row (+16: bank shift)
     constexpr int CH = KT / 8;               // 16-byte chunks per activation row
@@ -310,17 +312,22 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
     const __amdgpu_buffer_rsrc_t wrs =
         make_rsrc(static_cast<const char*>(g.w) + (int64_t)nw * g.ldw * WB,
                   (uint32_t)((int64_t)wrows * g.ldw * WB));
-    const uint32_t wrow_off = (uint32_t)((16 * w + r) * g.ldw * WB);
-    u32x4 wv[W8 ? 1 : STEPS];
-    uint2 wq[W8 ? STEPS : 1];
+    // wave w owns weight rows 16 (NB w + nb) + r, nb < NB: each activation
+    // fragment read from LDS feeds NB MFMAs
+    u32x4 wv[NB][W8 ? 1 : STEPS];
+    uint2 wq[NB][W8 ? STEPS : 1];
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
         const int k = k0 + 32 * t + 8 * g4;
-        const uint32_t off = t < nsteps ? wrow_off + (uint32_t)(k * WB) : 0x80000000u;
-        if constexpr (W8)
-            wq[t] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wrs, off, 0, 0));
-        else
-            wv[t] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const uint32_t wrow_off = (uint32_t)((16 * (NB * w + nb) + r) * g.ldw * WB);
+            const uint32_t off = t < nsteps ? wrow_off + (uint32_t)(k * WB) : 0x80000000u;
+            if constexpr (W8)
+                wq[nb][t] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wrs, off, 0, 0));
+            else
+                wv[nb][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
+        }
     }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -330,31 +337,40 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
     }
     lds_barrier();
 
-    f32x4 acc[MB];
+    f32x4 acc[NB][MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
         if (t < nsteps) {
-            bf16x8 wf;
-            if constexpr (W8) wf = i8x8_to_bf16x8(wq[t]);
-            else wf = __builtin_bit_cast(bf16x8, wv[t]);
+            bf16x8 wf[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                if constexpr (W8) wf[nb] = i8x8_to_bf16x8(wq[nb][t]);
+                else wf[nb] = __builtin_bit_cast(bf16x8, wv[nb][t]);
+            }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const bf16x8 af = *reinterpret_cast<const bf16x8*>(
                     lds + (16 * mb + r) * PITCH + (32 * t + 8 * g4) * 2);
-                acc[mb] = mfma16x16x32(wf, af, acc[mb]);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) acc[nb][mb] = mfma16x16x32(wf[nb], af, acc[nb][mb]);
             }
         }
     }
 
     float* P = g.part + (int64_t)blockIdx.y * g.M * g.N;
-    const int n = nw + 16 * w + 4 * g4;
-    if (n < g.N) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            const int m = m0 + 16 * mb + r;
-            if (m < g.M) *reinterpret_cast<f32x4*>(P + (int64_t)m * g.N + n) = acc[mb];
+    for (int nb = 0; nb < NB; ++nb) {
+        const int n = nw + 16 * (NB * w + nb) + 4 * g4;
+        if (n < g.N) {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int m = m0 + 16 * mb + r;
+                if (m < g.M) *reinterpret_cast<f32x4*>(P + (int64_t)m * g.N + n) = acc[nb][mb];
+            }
         }
     }
 }
@@ -550,16 +566,19 @@ __global__ __launch_bounds__(256) void widen_int8_kernel(const int8_t* __restric
 
 struct SkPlan {
     bool split = false;
-    int mb = 0, kt = 0, nw = 0, splits = 0, mtiles = 0, ntiles = 0;
+    int mb = 0, kt = 0, nw = 0, nb = 1, splits = 0, mtiles = 0, ntiles = 0;
     size_t ws_bytes = 0;
 };
 
 // Tile choice: one 64-row weight tile per workgroup and K slices of 256, so
 // a 2048 x 2048 weight becomes 256 workgroups of 32 KB each and the
 // 6144-row QKV weight 768 (three per CU: LDS <= 42 KB each, so the whole
-// grid is resident at once).  Slices of 512 only when 256 would need more
-// than 16 slices or more workgroups than fit on the chip at once for one
-// 80-row tile.  The slicing depends on (N, K) only, never on M, so each
+// grid is resident at once).  The tile is two waves of two 16-row blocks:
+// half the LDS fragment reads per output of four waves of one block
+// (measured 0.7-1.2 us faster per call at M = 67-134; one wave of four
+// blocks or two waves of four are slower).  Slices of 512 (four waves of
+// one block) only when 256 would need more than 16 slices or more
+// workgroups than fit on the chip at once for one 80-row tile.  The slicing depends on (N, K) only, never on M, so each
 // row's sums are added in the same order whatever the batch: a row's result
 // does not depend on how many rows share the call.
 constexpr int kSkResident = 256 * 3;
@@ -568,12 +587,15 @@ inline SkPlan plan_splitk(int M, int N, int K) {
     if (M <= 0 || M > 160 || N <= 0 || (N & 15) || K <= 0 || (K & 31)) return p;
     p.mb = M <= 80 ? (M + 15) / 16 : 5;
     p.mtiles = (M + 16 * p.mb - 1) / (16 * p.mb);
-    p.nw = 4;
-    p.ntiles = (N + 16 * p.nw - 1) / (16 * p.nw);
+    p.nw = 2;
+    p.nb = 2;
+    p.ntiles = (N + 63) / 64;
     p.kt = 256;
     p.splits = (K + 255) / 256;
     if ((int64_t)p.ntiles * p.splits > kSkResident || p.splits > kSkMaxSplits) {
         p.kt = 512;
+        p.nw = 4;
+        p.nb = 1;
         p.splits = (K + 511) / 512;
     }
     if (p.splits > kSkMaxSplits) return SkPlan{};
@@ -582,26 +604,24 @@ inline SkPlan plan_splitk(int M, int N, int K) {
     return p;
 }
 
-template <int KT, int NW, bool W8>
+template <int KT, int NW, bool W8, int NB>
 void launch_splitk_mb(const SkArgs& a, const SkPlan& p, hipStream_t s) {
     const dim3 grid(p.ntiles, p.splits, p.mtiles), block(64 * NW);
     switch (p.mb) {
-        case 1: hipLaunchKernelGGL((gemm_splitk_kernel<1, KT, NW, W8>), grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL((gemm_splitk_kernel<2, KT, NW, W8>), grid, block, 0, s, a); break;
-        case 3: hipLaunchKernelGGL((gemm_splitk_kernel<3, KT, NW, W8>), grid, block, 0, s, a); break;
-        case 4: hipLaunchKernelGGL((gemm_splitk_kernel<4, KT, NW, W8>), grid, block, 0, s, a); break;
-        default: hipLaunchKernelGGL((gemm_splitk_kernel<5, KT, NW, W8>), grid, block, 0, s, a); break;
+        case 1: hipLaunchKernelGGL((gemm_splitk_kernel<1, KT, NW, W8, NB>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((gemm_splitk_kernel<2, KT, NW, W8, NB>), grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL((gemm_splitk_kernel<3, KT, NW, W8, NB>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((gemm_splitk_kernel<4, KT, NW, W8, NB>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((gemm_splitk_kernel<5, KT, NW, W8, NB>), grid, block, 0, s, a); break;
     }
 }
 
 template <bool W8>
 void launch_splitk_w(const SkArgs& a, const SkPlan& p, hipStream_t s) {
     if (p.kt == 256) {
-        if (p.nw == 8) launch_splitk_mb<256, 8, W8>(a, p, s);
-        else launch_splitk_mb<256, 4, W8>(a, p, s);
+        launch_splitk_mb<256, 2, W8, 2>(a, p, s);
     } else {
-        if (p.nw == 8) launch_splitk_mb<512, 8, W8>(a, p, s);
-        else launch_splitk_mb<512, 4, W8>(a, p, s);
+        launch_splitk_mb<512, 4, W8, 1>(a, p, s);
     }
 }
 
