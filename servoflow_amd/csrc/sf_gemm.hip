@@ -444,13 +444,31 @@ __device__ __forceinline__ uint2 pack_bf16x4(f32x4 v) {
     return uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }
 
+// Output tile of a reduce workgroup when N % 64 == 0: 16 rows x the 64
+// columns of one weight tile of the split-K kernel, tile index fastest.  That
+// kernel writes every K slice of weight tile j from XCD j % 8 (workgroup id
+// mod 8 is the XCD, and its grid's x extent N / 64 is a multiple of 8 for
+// the model's N), so the reduce of tile j lands on the same XCD and reads
+// those partials from its L2.  Lanes 16r .. 16r + 15 share row m.
+__device__ __forceinline__ bool reduce_tile_rc(const EpiArgs& e, int& m, int& n) {
+    const int ntl = e.N / 64;
+    m = (int)(blockIdx.x / ntl) * 16 + (int)(threadIdx.x >> 4);
+    n = 64 * (int)(blockIdx.x % ntl) + 4 * (int)(threadIdx.x & 15);
+    return m < e.M;
+}
+
 template <int NS>
 __global__ __launch_bounds__(256) void reduce_plain_kernel(const EpiArgs e) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int n4 = e.N / 4;
-    if (idx >= (int64_t)e.M * n4) return;
-    const int m = (int)(idx / n4);
-    const int n = 4 * (int)(idx % n4);
+    int m, n;
+    if ((e.N & 63) == 0) {
+        if (!reduce_tile_rc(e, m, n)) return;
+    } else {
+        const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+        const int n4 = e.N / 4;
+        if (idx >= (int64_t)e.M * n4) return;
+        m = (int)(idx / n4);
+        n = 4 * (int)(idx % n4);
+    }
     f32x4 v = finish4<NS>(e, m, n);
     const int64_t off = (e.m_off + m) * e.ldc + n;
     if (e.c_f32) {
@@ -465,11 +483,8 @@ __global__ __launch_bounds__(256) void reduce_plain_kernel(const EpiArgs e) {
 // 16 consecutive lanes hold the 64 columns of one head of one row.
 template <int NS>
 __global__ __launch_bounds__(256) void reduce_heads_kernel(const EpiArgs e) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int n4 = e.N / 4;
-    if (idx >= (int64_t)e.M * n4) return;   // whole 16-lane groups (N % 64 == 0)
-    const int m = (int)(idx / n4);
-    const int n = 4 * (int)(idx % n4);
+    int m, n;   // N % 64 == 0: a 16-lane group is one head of one row
+    if (!reduce_tile_rc(e, m, n)) return;   // whole 16-lane groups
     f32x4 v = finish4<NS>(e, m, n);
     const int cols = e.H * 64;
     const int sec = n / cols;
@@ -633,13 +648,15 @@ inline void launch_splitk(const SkArgs& a, const SkPlan& p, bool w8, hipStream_t
 template <int NS>
 void launch_reduce(const sf_gemm_desc* d, const EpiArgs& e, hipStream_t s) {
     const int64_t quads = (int64_t)e.M * e.N / 4;
-    const unsigned blocks = (unsigned)((quads + 255) / 256);
+    const unsigned tiles = (unsigned)((int64_t)(e.N / 64) * ((e.M + 15) / 16));
     if (d->epilogue == SF_EPI_HEADS)
-        hipLaunchKernelGGL(reduce_heads_kernel<NS>, dim3(blocks), dim3(256), 0, s, e);
+        hipLaunchKernelGGL(reduce_heads_kernel<NS>, dim3(tiles), dim3(256), 0, s, e);
     else if (d->epilogue == SF_EPI_ADD_NORM)
         hipLaunchKernelGGL(reduce_addnorm_kernel<NS>, dim3(e.M), dim3(kAddNormThreads), 0, s, e);
+    else if ((e.N & 63) == 0)
+        hipLaunchKernelGGL(reduce_plain_kernel<NS>, dim3(tiles), dim3(256), 0, s, e);
     else
-        hipLaunchKernelGGL(reduce_plain_kernel<NS>, dim3(blocks), dim3(256), 0, s, e);
+        hipLaunchKernelGGL(reduce_plain_kernel<NS>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, e);
 }
 
 template <int NR, bool W8>
