@@ -9,10 +9,10 @@
 // Design (the split kernel serves the 67 x 4374 / 67 x <=1024
 // cross-attention; attn_short_kernel below serves key sets of <= 128, the
 // 67 x 67 self-attention):
-//   * a workgroup of 4 waves owns one (b, h, query chunk of 80 rows, key
-//     split), two workgroups per CU; all workgroups of one (b, h) run on one
-//     XCD (head_work).  Splitting the keys (flash-decoding) is what fills 256
-//     CUs when B*H = 32.
+//   * grid = (splits x query-chunks, H, B); a workgroup of 4 waves owns one
+//     (b, h, query chunk of 80 rows, key split), two workgroups per CU.
+//     Splitting the keys (flash-decoding) is what fills 256 CUs when
+//     B*H = 32.
 //   * K/V tiles of 128 keys are streamed HBM -> LDS by buffer_load ... lds
 //     (16-byte, coalesced, no VGPR staging) into a two-stage ring, so the
 //     next tile's loads are in flight while the current one is contracted;
@@ -274,30 +274,6 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
 // row is all ones turns P^T into l, so the VALU does no per-element adds and
 // l sums exactly the (hi + lo) weights the numerator uses.
 // ---------------------------------------------------------------------------
-// Workgroup placement for the split kernels: workgroups are dealt to the 8
-// XCDs by id mod 8.  (b, h) pair u and its X workgroups (key splits x query
-// chunks for the ring kernel, 4-row groups for the merge) take ids
-// u % 8 + 8 (floor(u / 8) X + x), so every workgroup of a pair runs on XCD
-// u % 8 and the merge reads the partials the ring kernel wrote from that
-// XCD's L2.  Pairs past the last complete group of 8 take consecutive ids.
-struct HeadWork {
-    int x, h, b;
-};
-__device__ __forceinline__ HeadWork head_work(int id, int X, int H, int B) {
-    const int full = (B * H / 8) * 8;
-    int u, x;
-    if (id < full * X) {
-        const int k = id / 8;
-        x = k % X;
-        u = (k / X) * 8 + id % 8;
-    } else {
-        const int t = id - full * X;
-        u = full + t / X;
-        x = t % X;
-    }
-    return {x, u % H, u / H};
-}
-
 constexpr int kRingStages = 2;
 constexpr int kKT = 128;                          // keys per tile (4 waves x 32)
 constexpr int kTileBytes = kKT * kD * 2;          // 16 KB per K (or V) tile
@@ -331,11 +307,10 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     const int g = lane >> 4;
     const int r = lane & 15;
     const int nsplit = a.nsplit;
-    const HeadWork hw = head_work(blockIdx.x, nsplit * a.nqc, a.H, a.B);
-    const int split = hw.x % nsplit;
-    const int qc = hw.x / nsplit;
-    const int h = hw.h;
-    const int b = hw.b;
+    const int split = blockIdx.x % nsplit;
+    const int qc = blockIdx.x / nsplit;
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
     const int q0 = qc * QR;
 
     int valid = a.Sk;
@@ -643,10 +618,9 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 // the loads unrolled so they overlap.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     const int lane = threadIdx.x & 63;
-    const HeadWork hw = head_work(blockIdx.x, (a.Sq + 3) / 4, a.H, a.B);
-    const int q = hw.x * 4 + (threadIdx.x >> 6);
-    const int h = hw.h;
-    const int b = hw.b;
+    const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
     if (q >= a.Sq) return;
     const int ns = a.nsplit;
     const size_t row0 = ((size_t)b * a.H + h) * ns * (size_t)a.Sq + q;   // split 0's row
@@ -977,8 +951,7 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         a.part_o = static_cast<float*>(workspace);
         a.part_ml = a.part_o + (size_t)d->B * d->H * ns * d->Sq * sfk::kD;
     }
-    if ((long)ns * nqc * d->H * d->B > 0x7fffffffL || (long)(d->Sq + 3) / 4 * d->H * d->B > 0x7fffffffL)
-        return SF_ENOTSUP;
+    if ((long)ns * nqc > 0x7fffffffL) return SF_ENOTSUP;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (short_keys) {
@@ -990,15 +963,14 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         else hipLaunchKernelGGL(sfk::attn_short_kernel<8>, grid, dim3(64), 0, s, a);
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
     }
-    const dim3 ring_grid((unsigned)((long)ns * nqc * d->H * d->B));
     if (d->exact_pv)
-        hipLaunchKernelGGL(sfk::attn_ring_kernel<true>, ring_grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(sfk::attn_ring_kernel<true>, dim3(ns * nqc, d->H, d->B), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(sfk::attn_ring_kernel<false>, ring_grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(sfk::attn_ring_kernel<false>, dim3(ns * nqc, d->H, d->B), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     if (ns > 1) {
-        hipLaunchKernelGGL(sfk::attn_merge_kernel, dim3((unsigned)((long)(d->Sq + 3) / 4 * d->H * d->B)),
-                           dim3(256), 0, s, a);
+        hipLaunchKernelGGL(sfk::attn_merge_kernel, dim3((d->Sq + 3) / 4, d->H, d->B), dim3(256), 0,
+                           s, a);
         if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     }
     return SF_OK;
