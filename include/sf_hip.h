@@ -204,9 +204,12 @@ size_t sf_gemm_workspace_bytes(const sf_gemm_desc* desc);
 
 int sf_gemm(const sf_gemm_desc* desc, void* stream);
 
-/* Host-side setup of the library path for this shape (algorithm selection,
- * once per shape and process; no device work).  sf_gemm does it on first
- * use; call this before capturing a graph that contains the call. */
+/* Setup of the library path (M > 160) for this shape, once per shape and
+ * process: the hipBLASLt algorithm is chosen by timing its first 16
+ * candidates on scratch buffers of the shape (synchronous: allocates,
+ * launches on a private stream, frees).  sf_gemm on a shape never prepared
+ * takes hipBLASLt's first candidate without timing.  Call this before
+ * capturing a graph that contains the call. */
 int sf_gemm_prepare(const sf_gemm_desc* desc);
 
 /* ---------------------------------------------------------------------------

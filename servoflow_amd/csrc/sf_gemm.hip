@@ -714,10 +714,58 @@ std::mutex g_lt_mu;
 std::map<int, hipblasLtHandle_t> g_lt_handles;
 std::map<std::tuple<int, int, int, int, int64_t, int64_t>, LtShape> g_lt_shapes;
 
+// Times each candidate algorithm on scratch buffers of the shape (zeros; 2
+// warm-up and 5 timed runs on a private stream) and returns the index of
+// the fastest, or -1 when none ran.  Called from sf_gemm_prepare only, never
+// under graph capture.
+int lt_pick_fastest(hipblasLtHandle_t h, const LtShape& sh, const hipblasLtMatmulHeuristicResult_t* res, int nres,
+                    int N, int K, int rows, int64_t lda, int64_t ldw) {
+    void *a = nullptr, *w = nullptr, *dbuf = nullptr, *ws = nullptr;
+    hipStream_t st = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int best = -1;
+    float best_ms = 0.f;
+    const size_t abytes = (size_t)rows * lda * 2, wbytes = (size_t)N * ldw * 2, dbytes = (size_t)rows * N * 4;
+    if (hipMalloc(&a, abytes) == hipSuccess && hipMalloc(&w, wbytes) == hipSuccess &&
+        hipMalloc(&dbuf, dbytes) == hipSuccess && hipMalloc(&ws, kLibLtBytes) == hipSuccess &&
+        hipStreamCreate(&st) == hipSuccess && hipEventCreate(&e0) == hipSuccess &&
+        hipEventCreate(&e1) == hipSuccess && hipMemsetAsync(a, 0, abytes, st) == hipSuccess &&
+        hipMemsetAsync(w, 0, wbytes, st) == hipSuccess) {
+        const float one = 1.f, zero = 0.f;
+        for (int i = 0; i < nres; ++i) {
+            if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kLibLtBytes) continue;
+            bool ok = true;
+            for (int r = 0; r < 7 && ok; ++r) {
+                if (r == 2) ok = hipEventRecord(e0, st) == hipSuccess;
+                ok = ok && hipblasLtMatmul(h, sh.desc, &one, w, sh.a, a, sh.b, &zero, dbuf, sh.d, dbuf, sh.d,
+                                           &res[i].algo, ws, kLibLtBytes, st) == HIPBLAS_STATUS_SUCCESS;
+            }
+            ok = ok && hipEventRecord(e1, st) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+            float ms = 0.f;
+            ok = ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+            if (ok && (best < 0 || ms < best_ms)) {
+                best = i;
+                best_ms = ms;
+            }
+        }
+    }
+    if (st) (void)hipStreamSynchronize(st);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (st) (void)hipStreamDestroy(st);
+    for (void* p : {a, w, dbuf, ws})
+        if (p) (void)hipFree(p);
+    (void)hipGetLastError();
+    return best;
+}
+
 // D (fp32 [rows][N]) = A_act (bf16 [rows][lda]) . W (bf16 [N][ldw])^T, in
 // hipBLASLt's column-major terms: D (N x rows) = op_T(W: K x N, ld ldw) .
-// (A_act: K x rows, ld lda).
-int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, hipblasLtHandle_t* h, const LtShape** out) {
+// (A_act: K x rows, ld lda).  tune: choose among hipBLASLt's first 16
+// candidates by timing them (sf_gemm_prepare); otherwise its first choice.
+// A shape keeps the algorithm it was first created with.
+int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, hipblasLtHandle_t* h, const LtShape** out,
+              bool tune = false) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return SF_EDEVICE;
     std::lock_guard<std::mutex> lock(g_lt_mu);
@@ -746,13 +794,19 @@ int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, hipblasLtHandle_
         const uint64_t wsmax = kLibLtBytes;
         ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax,
                                                          sizeof wsmax) == HIPBLAS_STATUS_SUCCESS;
-        hipblasLtMatmulHeuristicResult_t res[1];
+        constexpr int kCand = 16;
+        hipblasLtMatmulHeuristicResult_t res[kCand];
         int nres = 0;
-        ok = ok && hipblasLtMatmulAlgoGetHeuristic(*h, sh.desc, sh.a, sh.b, sh.d, sh.d, pref, 1, res, &nres) ==
-                       HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatmulAlgoGetHeuristic(*h, sh.desc, sh.a, sh.b, sh.d, sh.d, pref, tune ? kCand : 1, res,
+                                                   &nres) == HIPBLAS_STATUS_SUCCESS;
         ok = ok && nres > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= kLibLtBytes;
         if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
-        if (ok) sh.algo = res[0].algo;
+        int pick = 0;
+        if (ok && tune && nres > 1) {
+            const int best = lt_pick_fastest(*h, sh, res, nres, N, K, rows, lda, ldw);
+            if (best >= 0) pick = best;
+        }
+        if (ok) sh.algo = res[pick].algo;
         sh.ok = ok;
         it = g_lt_shapes.emplace(key, sh).first;
     }
@@ -907,7 +961,7 @@ extern "C" int sf_gemm_prepare(const sf_gemm_desc* d) {
     const LtShape* sh = nullptr;
     for (int rows : {lp.chunk, d->M % lp.chunk}) {
         if (rows <= 0) continue;
-        const int st = lt_lookup(d->N, d->K, rows, d->lda, ldw, &h, &sh);
+        const int st = lt_lookup(d->N, d->K, rows, d->lda, ldw, &h, &sh, true);
         if (st != SF_OK) return st;
     }
     return SF_OK;
