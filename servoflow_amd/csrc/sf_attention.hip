@@ -10,7 +10,7 @@
 // cross-attention; attn_short_kernel below serves key sets of <= 128, the
 // 67 x 67 self-attention):
 //   * grid = (splits x query-chunks, H, B); a workgroup of 4 waves owns one
-//     (b, h, query chunk of 80 rows, key split), two workgroups per CU.
+//     (b, h, query chunk of 80 rows, key split); up to two fit on a CU.
 //     Splitting the keys (flash-decoding) is what fills 256 CUs when
 //     B*H = 32.
 //   * K/V tiles of 128 keys are streamed HBM -> LDS by buffer_load ... lds
@@ -258,10 +258,9 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
 // ---------------------------------------------------------------------------
 // Split kernel, ring-pipelined (the cross-attention path).
 //
-// One (b, h, query chunk, key split) per workgroup of 4 waves, two
-// workgroups per CU (two waves per SIMD: the softmax is VALU-issue bound and
-// one wave alone issues VALU at half the SIMD's rate); the splits are chosen
-// so B*H*splits ~ 512.  K and V tiles of 128 keys go HBM -> LDS directly
+// One (b, h, query chunk, key split) per workgroup of 4 waves; two
+// workgroups fit on a CU (64 KB of LDS each), and the split count puts about
+// one per CU (choose_splits).  K and V tiles of 128 keys go HBM -> LDS directly
 // (buffer_load ... lds, no VGPR staging) into a 2-stage ring per workgroup,
 // a tile's loads issued as soon as its stage is free.  Rows
 // sit in LDS in their natural [key][64] layout with the 16-byte chunks of
@@ -833,23 +832,29 @@ using sfk::kMaxSplits;
 
 int query_chunks(const sf_attn_desc* d) { return (d->Sq + 16 * sfk::kQB - 1) / (16 * sfk::kQB); }
 
-// MI355X has 256 CUs and the ring kernel runs two workgroups per CU (64 KB
-// LDS ring each).  When B*H*query-chunks alone fills the CUs the keys are not
-// split (no partials, no merge pass: measured faster at B = 8 and 16 than two
-// splits); otherwise splits make the grid one round of workgroups, each split
-// covering at least one 128-key tile.
+// MI355X has 256 CUs.  When B*H*query-chunks alone fills them the keys are
+// not split (no partials, no merge pass: measured faster at B = 8 and 16 than
+// two splits).  Otherwise the keys are split so that the grid is about one
+// workgroup per CU, and then into the fewest splits whose longest split has
+// the same number of 128-key tiles (image keys at B = 1: 35 tiles, 8 splits
+// of <= 5 tiles -> 7 splits).  Measured at B = 1 on 4374 keys: 7 splits
+// 20.3 us, 8 21.0, 12 22.1, 16 (two workgroups per CU) 24.8; at B = 2, 4
+// splits 26.5 us against 29.3 for 8: a workgroup alone on its CU contracts
+// its tiles at the CU's full rate, and fewer splits halve the partials the
+// merge pass reads.
 constexpr long kNumCUs = 256;
-constexpr long kWgPerCU = 2;
 
 int choose_splits(const sf_attn_desc* d) {
     if (d->num_splits > 0) return d->num_splits < kMaxSplits ? d->num_splits : kMaxSplits;
     const long base = (long)d->B * d->H * query_chunks(d);
     if (base <= 0) return 1;
     if (base >= kNumCUs) return 1;
-    long ns = kNumCUs * kWgPerCU / base;
-    const long cap = d->Sk / 128;
-    if (ns > cap) ns = cap;
+    const long tiles = ((long)d->Sk + 127) / 128;
+    long ns = kNumCUs / base;
+    if (ns > tiles) ns = tiles;
     if (ns < 1) ns = 1;
+    const long longest = (tiles + ns - 1) / ns;
+    ns = (tiles + longest - 1) / longest;
     if (ns > kMaxSplits) ns = kMaxSplits;
     return (int)ns;
 }

@@ -106,9 +106,9 @@ def test_split_count_invariance(ns):
 
 @pytest.mark.parametrize("ns", [8, 9])
 def test_ring_variants_image_b1(ns):
-    """num_splits = 8 gives 256 workgroups (the 8-wave ring kernel, one per
-    CU), 9 gives 288 (the 4-wave kernel, two per CU); both against the
-    oracle, with and without valid lengths."""
+    """num_splits = 8 gives 256 workgroups (one per CU, splits of 4-5
+    tiles), 9 gives 288 (more workgroups than CUs); both against the oracle,
+    with and without valid lengths."""
     q = rounded(155, (1, 32, 67, 64))
     k, v = rounded(156, (1, 32, 4374, 64)), rounded(157, (1, 32, 4374, 64))
     got = run(q, k, v, num_splits=ns)
