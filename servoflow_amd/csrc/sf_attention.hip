@@ -97,38 +97,49 @@ typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 // them to their result registers, so no use can be scheduled before it.
 // Early-clobber outputs: a result register must not double as an address
 // that a later read of the batch still has to send.
+// OFF: a constant byte offset added to every address (the ring stage).
+#define SF_TR16_X8(OFF)                                                                         \
+    asm volatile("ds_read_b64_tr_b16 %0, %8 offset:" #OFF "\n\t"                              \
+                 "ds_read_b64_tr_b16 %1, %9 offset:" #OFF "\n\t"                              \
+                 "ds_read_b64_tr_b16 %2, %10 offset:" #OFF "\n\t"                             \
+                 "ds_read_b64_tr_b16 %3, %11 offset:" #OFF "\n\t"                             \
+                 "ds_read_b64_tr_b16 %4, %12 offset:" #OFF "\n\t"                             \
+                 "ds_read_b64_tr_b16 %5, %13 offset:" #OFF "\n\t"                             \
+                 "ds_read_b64_tr_b16 %6, %14 offset:" #OFF "\n\t"                             \
+                 "ds_read_b64_tr_b16 %7, %15 offset:" #OFF                                     \
+                 : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), \
+                   "=&v"(o[6]), "=&v"(o[7])                                                    \
+                 : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]),       \
+                   "v"(addr[5]), "v"(addr[6]), "v"(addr[7])                                    \
+                 : "memory")
+template <int OFF>
 __device__ __forceinline__ void lds_read_tr16_x8(u32x2v (&o)[8], const uint32_t (&addr)[8]) {
-    asm volatile(
-        "ds_read_b64_tr_b16 %0, %8\n\t"
-        "ds_read_b64_tr_b16 %1, %9\n\t"
-        "ds_read_b64_tr_b16 %2, %10\n\t"
-        "ds_read_b64_tr_b16 %3, %11\n\t"
-        "ds_read_b64_tr_b16 %4, %12\n\t"
-        "ds_read_b64_tr_b16 %5, %13\n\t"
-        "ds_read_b64_tr_b16 %6, %14\n\t"
-        "ds_read_b64_tr_b16 %7, %15"
-        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]),
-          "=&v"(o[6]), "=&v"(o[7])
-        : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]),
-          "v"(addr[6]), "v"(addr[7])
-        : "memory");
+    static_assert(OFF == 0 || OFF == 32768, "stage offsets of the ring");
+    if constexpr (OFF == 0) SF_TR16_X8(0);
+    else SF_TR16_X8(32768);
 }
+#undef SF_TR16_X8
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)(p);
 }
 
 // Four ds_read_b128 (the wave's K fragments of a ring stage), no wait.
+#define SF_B128_X4(OFF)                                                            \
+    asm volatile("ds_read_b128 %0, %4 offset:" #OFF "\n\t"                       \
+                 "ds_read_b128 %1, %5 offset:" #OFF "\n\t"                       \
+                 "ds_read_b128 %2, %6 offset:" #OFF "\n\t"                       \
+                 "ds_read_b128 %3, %7 offset:" #OFF                                \
+                 : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3])             \
+                 : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3])         \
+                 : "memory")
+template <int OFF>
 __device__ __forceinline__ void lds_read_b128_x4(u32x4 (&o)[4], const uint32_t (&addr)[4]) {
-    asm volatile(
-        "ds_read_b128 %0, %4\n\t"
-        "ds_read_b128 %1, %5\n\t"
-        "ds_read_b128 %2, %6\n\t"
-        "ds_read_b128 %3, %7"
-        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3])
-        : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3])
-        : "memory");
+    static_assert(OFF == 0 || OFF == 32768, "stage offsets of the ring");
+    if constexpr (OFF == 0) SF_B128_X4(0);
+    else SF_B128_X4(32768);
 }
+#undef SF_B128_X4
 
 // max(x, x of lane ^ 16) and max(x, x of lane ^ 32) with the VALU lane swaps
 // of gfx950 (v_permlane16/32_swap with both operands x: the two results hold,
@@ -280,6 +291,8 @@ constexpr int kStageBytes = 2 * kTileBytes;       // K then V
 
 __device__ __forceinline__ int ring_swz(int key) { return (key >> 1) & 7; }
 
+template <int V> struct StageOff { static constexpr int value = V; };
+
 // Key-padding mask bytes of keys k..k+3 (k a multiple of 4) as a 32-bit
 // word.  The buffer range is Sk rounded up to 4 bytes: words past it read as
 // 0, and bytes of keys >= Sk are never used (those keys are out of range).
@@ -302,7 +315,9 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = tid >> 6;
+    // the wave index as a scalar, so the LDS-DMA destinations (M0) and the
+    // per-tile buffer resources are scalar arithmetic
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4;
     const int r = lane & 15;
     const int nsplit = a.nsplit;
@@ -329,8 +344,6 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
     const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
     const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qp, (uint32_t)(a.Sq * a.q_ss * 2));
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, (uint32_t)(max(kend, 0) * a.k_ss * 2));
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vp, (uint32_t)(max(kend, 0) * a.v_ss * 2));
     const __amdgpu_buffer_rsrc_t mrs =
         make_rsrc(a.kv_mask ? static_cast<const void*>(a.kv_mask + b * a.kv_mask_stride) : static_cast<const void*>(a.q),
                   a.kv_mask ? (uint32_t)((a.Sk + 3) & ~3) : 0u);
@@ -346,30 +359,34 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 
     // DMA of one tile into a stage: wave w, op j fills LDS chunks
     // (4w + j) * 64 + lane = key * 8 + slot of K (and of V), loading global
-    // chunk slot ^ swz(key) of that key.  Keys past kend read as zeros.
-    int chunk_key[4], chunk_col[4];
+    // chunk slot ^ swz(key) of that key.  The tile's rows are addressed
+    // through a buffer resource based at the tile's first key and ending at
+    // kend (scalar work per tile), so the per-lane offsets are the same for
+    // every tile and keys past kend read as zeros.
+    uint32_t koffj[4], voffj[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int p = (4 * w + j) * 64 + lane;
-        chunk_key[j] = p >> 3;
-        chunk_col[j] = ((p & 7) ^ ring_swz(p >> 3)) * 8;
+        const int key = p >> 3;
+        const int col = ((p & 7) ^ ring_swz(key)) * 8;
+        koffj[j] = (uint32_t)((key * a.k_ss + col) * 2);
+        voffj[j] = (uint32_t)((key * a.v_ss + col) * 2);
     }
     auto issue = [&](int t) {
         const int kt = kbeg + t * kKT;
+        const uint32_t rows = (uint32_t)max(kend - kt, 0);
+        const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp + (int64_t)kt * a.k_ss, rows * (uint32_t)a.k_ss * 2u);
+        const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vp + (int64_t)kt * a.v_ss, rows * (uint32_t)a.v_ss * 2u);
         char* st = ring + (t % kRingStages) * kStageBytes;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t koff = (uint32_t)(((kt + chunk_key[j]) * a.k_ss + chunk_col[j]) * 2);
+        for (int j = 0; j < 4; ++j)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                krs, (__attribute__((address_space(3))) void*)(st + (4 * w + j) * 1024), 16, koff, 0, 0, 0);
-        }
+                krs, (__attribute__((address_space(3))) void*)(st + (4 * w + j) * 1024), 16, koffj[j], 0, 0, 0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t voff = (uint32_t)(((kt + chunk_key[j]) * a.v_ss + chunk_col[j]) * 2);
+        for (int j = 0; j < 4; ++j)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 vrs, (__attribute__((address_space(3))) void*)(st + kTileBytes + (4 * w + j) * 1024), 16,
-                voff, 0, 0, 0);
-        }
+                voffj[j], 0, 0, 0);
     };
     // Key-padding mask words of tile t, loaded one tile ahead and always
     // BEFORE the next tile's DMA is issued: vector loads complete in issue
@@ -400,7 +417,11 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 
     f32x4 acc[kQB][4];   // O^T blocks: lane holds d = 16db + 4g + i, q = 16qb + r
     f32x4 accl[kQB];     // row sums: element 0 of lanes 0..15 holds l of query 16qb + r
+    // m: running max of each query row in log2 units (-inf until a finite
+    // score has been seen).  A tile whose raw scores stay at or below
+    // (m + 8) / scale_log2 keeps m, so every weight is <= 2^8.
     float m[kQB], l[kQB];
+    const float inv_sl2 = 1.f / a.scale_log2;
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
         m[qb] = -INFINITY;
@@ -416,53 +437,43 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     bool v_out_of_range = false;   // fp16 form: some |v| >= 2^16 (inf included)
 
     const int wkey = 32 * w;   // this wave's first key inside a tile
-    // per-lane LDS byte offsets inside a stage (swizzled rows)
-    int koffs[2][2];
+    // LDS byte addresses of this lane's K fragment and V^T transpose reads in
+    // stage 0 (swizzled rows); stage 1 adds the reads' constant offset field
+    static_assert(kStageBytes == 32768 && kRingStages == 2, "the LDS reads encode the stage offset");
+    const uint32_t lbase = lds_addr(ring);
+    uint32_t ka[4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
         const int key = wkey + 16 * kb + r;
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) koffs[kb][hh] = key * 128 + (((g + 4 * hh) ^ ring_swz(key)) * 16);
+        for (int hh = 0; hh < 2; ++hh) ka[2 * kb + hh] = lbase + key * 128 + (((g + 4 * hh) ^ ring_swz(key)) * 16);
     }
-    int voffs[2][4];   // [key half][db]: V^T transpose-read addresses
+    uint32_t va[8];   // [2 db + key half]
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
         const int key = wkey + 16 * hf + 4 * g + (r >> 2);
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
             const int d = 16 * db + 4 * (r & 3);
-            voffs[hf][db] = kTileBytes + key * 128 + (((d >> 3) ^ ring_swz(key)) * 16) + (d & 7) * 2;
+            va[2 * db + hf] = lbase + kTileBytes + key * 128 + (((d >> 3) ^ ring_swz(key)) * 16) + (d & 7) * 2;
         }
     }
 
-    for (int t = 0; t < ntiles; ++t) {
+    // One tile; SOFF (0 or kStageBytes) is the stage it sits in, t % 2.
+    auto tile = [&](const int t, auto soff) {
+        constexpr int SOFF = decltype(soff)::value;
         const int kt = kbeg + t * kKT;
         ring_wait_barrier();   // tile t has landed; tile t + 1 may still stream in
-        const char* st = ring + (t % kRingStages) * kStageBytes;
         if (kt + wkey < kend && !(a.causal && kt + wkey > q0 + QR - 1)) {
             // K fragments, then V^T: K is waited for before the S contraction,
             // V^T only before P.V, so the transpose reads overlap S.
             u32x4 kw[4];
-            {
-                const uint32_t sbase = lds_addr(st);
-                const uint32_t ka[4] = {sbase + koffs[0][0], sbase + koffs[0][1], sbase + koffs[1][0],
-                                        sbase + koffs[1][1]};
-                lds_read_b128_x4(kw, ka);
-            }
+            lds_read_b128_x4<SOFF>(kw, ka);
             u32x2v vt[8];
-            {
-                const uint32_t sbase = lds_addr(st);
-                uint32_t va[8];
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    va[2 * db] = sbase + voffs[0][db];
-                    va[2 * db + 1] = sbase + voffs[1][db];
-                }
-                lds_read_tr16_x8(vt, va);
-                // K landed (LDS reads return in order; no scalar loads are in
-                // flight in the loop, so the count is exact); V^T may not have
-                asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(kw[0]), "+v"(kw[1]), "+v"(kw[2]), "+v"(kw[3]) :: "memory");
-            }
+            lds_read_tr16_x8<SOFF>(vt, va);
+            // K landed (LDS reads return in order; no scalar loads are in
+            // flight in the loop, so the count is exact); V^T may not have
+            asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(kw[0]), "+v"(kw[1]), "+v"(kw[2]), "+v"(kw[3]) :: "memory");
             bf16x8 kf[2][2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -496,24 +507,26 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                     }
                 }
             }
-            float mx[kQB];
+            // The lane's own maximum over its 8 scores of each row block.  A
+            // row's maximum over the tile exceeds its threshold exactly when
+            // one of the four lanes holding that row does, so the wave-wide
+            // test needs no cross-lane maximum; that is taken only when the
+            // rows are rescaled.
+            float lmx[kQB];
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb) {
                 const f32x4 u = s[qb][0], v = s[qb][1];
-                mx[qb] = fmaxf(fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3])),
-                               fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+                lmx[qb] = fmaxf(fmaxf(fmaxf(fmaxf(fmaxf(fmaxf(fmaxf(u[0], u[1]), u[2]), u[3]), v[0]), v[1]), v[2]),
+                                v[3]);
             }
-#pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) mx[qb] = max_xor16(mx[qb]);
-#pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) mx[qb] = max_xor32(mx[qb]) * a.scale_log2;
             bool grow = false;
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) grow |= mx[qb] > m[qb] + 8.f;
+            for (int qb = 0; qb < kQB; ++qb) grow |= lmx[qb] > fmaf(m[qb], inv_sl2, 8.f * inv_sl2);
             if (__any(grow)) {
 #pragma unroll
                 for (int qb = 0; qb < kQB; ++qb) {
-                    const float mnew = fmaxf(m[qb], mx[qb]);
+                    const float mx = max_xor32(max_xor16(lmx[qb])) * a.scale_log2;
+                    const float mnew = fmaxf(m[qb], mx);
                     const float alpha = fast_exp2(m[qb] - (mnew == -INFINITY ? 0.f : mnew));
                     m[qb] = mnew;
                     accl[qb] *= alpha;
@@ -591,13 +604,19 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                     }
                     accl[qb] = mfma16x16x32(ones, ph8, accl[qb]);
                     accl[qb] = mfma16x16x32(ones, pl8, accl[qb]);
-                            }
+                }
             }
         }   // live keys
         // every wave is done with this stage before it is refilled
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (a.kv_mask) load_mask(t + 1, mw_next);
         issue(t + kRingStages);
+    };
+    // Two tiles per iteration, one per stage, so every LDS read of a tile
+    // carries its stage as a constant offset.
+    for (int t = 0; t < ntiles; t += 2) {
+        tile(t, StageOff<0>{});
+        if (t + 1 < ntiles) tile(t + 1, StageOff<kStageBytes>{});
     }
     // The loads issued past the last tile land in LDS that the epilogue
     // reuses: every wave waits for its own, then all waves meet.
