@@ -155,32 +155,33 @@ __device__ __forceinline__ float max_xor32(float x) {
     return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 
-// Shared epilogue of the split kernels: row sums, then the four waves'
-// (m, l, O) merge through LDS (xo_base: >= 43.5 KB of LDS no longer in use),
-// then the normalised output (one split) or the split's partials.
+// Epilogue of the ring kernel: the four waves' (m, l, O) merged through LDS
+// (xo_base: >= 64 KB of LDS no longer in use), then the normalised output
+// (one split) or the split's partials.  Wave w owns head dims
+// [16w, 16w + 16).  Every wave writes its row maxima and sums, its
+// out-of-range flag and, unscaled, the three d-blocks it does not own; after
+// ONE barrier each owner takes the four waves' maxima, scales the four
+// contributions to its d-block and sums them, so each output element is
+// summed once and stored as a 4-vector.
 __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo_base,
-                                                    f32x4 (&acc)[kQB][4], float (&m)[kQB],
-                                                    float (&l)[kQB], int w, int g, int r, int lane,
+                                                    f32x4 (&acc)[kQB][4], const float (&m)[kQB],
+                                                    const float (&l)[kQB], int w, int g, int r, int lane,
                                                     int b, int h, int q0, int split, int nsplit,
-                                                    bool l_per_lane = true, bool poison = false) {
+                                                    bool v_out_of_range) {
     constexpr int QR = 16 * kQB;
-    // ---- Row sums: each lane summed its own 8 keys per tile; add the four
-    //      lane groups that share a query.
-    if (l_per_lane) {
+    float* xo = xo_base;                                  // [4 writer][3 slot][kQB][64 lanes][4]
+    float* sm = xo + 4 * 3 * kQB * 64 * 4;                // [4][QR]
+    float* sl = sm + 4 * QR;                              // [4][QR]
+    uint32_t* pz = reinterpret_cast<uint32_t*>(sl + 4 * QR);   // [4] per-wave out-of-range flags
+    static_assert((4 * 3 * kQB * 64 * 4 + 2 * 4 * QR + 4) * 4 <= 2 * 32768, "fits the ring's LDS");
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
-            l[qb] += __shfl_xor(l[qb], 16, 64);
-            l[qb] += __shfl_xor(l[qb], 32, 64);
-        }
+    for (int o = 0; o < 4; ++o) {
+        if (o == w) continue;
+        const int slot = o - (o > w ? 1 : 0);
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb)
+            *reinterpret_cast<f32x4*>(xo + (((w * 3 + slot) * kQB + qb) * 64 + lane) * 4) = acc[qb][o];
     }
-
-    // ---- Merge the four waves' (m, l, O).  Wave w owns head dims
-    //      [16w, 16w + 16); the other waves hand it their partial sums for
-    //      that d-block through LDS in two rounds (owners 0,1 then 2,3), so
-    //      each output element is summed once and stored as a 4-vector.
-    float* xo = xo_base;                                 // [4 w][2 slot][kQB][64 lanes][4]
-    float* sm = xo + 4 * 2 * kQB * 64 * 4;               // [4][QR]
-    float* sl = sm + 4 * QR;                             // [4][QR]
     if (g == 0) {
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
@@ -188,81 +189,72 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
             sl[w * QR + 16 * qb + r] = l[qb];
         }
     }
+    const bool wave_oor = __any(v_out_of_range);
+    if (lane == 0) pz[w] = wave_oor ? 1u : 0u;
     __syncthreads();
-    float Lq[kQB], Mq[kQB];
-#pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
-        const int q = 16 * qb + r;
-        const float m0 = sm[q], m1 = sm[QR + q], m2 = sm[2 * QR + q], m3 = sm[3 * QR + q];
-        const float M = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
-        const float Muse = M == -INFINITY ? 0.f : M;
-        Lq[qb] = sl[q] * fast_exp2(m0 - Muse) + sl[QR + q] * fast_exp2(m1 - Muse) +
-                 sl[2 * QR + q] * fast_exp2(m2 - Muse) + sl[3 * QR + q] * fast_exp2(m3 - Muse);
-        Mq[qb] = M;
-        const float f = fast_exp2(m[qb] - Muse);
-#pragma unroll
-        for (int db = 0; db < 4; ++db) acc[qb][db] *= f;
-    }
 
+    // V outside the fp16 form's range anywhere in this workgroup's keys: its
+    // rows (or split partials) become NaN rather than silently saturated.
+    const bool poison = (pz[0] | pz[1] | pz[2] | pz[3]) != 0;
     const size_t bh = (size_t)b * a.H + h;
     const size_t pbase = (bh * nsplit + split) * (size_t)a.Sq;
     const int d0 = 16 * w + 4 * g;
+    // quiet-NaN bit patterns (written as integers: the kernels are compiled
+    // on the assumption of no NaN arithmetic)
+    constexpr uint32_t kNaN32 = 0x7fc00000u, kNaN16x2 = 0x7fc07fc0u;
 #pragma unroll
-    for (int round = 0; round < 2; ++round) {
+    for (int qb = 0; qb < kQB; ++qb) {
+        const int qr = 16 * qb + r;
+        float mk[4], f[4];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int owner = 2 * round + j;
-            if (owner == w) continue;
+        for (int k = 0; k < 4; ++k) mk[k] = sm[k * QR + qr];
+        const float M = fmaxf(fmaxf(mk[0], mk[1]), fmaxf(mk[2], mk[3]));
+        const float Muse = M == -INFINITY ? 0.f : M;
+        float L = 0.f;
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb)
-                *reinterpret_cast<f32x4*>(xo + (((w * 2 + j) * kQB + qb) * 64 + lane) * 4) =
-                    acc[qb][owner];
+        for (int k = 0; k < 4; ++k) {
+            f[k] = fast_exp2(mk[k] - Muse);
+            L += sl[k * QR + qr] * f[k];
         }
-        __syncthreads();
-        if ((w >> 1) == round) {
-            const int j = w & 1;
+        // the four waves' contributions in wave order, the own one from
+        // registers (a wave-uniform branch keeps acc's indices constant: a
+        // runtime index would move the accumulators to scratch memory)
+        f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
-                // acc[qb][w] with constant indices (a runtime index would move
-                // the accumulators to scratch memory).
-                f32x4 o = j ? acc[qb][2 * round + 1] : acc[qb][2 * round];
-#pragma unroll
-                for (int ww = 0; ww < 4; ++ww) {
-                    if (ww == w) continue;
-                    o += *reinterpret_cast<const f32x4*>(xo + (((ww * 2 + j) * kQB + qb) * 64 + lane) * 4);
-                }
-                const int q = q0 + 16 * qb + r;
-                if (q >= a.Sq) continue;
-                // poison: quiet-NaN bit patterns (written as integers: the
-                // kernels are compiled on the assumption of no NaN arithmetic)
-                constexpr uint32_t kNaN32 = 0x7fc00000u, kNaN16x2 = 0x7fc07fc0u;
-                if (nsplit == 1) {
-                    const float inv = Lq[qb] > 0.f ? 1.f / Lq[qb] : 0.f;
-                    o *= inv;
-                    const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + d0;
-                    if (a.out_f32) {
-                        u32x4 ob = __builtin_bit_cast(u32x4, o);
-                        if (poison) ob = u32x4{kNaN32, kNaN32, kNaN32, kNaN32};
-                        *reinterpret_cast<u32x4*>(reinterpret_cast<float*>(a.o) + off) = ob;
-                    } else {
-                        uint2 pk2;
-                        pk2.x = poison ? kNaN16x2 : pack_bf16x2(o[0], o[1]);
-                        pk2.y = poison ? kNaN16x2 : pack_bf16x2(o[2], o[3]);
-                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.o) + off) = pk2;
-                    }
-                } else {
-                    u32x4 ob = __builtin_bit_cast(u32x4, o);
-                    if (poison) ob = u32x4{kNaN32, kNaN32, kNaN32, kNaN32};
-                    *reinterpret_cast<u32x4*>(a.part_o + (pbase + q) * kD + d0) = ob;
-                    if (w == 0 && g == 0) {
-                        uint32_t* ml = reinterpret_cast<uint32_t*>(a.part_ml + (pbase + q) * 2);
-                        ml[0] = poison ? kNaN32 : __float_as_uint(Mq[qb]);
-                        ml[1] = poison ? kNaN32 : __float_as_uint(Lq[qb]);
-                    }
-                }
+        for (int k = 0; k < 4; ++k) {
+            if (k == w) {
+                o += acc[qb][k] * f[k];
+            } else {
+                const int slot = w - (w > k ? 1 : 0);
+                o += *reinterpret_cast<const f32x4*>(xo + (((k * 3 + slot) * kQB + qb) * 64 + lane) * 4) * f[k];
             }
         }
-        if (round == 0) __syncthreads();
+        const int q = q0 + qr;
+        if (q >= a.Sq) continue;
+        if (nsplit == 1) {
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            o *= inv;
+            const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + d0;
+            if (a.out_f32) {
+                u32x4 ob = __builtin_bit_cast(u32x4, o);
+                if (poison) ob = u32x4{kNaN32, kNaN32, kNaN32, kNaN32};
+                *reinterpret_cast<u32x4*>(reinterpret_cast<float*>(a.o) + off) = ob;
+            } else {
+                uint2 pk2;
+                pk2.x = poison ? kNaN16x2 : pack_bf16x2(o[0], o[1]);
+                pk2.y = poison ? kNaN16x2 : pack_bf16x2(o[2], o[3]);
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.o) + off) = pk2;
+            }
+        } else {
+            u32x4 ob = __builtin_bit_cast(u32x4, o);
+            if (poison) ob = u32x4{kNaN32, kNaN32, kNaN32, kNaN32};
+            *reinterpret_cast<u32x4*>(a.part_o + (pbase + q) * kD + d0) = ob;
+            if (w == 0 && g == 0) {
+                uint32_t* ml = reinterpret_cast<uint32_t*>(a.part_ml + (pbase + q) * 2);
+                ml[0] = poison ? kNaN32 : __float_as_uint(M);
+                ml[1] = poison ? kNaN32 : __float_as_uint(L);
+            }
+        }
     }
 }
 
@@ -623,11 +615,8 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) l[qb] = __shfl(accl[qb][0], r, 64);
-    // V outside the fp16 form's range anywhere in this workgroup's keys: its
-    // rows (or split partials) become NaN rather than silently saturated.
-    const bool poison = !kExactPV && __syncthreads_or(v_out_of_range);
     attn_split_epilogue(a, reinterpret_cast<float*>(ring), acc, m, l, w, g, r, lane, b, h, q0,
-                        split, nsplit, false, poison);
+                        split, nsplit, !kExactPV && v_out_of_range);
 }
 
 // Log-sum-exp merge of the split partials.  One wave per output row
