@@ -546,7 +546,7 @@ __global__ __launch_bounds__(kAddNormThreads) void reduce_addnorm_kernel(const E
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
+    lds_barrier();   // the residual stores above stay in flight
     float total = 0.f;
 #pragma unroll
     for (int w = 0; w < kAddNormThreads / 64; ++w) total += red[w];
