@@ -181,6 +181,40 @@ def test_sample_graph_equals_eager_and_oracle():
     assert mean_rel(eager - x0, ref - x0) < 8 * max(floor, 1e-4)
 
 
+def test_condition_cache_semantics():
+    """The cached condition K/V behave as the engine's condition cache
+    (test_vla_pipeline.cpp:69-153 checks re-encode on a new frame and reuse
+    otherwise): repeated samples with one condition reuse it (identical
+    bits, the captured graph replayed), a new condition replaces it (the
+    replayed graph then gives what an eager run on a fresh model with that
+    condition gives), and going back to the first condition reproduces the
+    first result exactly -- nothing of the old condition survives."""
+    c = small_cfg()
+    m = build(c)
+    cond_a = make_condition(c, seed=5)
+    cond_b = make_condition(c, seed=50, lang_len=[40, 96])
+    x0 = O.randn(7, (c.batch, c.horizon, c.action_dim))
+
+    def run(model, use_graph):
+        x = torch.from_numpy(x0).to(DEV)
+        model.sample(x, use_graph=use_graph)
+        torch.cuda.synchronize()
+        return x.cpu().numpy()
+
+    set_cond(m, *cond_a)
+    a1 = run(m, True)
+    a2 = run(m, True)
+    assert np.array_equal(a1, a2)
+    set_cond(m, *cond_b)
+    b1 = run(m, True)
+    assert not np.array_equal(b1, a1)
+    fresh = build(c)
+    set_cond(fresh, *cond_b)
+    assert np.array_equal(b1, run(fresh, False))
+    set_cond(m, *cond_a)
+    assert np.array_equal(run(m, True), a1)
+
+
 def test_batch_slots_are_independent():
     # lang_max 192: the condition projections (rows B*192) take the same GEMM
     # kernel at batch 1 and 2, so each slot sees the same summation order and
