@@ -21,7 +21,9 @@ and the one-time condition encode.
 
 `cpu_baseline` is the CPU oracle (oracle/, the fp32 restatement of the
 reference's RDTBlock / denoise_step / naive attention) timed on the host
-cores: one full 28-layer denoise step, scaled by 5 to a loop.
+cores: one full 28-layer denoise step, scaled by 5 to a loop.  `extra`
+also carries the oracle's attention ops of configs 1 and 2 on the host
+(`cpu_self_b1_ms`, `cpu_cross_img_b1_ms`) beside their GPU times.
 """
 import argparse
 import json
@@ -260,6 +262,31 @@ def cpu_baseline(budget_s=25.0):
     }
 
 
+def cpu_attention_ops():
+    """The attention ops of configs 1 and 2 on the host cores: the oracle's
+    fp32 restatement of naive_attention_kernel (attention.cu:90-139), median
+    of 3 runs each -- the self-attention op (1 x 32 heads x 67 x 67 x 64,
+    fp32) and the batch-1 image cross-attention op (67 queries x 4374 keys)."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    def med(fn):
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)) * 1e3
+
+    q = O.randn(31, (1, 32, 67, 64))
+    k, v = O.randn(32, (1, 32, 67, 64)), O.randn(33, (1, 32, 67, 64))
+    self_ms = med(lambda: O.attention_f32(q, k, v))
+    k, v = O.bf16_round(O.randn(34, (1, 32, 4374, 64))), O.bf16_round(O.randn(35, (1, 32, 4374, 64)))
+    cross_ms = med(lambda: O.attention_f32(q, k, v))
+    return {"cpu_self_b1_ms": round(self_ms, 3), "cpu_cross_img_b1_ms": round(cross_ms, 3)}
+
+
 def profile_roofline(iters=50):
     """Runs only what the roofline profiles measure: the batch-1 image
     cross-attention op (attn_ring_kernel + attn_merge_kernel) `iters` times,
@@ -370,6 +397,8 @@ def main():
             del m
             torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_baseline()
+    if cpu is not None:
+        extra.update(cpu_attention_ops())
     line = {
         "metric": METRIC,
         "value": round(loop1, 4),
