@@ -6,7 +6,7 @@
 // (src/backend/cuda/ops/attention.cu:183-197), whose arithmetic is the
 // online-softmax loop of naive_attention_kernel (attention.cu:90-139).
 //
-// Design (the split kernel serves the 67 x 4374 / 67 x <=1024
+// Design (the ring kernel serves the 67 x 4374 / 67 x <=1024
 // cross-attention; attn_short_kernel below serves key sets of <= 128, the
 // 67 x 67 self-attention):
 //   * grid = (splits x query-chunks, H, B); a workgroup of 4 waves owns one
@@ -23,9 +23,11 @@
 //     accumulator layout (lane = query, 4 consecutive keys per lane) is
 //     directly the B operand P^T, so no shuffle sits between the two
 //     contractions.
-//   * P is carried as a bf16 (hi, lo) pair so the P.V contraction keeps ~16
-//     mantissa bits; a single bf16 P costs ~1.1e-3 mean relative error on
-//     its own, which is the whole 1e-3 budget.
+//   * P.V runs in fp16 by default (V converted exactly below 2^16, P
+//     rounded to fp16; ~2.4e-4 mean relative error) with NaN rows for V out
+//     of that range; the exact form carries P as a bf16 (hi, lo) pair against
+//     bf16 V (~16 mantissa bits of P: a single bf16 P costs ~1.1e-3 mean
+//     relative error on its own, the whole 1e-3 budget).
 //   * Online softmax in the log2 domain; the four waves' (m, l, O) merge in
 //     LDS; multi-split partials merge in a second small kernel.
 #include <hip/hip_runtime.h>
@@ -270,11 +272,11 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
 // key row k XOR-swizzled by (k >> 1) & 7, which makes both the K fragment
 // reads (16 rows x 16 B) and the V^T transpose reads (4 rows x 8 B per
 // 16-lane group) bank-conflict free.  Q fragments live in registers.  The
-// arithmetic (S^T = K.Q^T, lazy-rescaled log2 softmax, P as a bf16 hi/lo
-// pair, O^T += V^T.P^T, 4-wave LDS merge) is the split kernel's, except that
-// the row sums come from the MFMA pipe: a constant V^T fragment whose first
-// row is all ones turns P^T into l, so the VALU does no per-element adds and
-// l sums exactly the (hi + lo) weights the numerator uses.
+// arithmetic: S^T = K.Q^T, lazy-rescaled log2 softmax, O^T += V^T.P^T
+// (fp16, or bf16 with P as a hi/lo pair), 4-wave LDS merge; the row sums
+// come from the MFMA pipe: a constant V^T fragment whose first row is all
+// ones turns P^T into l, so the VALU does no per-element adds and l sums
+// exactly the rounded weights the numerator uses.
 // ---------------------------------------------------------------------------
 constexpr int kRingStages = 2;
 constexpr int kKT = 128;                          // keys per tile (4 waves x 32)
