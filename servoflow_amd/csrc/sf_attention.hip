@@ -622,19 +622,19 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 }
 
 // Log-sum-exp merge of the split partials.  One wave per output row
-// (b, h, q): lane s < nsplit loads split s's (max, sum), the wave reduces
-// them, and each lane then accumulates head dim d = lane over the splits with
-// the loads unrolled so they overlap.
+// (b, h, q): lane s < nsplit loads split s's (max, sum) and every lane loads
+// head dim d = lane of every split's partial output, all up front; the
+// splits' (max, sum) then come to every lane through v_readlane (scalar
+// registers, no LDS round trips), and each lane forms
+// out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     const int lane = threadIdx.x & 63;
     const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int h = blockIdx.y;
     const int b = blockIdx.z;
     if (q >= a.Sq) return;
-    const int ns = a.nsplit;
+    const int ns = a.nsplit;   // <= kMaxSplits = 64
     const size_t row0 = ((size_t)b * a.H + h) * ns * (size_t)a.Sq + q;   // split 0's row
-    // every load first: this lane's split (m, l) and head dim `lane` of the
-    // first kMergeBatch splits' partial outputs
     constexpr int kMergeBatch = 16;
     float ms = -INFINITY, ls = 0.f;
     bool poisoned = false;   // a split marked its partials NaN (V out of range)
@@ -647,28 +647,35 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     float v0[kMergeBatch];
 #pragma unroll
     for (int j = 0; j < kMergeBatch; ++j)
-        v0[j] = a.part_o[(row0 + (size_t)min(j, ns - 1) * a.Sq) * kD + lane];
-    float M = ms;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        if (j < ns) v0[j] = a.part_o[(row0 + (size_t)j * a.Sq) * kD + lane];
+    float M = -INFINITY;
+    for (int j = 0; j < ns; ++j) M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(ms), j)));
     const float Muse = M == -INFINITY ? 0.f : M;
-    float wgt = lane < ns ? fast_exp2(ms - Muse) : 0.f;
-    float L = wgt * ls;
+    float L = 0.f, o = 0.f;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
-    wgt *= L > 0.f ? 1.f / L : 0.f;
-    float o = 0.f;
-#pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j)
-        if (j < ns) o += __shfl(wgt, j, 64) * v0[j];
+    for (int j = 0; j < kMergeBatch; ++j) {
+        if (j < ns) {
+            const float e = fast_exp2(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(ms), j)) - Muse);
+            L += e * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(ls), j));
+            o += e * v0[j];
+        }
+    }
     for (int s0 = kMergeBatch; s0 < ns; s0 += 8) {
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             v[j] = s0 + j < ns ? a.part_o[(row0 + (size_t)(s0 + j) * a.Sq) * kD + lane] : 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o += __shfl(wgt, s0 + j < ns ? s0 + j : 0, 64) * v[j];
+        for (int j = 0; j < 8; ++j) {
+            if (s0 + j < ns) {
+                const float e = fast_exp2(
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(ms), s0 + j)) - Muse);
+                L += e * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(ls), s0 + j));
+                o += e * v[j];
+            }
+        }
     }
+    o *= L > 0.f ? 1.f / L : 0.f;
     if (__any(poisoned)) {   // NaN bits written as integers (no-NaN arithmetic assumed)
         const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + lane;
         if (a.out_f32) reinterpret_cast<uint32_t*>(a.o)[off] = 0x7fc00000u;

@@ -260,6 +260,27 @@ struct SkArgs {
 
 // LDS barrier that leaves outstanding global loads in flight (a plain
 // __syncthreads also waits for every vector-memory load of the wave).
+// Sum over the 16 lanes of each row (DPP quad permutes, then the row's half
+// mirror and mirror: VALU only, no LDS round trip); every lane of the row
+// gets the sum, added in the order of an xor butterfly over 1, 2, 4, 8.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));   // quad_perm 1,0,3,2
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));   // quad_perm 2,3,0,1
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, true));  // row_half_mirror
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF, true));  // row_mirror
+    return x;
+}
+
+// Sum over the 64 lanes of a wave: the row sums, then the rows paired by
+// v_permlane16_swap and v_permlane32_swap (VALU lane swaps of gfx950).
+__device__ __forceinline__ float wave_sum(float x) {
+    x = row16_sum(x);
+    auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
@@ -495,8 +516,7 @@ __global__ __launch_bounds__(256) void reduce_heads_kernel(const EpiArgs e) {
         const f32x4 gq = *reinterpret_cast<const f32x4*>(gamma + d);
         // rms_norm_kernel_impl over the 64 head dims (norm.cuh:89-122)
         float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) ss += __shfl_xor(ss, off, 64);
+        ss = row16_sum(ss);
         const float inv_rms = 1.f / sqrtf(ss / 64.f + e.eps);
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = v[j] * inv_rms * gq[j];
@@ -543,8 +563,7 @@ __global__ __launch_bounds__(kAddNormThreads) void reduce_addnorm_kernel(const E
 #pragma unroll
     for (int i = 0; i < kAddNormMaxChunks; ++i)
         if (i < nch) *reinterpret_cast<f32x4*>(x + 4 * ((int)threadIdx.x + kAddNormThreads * i)) = xv[i];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    ss = wave_sum(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     lds_barrier();   // the residual stores above stay in flight
     float total = 0.f;
