@@ -295,11 +295,13 @@ __device__ __forceinline__ uint32_t mask_word(__amdgpu_buffer_rsrc_t mrs, int ke
 }
 
 // Wait until at most one tile's loads (8 per wave) of this wave are still
-// outstanding, then barrier: every wave's share of the older tile has landed.
-// Vector loads complete in issue order, so this covers the tile being
-// waited for and every load issued before it (Q, mask words).
-__device__ __forceinline__ void ring_wait_barrier() {
-    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+// outstanding: the older tile has landed.  Vector loads complete in issue
+// order, so this covers the tile being waited for and every load issued
+// before it (Q, mask words).  No barrier: a wave's DMA fills exactly the 32
+// key rows of K and V that the same wave contracts, so no wave ever reads
+// LDS that another wave writes inside the tile loop.
+__device__ __forceinline__ void ring_wait() {
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 }
 
 template <bool kExactPV>   // false: P.V in fp16 (V exact below 2^16); true: bf16 V, P as (hi, lo)
@@ -397,7 +399,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     // tiles at or past ntiles lie beyond the buffer range and load zeros (no
     // memory traffic).  With the issue unconditional, the compiler's own
     // vmcnt bookkeeping sees the ring loads as always in flight behind Q and
-    // the mask words, and ring_wait_barrier waits for one tile at a time.
+    // the mask words, and ring_wait waits for one tile at a time.
     issue(0);
     issue(1);
     // Wait for the Q fragments here, behind the first tiles' loads.  Inside
@@ -457,7 +459,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     auto tile = [&](const int t, auto soff) {
         constexpr int SOFF = decltype(soff)::value;
         const int kt = kbeg + t * kKT;
-        ring_wait_barrier();   // tile t has landed; tile t + 1 may still stream in
+        ring_wait();   // tile t has landed; tile t + 1 may still stream in
         if (kt + wkey < kend && !(a.causal && kt + wkey > q0 + QR - 1)) {
             // K fragments, then V^T: K is waited for before the S contraction,
             // V^T only before P.V, so the transpose reads overlap S.
@@ -601,8 +603,8 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                 }
             }
         }   // live keys
-        // every wave is done with this stage before it is refilled
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // this wave's reads of the stage are done before its rows are refilled
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (a.kv_mask) load_mask(t + 1, mw_next);
         issue(t + kRingStages);
     };
