@@ -159,83 +159,88 @@ __device__ __forceinline__ float max_xor32(float x) {
 
 // Epilogue of the ring kernel: the four waves' (m, l, O) merged through LDS
 // (xo_base: >= 64 KB of LDS no longer in use), then the normalised output
-// (one split) or the split's partials.  Wave w owns head dims
-// [16w, 16w + 16).  Every wave writes its row maxima and sums, its
+// (one split) or the split's partials.  Wave W owns head dims
+// [16W, 16W + 16).  Every wave writes its row maxima and sums (lanes 0..15
+// hold a row's sum in element 0 of the row-sum accumulator), its
 // out-of-range flag and, unscaled, the three d-blocks it does not own; after
 // ONE barrier each owner takes the four waves' maxima, scales the four
 // contributions to its d-block and sums them, so each output element is
-// summed once and stored as a 4-vector.
+// summed once and stored as a 4-vector.  W is a template parameter (the
+// caller switches on the wave index): the owner's block is then a constant
+// register index, and every LDS read of the merge is issued before the
+// first one is used (one LDS round trip instead of one per row block).
+template <int W>
 __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo_base,
-                                                    f32x4 (&acc)[kQB][4], const float (&m)[kQB],
-                                                    const float (&l)[kQB], int w, int g, int r, int lane,
-                                                    int b, int h, int q0, int split, int nsplit,
+                                                    const f32x4 (&acc)[kQB][4], const f32x4 (&accl)[kQB],
+                                                    const float (&m)[kQB], int g, int r, int lane, int b,
+                                                    int h, int q0, int split, int nsplit,
                                                     bool v_out_of_range) {
     constexpr int QR = 16 * kQB;
     float* xo = xo_base;                                  // [4 writer][3 slot][kQB][64 lanes][4]
-    float* sm = xo + 4 * 3 * kQB * 64 * 4;                // [4][QR]
-    float* sl = sm + 4 * QR;                              // [4][QR]
+    float* sm = xo + 4 * 3 * kQB * 64 * 4;                // [QR][4 writer]
+    float* sl = sm + 4 * QR;                              // [QR][4 writer]
     uint32_t* pz = reinterpret_cast<uint32_t*>(sl + 4 * QR);   // [4] per-wave out-of-range flags
     static_assert((4 * 3 * kQB * 64 * 4 + 2 * 4 * QR + 4) * 4 <= 2 * 32768, "fits the ring's LDS");
 #pragma unroll
     for (int o = 0; o < 4; ++o) {
-        if (o == w) continue;
-        const int slot = o - (o > w ? 1 : 0);
+        if (o == W) continue;
+        const int slot = o - (o > W ? 1 : 0);
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb)
-            *reinterpret_cast<f32x4*>(xo + (((w * 3 + slot) * kQB + qb) * 64 + lane) * 4) = acc[qb][o];
+            *reinterpret_cast<f32x4*>(xo + (((W * 3 + slot) * kQB + qb) * 64 + lane) * 4) = acc[qb][o];
     }
     if (g == 0) {
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
-            sm[w * QR + 16 * qb + r] = m[qb];
-            sl[w * QR + 16 * qb + r] = l[qb];
+            sm[(16 * qb + r) * 4 + W] = m[qb];
+            sl[(16 * qb + r) * 4 + W] = accl[qb][0];
         }
     }
     const bool wave_oor = __any(v_out_of_range);
-    if (lane == 0) pz[w] = wave_oor ? 1u : 0u;
+    if (lane == 0) pz[W] = wave_oor ? 1u : 0u;
     __syncthreads();
 
+    // every read, then the arithmetic
+    const u32x4 pzv = *reinterpret_cast<const u32x4*>(pz);
+    f32x4 mk[kQB], lk[kQB], c[kQB][3];
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+        mk[qb] = *reinterpret_cast<const f32x4*>(sm + (16 * qb + r) * 4);
+        lk[qb] = *reinterpret_cast<const f32x4*>(sl + (16 * qb + r) * 4);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int k = j + (j >= W ? 1 : 0);          // the other writers, in wave order
+            const int slot = W - (W > k ? 1 : 0);        // W's slot in writer k's blocks
+            c[qb][j] = *reinterpret_cast<const f32x4*>(xo + (((k * 3 + slot) * kQB + qb) * 64 + lane) * 4);
+        }
+    }
     // V outside the fp16 form's range anywhere in this workgroup's keys: its
     // rows (or split partials) become NaN rather than silently saturated.
-    const bool poison = (pz[0] | pz[1] | pz[2] | pz[3]) != 0;
+    const bool poison = (pzv[0] | pzv[1] | pzv[2] | pzv[3]) != 0;
     const size_t bh = (size_t)b * a.H + h;
     const size_t pbase = (bh * nsplit + split) * (size_t)a.Sq;
-    const int d0 = 16 * w + 4 * g;
+    const int d0 = 16 * W + 4 * g;
     // quiet-NaN bit patterns (written as integers: the kernels are compiled
     // on the assumption of no NaN arithmetic)
     constexpr uint32_t kNaN32 = 0x7fc00000u, kNaN16x2 = 0x7fc07fc0u;
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
-        const int qr = 16 * qb + r;
-        float mk[4], f[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) mk[k] = sm[k * QR + qr];
-        const float M = fmaxf(fmaxf(mk[0], mk[1]), fmaxf(mk[2], mk[3]));
+        const float M = fmaxf(fmaxf(mk[qb][0], mk[qb][1]), fmaxf(mk[qb][2], mk[qb][3]));
         const float Muse = M == -INFINITY ? 0.f : M;
+        float f[4];
         float L = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            f[k] = fast_exp2(mk[k] - Muse);
-            L += sl[k * QR + qr] * f[k];
+            f[k] = fast_exp2(mk[qb][k] - Muse);
+            L += lk[qb][k] * f[k];
         }
-        // the four waves' contributions in wave order, the own one from
-        // registers (a wave-uniform branch keeps acc's indices constant: a
-        // runtime index would move the accumulators to scratch memory)
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
+        f32x4 o = acc[qb][W] * f[W];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if (k == w) {
-                o += acc[qb][k] * f[k];
-            } else {
-                const int slot = w - (w > k ? 1 : 0);
-                o += *reinterpret_cast<const f32x4*>(xo + (((k * 3 + slot) * kQB + qb) * 64 + lane) * 4) * f[k];
-            }
-        }
-        const int q = q0 + qr;
+        for (int j = 0; j < 3; ++j) o += c[qb][j] * f[j + (j >= W ? 1 : 0)];
+        const int q = q0 + 16 * qb + r;
         if (q >= a.Sq) continue;
         if (nsplit == 1) {
-            const float inv = L > 0.f ? 1.f / L : 0.f;
-            o *= inv;
+            o *= L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
             const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + d0;
             if (a.out_f32) {
                 u32x4 ob = __builtin_bit_cast(u32x4, o);
@@ -251,7 +256,7 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
             u32x4 ob = __builtin_bit_cast(u32x4, o);
             if (poison) ob = u32x4{kNaN32, kNaN32, kNaN32, kNaN32};
             *reinterpret_cast<u32x4*>(a.part_o + (pbase + q) * kD + d0) = ob;
-            if (w == 0 && g == 0) {
+            if (W == 0 && g == 0) {
                 uint32_t* ml = reinterpret_cast<uint32_t*>(a.part_ml + (pbase + q) * 2);
                 ml[0] = poison ? kNaN32 : __float_as_uint(M);
                 ml[1] = poison ? kNaN32 : __float_as_uint(L);
@@ -416,7 +421,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     // m: running max of each query row in log2 units (-inf until a finite
     // score has been seen).  A tile whose raw scores stay at or below
     // (m + 8) / scale_log2 keeps m, so every weight is <= 2^8.
-    float m[kQB], l[kQB];
+    float m[kQB];
     const float inv_sl2 = 1.f / a.scale_log2;
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
@@ -617,10 +622,14 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     // The loads issued past the last tile land in LDS that the epilogue
     // reuses: every wave waits for its own, then all waves meet.
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-#pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) l[qb] = __shfl(accl[qb][0], r, 64);
-    attn_split_epilogue(a, reinterpret_cast<float*>(ring), acc, m, l, w, g, r, lane, b, h, q0,
-                        split, nsplit, !kExactPV && v_out_of_range);
+    float* xo = reinterpret_cast<float*>(ring);
+    const bool oor = !kExactPV && v_out_of_range;
+    switch (w) {   // wave-uniform
+        case 0: attn_split_epilogue<0>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit, oor); break;
+        case 1: attn_split_epilogue<1>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit, oor); break;
+        case 2: attn_split_epilogue<2>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit, oor); break;
+        default: attn_split_epilogue<3>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit, oor); break;
+    }
 }
 
 // Log-sum-exp merge of the split partials.  One wave per output row

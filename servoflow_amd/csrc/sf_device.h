@@ -1,8 +1,8 @@
 // Device-side helpers shared by the gfx950 kernels of libsf_hip_kernels.so.
 //
-// Vector types match the operand types of the CDNA4 MFMA builtins, and the
-// bf16 conversions are plain bit manipulation so that host tests can restate
-// them exactly (round-to-nearest-even, NaN kept quiet).
+// Vector types match the operand types of the CDNA4 MFMA builtins.  fp32 ->
+// bf16 conversions use gfx950's v_cvt_pk_bf16_f32 (round to nearest even,
+// NaN stays NaN), which host tests restate as the usual bit manipulation.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,6 +11,8 @@
 namespace sfk {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -18,17 +20,14 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
     return __uint_as_float(h << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays NaN.
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+// Two fp32 -> packed bf16x2 (low half = a), one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, bf16x2v));
 }
 
-// Two fp32 -> packed bf16x2 (low half = a).
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+// fp32 -> bf16 bits, round to nearest even; NaN stays NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ bf16x8 u32x4_as_bf16x8(u32x4 v) {
