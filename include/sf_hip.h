@@ -78,14 +78,14 @@ typedef enum sf_dtype {
  * num_splits: 0 chooses the split-K factor automatically; n > 0 forces n
  * (at most 64).
  * exact_pv: 0 (default) runs the key-split kernel's (Sk > 128) P.V
- * contraction in fp16: V converted exactly (bf16's 8 significant bits fit
- * fp16's 11 below 2^16) and P rounded toward zero to fp16, ~2.4e-4 mean
- * relative error on the output.  V must then hold |v| < 2^16: a workgroup
- * that meets a larger or infinite value writes NaN to its output rows (to
- * its split's partials, which the merge turns into NaN rows) instead of a
- * saturated result; a NaN in V propagates as in fp32 arithmetic.  1 keeps V
- * in bf16 and P as a bf16 (hi, lo) pair (~1e-5) for any finite V, at ~15%
- * more time per key tile.
+ * contraction in fp16: V converted with rounding to nearest, exact for
+ * |v| < 2^16 (bf16's 8 significant bits fit fp16's 11), and P rounded to
+ * the nearest fp16, ~2e-4 mean relative error on the output.  A V element
+ * with |v| >= 2^16 converts to +-inf, so the output column (head dim) it
+ * belongs to becomes inf or NaN in every row that attends to its key, never
+ * a saturated value; the other columns are unaffected.  A NaN or inf in V
+ * behaves the same way.  1 keeps V in bf16 and P as a bf16 (hi, lo) pair
+ * (~1e-5) for any finite V, at ~15% more time per key tile.
  * scale must be >= 0 (SF_ENOTSUP otherwise).
  *
  * Supported: in_dtype SF_BF16, out_dtype SF_BF16 or SF_F32, D == 64,

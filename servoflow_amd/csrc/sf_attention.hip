@@ -23,11 +23,11 @@
 //     accumulator layout (lane = query, 4 consecutive keys per lane) is
 //     directly the B operand P^T, so no shuffle sits between the two
 //     contractions.
-//   * P.V runs in fp16 by default (V converted exactly below 2^16, P
-//     rounded to fp16; ~2.4e-4 mean relative error) with NaN rows for V out
-//     of that range; the exact form carries P as a bf16 (hi, lo) pair against
-//     bf16 V (~16 mantissa bits of P: a single bf16 P costs ~1.1e-3 mean
-//     relative error on its own, the whole 1e-3 budget).
+//   * P.V runs in fp16 by default (V converted exactly below 2^16, inf
+//     above, P rounded to the nearest fp16); the exact form carries P as a
+//     bf16 (hi, lo) pair against bf16 V (~16 mantissa bits of P: a single
+//     bf16 P costs ~1.1e-3 mean relative error on its own, the whole 1e-3
+//     budget).
 //   * Online softmax in the log2 domain; the four waves' (m, l, O) merge in
 //     LDS; multi-split partials merge in a second small kernel.
 #include <hip/hip_runtime.h>
@@ -161,8 +161,8 @@ __device__ __forceinline__ float max_xor32(float x) {
 // (xo_base: >= 64 KB of LDS no longer in use), then the normalised output
 // (one split) or the split's partials.  Wave W owns head dims
 // [16W, 16W + 16).  Every wave writes its row maxima and sums (lanes 0..15
-// hold a row's sum in element 0 of the row-sum accumulator), its
-// out-of-range flag and, unscaled, the three d-blocks it does not own; after
+// hold a row's sum in element 0 of the row-sum accumulator) and, unscaled,
+// the three d-blocks it does not own; after
 // ONE barrier each owner takes the four waves' maxima, scales the four
 // contributions to its d-block and sums them, so each output element is
 // summed once and stored as a 4-vector.  W is a template parameter (the
@@ -173,14 +173,12 @@ template <int W>
 __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo_base,
                                                     const f32x4 (&acc)[kQB][4], const f32x4 (&accl)[kQB],
                                                     const float (&m)[kQB], int g, int r, int lane, int b,
-                                                    int h, int q0, int split, int nsplit,
-                                                    bool v_out_of_range) {
+                                                    int h, int q0, int split, int nsplit) {
     constexpr int QR = 16 * kQB;
     float* xo = xo_base;                                  // [4 writer][3 slot][kQB][64 lanes][4]
     float* sm = xo + 4 * 3 * kQB * 64 * 4;                // [QR][4 writer]
     float* sl = sm + 4 * QR;                              // [QR][4 writer]
-    uint32_t* pz = reinterpret_cast<uint32_t*>(sl + 4 * QR);   // [4] per-wave out-of-range flags
-    static_assert((4 * 3 * kQB * 64 * 4 + 2 * 4 * QR + 4) * 4 <= 2 * 32768, "fits the ring's LDS");
+    static_assert((4 * 3 * kQB * 64 * 4 + 2 * 4 * QR) * 4 <= 2 * 32768, "fits the ring's LDS");
 #pragma unroll
     for (int o = 0; o < 4; ++o) {
         if (o == W) continue;
@@ -196,12 +194,9 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
             sl[(16 * qb + r) * 4 + W] = accl[qb][0];
         }
     }
-    const bool wave_oor = __any(v_out_of_range);
-    if (lane == 0) pz[W] = wave_oor ? 1u : 0u;
     __syncthreads();
 
     // every read, then the arithmetic
-    const u32x4 pzv = *reinterpret_cast<const u32x4*>(pz);
     f32x4 mk[kQB], lk[kQB], c[kQB][3];
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
@@ -214,15 +209,9 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
             c[qb][j] = *reinterpret_cast<const f32x4*>(xo + (((k * 3 + slot) * kQB + qb) * 64 + lane) * 4);
         }
     }
-    // V outside the fp16 form's range anywhere in this workgroup's keys: its
-    // rows (or split partials) become NaN rather than silently saturated.
-    const bool poison = (pzv[0] | pzv[1] | pzv[2] | pzv[3]) != 0;
     const size_t bh = (size_t)b * a.H + h;
     const size_t pbase = (bh * nsplit + split) * (size_t)a.Sq;
     const int d0 = 16 * W + 4 * g;
-    // quiet-NaN bit patterns (written as integers: the kernels are compiled
-    // on the assumption of no NaN arithmetic)
-    constexpr uint32_t kNaN32 = 0x7fc00000u, kNaN16x2 = 0x7fc07fc0u;
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
         const float M = fmaxf(fmaxf(mk[qb][0], mk[qb][1]), fmaxf(mk[qb][2], mk[qb][3]));
@@ -243,24 +232,15 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
             o *= L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
             const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + d0;
             if (a.out_f32) {
-                u32x4 ob = __builtin_bit_cast(u32x4, o);
-                if (poison) ob = u32x4{kNaN32, kNaN32, kNaN32, kNaN32};
-                *reinterpret_cast<u32x4*>(reinterpret_cast<float*>(a.o) + off) = ob;
+                *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.o) + off) = o;
             } else {
-                uint2 pk2;
-                pk2.x = poison ? kNaN16x2 : pack_bf16x2(o[0], o[1]);
-                pk2.y = poison ? kNaN16x2 : pack_bf16x2(o[2], o[3]);
+                const uint2 pk2 = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
                 *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.o) + off) = pk2;
             }
         } else {
-            u32x4 ob = __builtin_bit_cast(u32x4, o);
-            if (poison) ob = u32x4{kNaN32, kNaN32, kNaN32, kNaN32};
-            *reinterpret_cast<u32x4*>(a.part_o + (pbase + q) * kD + d0) = ob;
-            if (W == 0 && g == 0) {
-                uint32_t* ml = reinterpret_cast<uint32_t*>(a.part_ml + (pbase + q) * 2);
-                ml[0] = poison ? kNaN32 : __float_as_uint(M);
-                ml[1] = poison ? kNaN32 : __float_as_uint(L);
-            }
+            *reinterpret_cast<f32x4*>(a.part_o + (pbase + q) * kD + d0) = o;
+            if (W == 0 && g == 0)
+                *reinterpret_cast<float2*>(a.part_ml + (pbase + q) * 2) = float2{M, L};
         }
     }
 }
@@ -419,13 +399,15 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     f32x4 acc[kQB][4];   // O^T blocks: lane holds d = 16db + 4g + i, q = 16qb + r
     f32x4 accl[kQB];     // row sums: element 0 of lanes 0..15 holds l of query 16qb + r
     // m: running max of each query row in log2 units (-inf until a finite
-    // score has been seen).  A tile whose raw scores stay at or below
-    // (m + 8) / scale_log2 keeps m, so every weight is <= 2^8.
-    float m[kQB];
+    // score has been seen); nm: the offset the weights use, -m (0 while m is
+    // -inf).  A tile whose raw scores stay at or below (m + 8) / scale_log2
+    // keeps m, so every weight is <= 2^8.
+    float m[kQB], nm[kQB];
     const float inv_sl2 = 1.f / a.scale_log2;
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
         m[qb] = -INFINITY;
+        nm[qb] = 0.f;
         accl[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int db = 0; db < 4; ++db) acc[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -435,7 +417,6 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     const bf16x8 ones = u32x4_as_bf16x8(u32x4{one2, one2, one2, one2});
     const uint32_t oneh = r == 0 ? 0x3c003c00u : 0u;
     const f16x8 ones_f16 = u32x4_as_f16x8(u32x4{oneh, oneh, oneh, oneh});
-    bool v_out_of_range = false;   // fp16 form: some |v| >= 2^16 (inf included)
 
     const int wkey = 32 * w;   // this wave's first key inside a tile
     // LDS byte addresses of this lane's K fragment and V^T transpose reads in
@@ -528,6 +509,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                 for (int qb = 0; qb < kQB; ++qb) {
                     const float mx = max_xor32(max_xor16(lmx[qb])) * a.scale_log2;
                     const float mnew = fmaxf(m[qb], mx);
+                    if constexpr (!kExactPV) nm[qb] = mnew == -INFINITY ? 0.f : -mnew;
                     const float alpha = fast_exp2(m[qb] - (mnew == -INFINITY ? 0.f : mnew));
                     m[qb] = mnew;
                     accl[qb] *= alpha;
@@ -535,17 +517,17 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                     for (int db = 0; db < 4; ++db) acc[qb][db] *= alpha;
                 }
             }
-            // V^T fragments: bf16 as read (exact form), or converted to fp16,
-            // which is exact for |v| < 2^16 (bf16's 8 significant bits fit
-            // fp16's 11); the lane notes any larger value (a NaN, which the
-            // max ignores, propagates through the arithmetic instead).
+            // V^T fragments: bf16 as read (exact form), or converted to fp16
+            // with rounding to nearest, which is exact for |v| < 2^16 (bf16's
+            // 8 significant bits fit fp16's 11) and gives +-inf above: an
+            // out-of-range (or infinite or NaN) v makes the output columns it
+            // reaches inf or NaN, never a saturated value.
             bf16x8 vf[4];
             f16x8 vh[4];
             {
                 // V^T landed
                 asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vt[0]), "+v"(vt[1]), "+v"(vt[2]), "+v"(vt[3]),
                              "+v"(vt[4]), "+v"(vt[5]), "+v"(vt[6]), "+v"(vt[7]) :: "memory");
-                float vmax = 0.f;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
                     const u32x4 vw = {vt[2 * db][0], vt[2 * db][1], vt[2 * db + 1][0], vt[2 * db + 1][1]};
@@ -557,30 +539,27 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                         for (int e = 0; e < 4; ++e) {
                             const float lo = __uint_as_float(vw[e] << 16);
                             const float hi = __uint_as_float(vw[e] & 0xffff0000u);
-                            hw[e] = pack_f16x2_rtz(lo, hi);
-                            vmax = fmaxf(vmax, fmaxf(fabsf(lo), fabsf(hi)));
+                            hw[e] = pack_f16x2_rn(lo, hi);
                         }
                         vh[db] = u32x4_as_f16x8(hw);
                     }
                 }
-                if constexpr (!kExactPV) v_out_of_range |= !(vmax < 65536.f);
             }
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb) {
-                const float nmuse = m[qb] == -INFINITY ? 0.f : -m[qb];
                 if constexpr (!kExactPV) {
-                    // P rounded toward zero to fp16 (P <= 2^8 by the lazy
-                    // rescale; ~2.4e-4 mean relative error on the output); l
-                    // sums the same rounded weights.
+                    // P rounded to the nearest fp16 (P <= 2^8 by the lazy
+                    // rescale); l sums the same rounded weights.
                     float pf[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) pf[j] = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nmuse));
-                    const f16x8 p8 = u32x4_as_f16x8(u32x4{pack_f16x2_rtz(pf[0], pf[1]), pack_f16x2_rtz(pf[2], pf[3]),
-                                                          pack_f16x2_rtz(pf[4], pf[5]), pack_f16x2_rtz(pf[6], pf[7])});
+                    for (int j = 0; j < 8; ++j) pf[j] = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nm[qb]));
+                    const f16x8 p8 = u32x4_as_f16x8(u32x4{pack_f16x2_rn(pf[0], pf[1]), pack_f16x2_rn(pf[2], pf[3]),
+                                                          pack_f16x2_rn(pf[4], pf[5]), pack_f16x2_rn(pf[6], pf[7])});
 #pragma unroll
                     for (int db = 0; db < 4; ++db) acc[qb][db] = mfma16x16x32_f16(vh[db], p8, acc[qb][db]);
                     accl[qb] = mfma16x16x32_f16(ones_f16, p8, accl[qb]);
                 } else {
+                    const float nmuse = m[qb] == -INFINITY ? 0.f : -m[qb];
                     uint32_t pb[8], lb[8];
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
@@ -623,12 +602,11 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     // reuses: every wave waits for its own, then all waves meet.
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     float* xo = reinterpret_cast<float*>(ring);
-    const bool oor = !kExactPV && v_out_of_range;
     switch (w) {   // wave-uniform
-        case 0: attn_split_epilogue<0>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit, oor); break;
-        case 1: attn_split_epilogue<1>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit, oor); break;
-        case 2: attn_split_epilogue<2>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit, oor); break;
-        default: attn_split_epilogue<3>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit, oor); break;
+        case 0: attn_split_epilogue<0>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
+        case 1: attn_split_epilogue<1>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
+        case 2: attn_split_epilogue<2>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
+        default: attn_split_epilogue<3>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
     }
 }
 
@@ -648,12 +626,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     const size_t row0 = ((size_t)b * a.H + h) * ns * (size_t)a.Sq + q;   // split 0's row
     constexpr int kMergeBatch = 16;
     float ms = -INFINITY, ls = 0.f;
-    bool poisoned = false;   // a split marked its partials NaN (V out of range)
     if (lane < ns) {
         const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (row0 + (size_t)lane * a.Sq) * 2);
         ms = ml.x;
         ls = ml.y;
-        poisoned = (__float_as_uint(ml.y) & 0x7fffffffu) > 0x7f800000u;
     }
     float v0[kMergeBatch];
 #pragma unroll
@@ -687,12 +663,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
         }
     }
     o *= L > 0.f ? 1.f / L : 0.f;
-    if (__any(poisoned)) {   // NaN bits written as integers (no-NaN arithmetic assumed)
-        const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + lane;
-        if (a.out_f32) reinterpret_cast<uint32_t*>(a.o)[off] = 0x7fc00000u;
-        else reinterpret_cast<uint16_t*>(a.o)[off] = 0x7fc0u;
-        return;
-    }
     store_out(a, b, h, q, lane, o);
 }
 

@@ -56,10 +56,11 @@ __device__ __forceinline__ f16x8 u32x4_as_f16x8(u32x4 v) {
     return __builtin_bit_cast(f16x8, v);
 }
 
-// Two fp32 -> packed fp16x2 (low half = a), rounded toward zero
-// (v_cvt_pkrtz_f16_f32); values beyond the fp16 range saturate to +-65504.
-__device__ __forceinline__ uint32_t pack_f16x2_rtz(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+// Two fp32 -> packed fp16x2 (low half = a), round to nearest even (values
+// beyond the fp16 range give +-inf): one v_cvt_pk_f16_f32.
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_f16x2_rn(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, f16x2v));
 }
 
 // The fp16 form of mfma16x16x32, same operand layout.
