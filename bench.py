@@ -38,11 +38,11 @@ METRIC = "RDT-1B denoise-loop latency ms (bs=1) + cross-attn HBM GB/s vs rooflin
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per roofline op measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (x2.0 / x1.0, scales read off a 256 MiB copy kernel) on `bench.py
-# --profile-roofline`: ring kernel 38.06 MB read + 3.97 MB written, merge
-# 4.47 MB read + 0.27 MB written (profiles/cross_attention_image_roofline.md).
+# --profile-roofline`: ring kernel 38.12 MB read + 3.97 MB written, merge
+# 4.46 MB read + 0.27 MB written (profiles/cross_attention_image_roofline.md).
 # Re-measured whenever the attention kernels change.
-TRAFFIC_B1_IMAGE_BYTES = 46767981
-TRAFFIC_B8_IMAGE_BYTES = 291343591   # same profile, batch-8 op (no key split)
+TRAFFIC_B1_IMAGE_BYTES = 46822248
+TRAFFIC_B8_IMAGE_BYTES = 291396834   # same profile, batch-8 op (no key split)
 
 
 def attn_bytes(B, H, Sq, Sk_valid_total, D=64, eb=2):
