@@ -38,11 +38,11 @@ METRIC = "RDT-1B denoise-loop latency ms (bs=1) + cross-attn HBM GB/s vs rooflin
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per roofline op measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (x2.0 / x1.0, scales read off a 256 MiB copy kernel) on `bench.py
-# --profile-roofline`: ring kernel 38.12 MB read + 3.97 MB written, merge
+# --profile-roofline`: ring kernel 38.13 MB read + 3.97 MB written, merge
 # 4.46 MB read + 0.27 MB written (profiles/cross_attention_image_roofline.md).
 # Re-measured whenever the attention kernels change.
-TRAFFIC_B1_IMAGE_BYTES = 46822248
-TRAFFIC_B8_IMAGE_BYTES = 291396834   # same profile, batch-8 op (no key split)
+TRAFFIC_B1_IMAGE_BYTES = 46831463
+TRAFFIC_B8_IMAGE_BYTES = 291406049   # same profile, batch-8 op (no key split)
 
 
 def attn_bytes(B, H, Sq, Sk_valid_total, D=64, eb=2):
@@ -288,38 +288,21 @@ def cpu_attention_ops():
 
 
 def profile_roofline(iters=50):
-    """Runs only what the roofline profiles measure: the batch-1 image
-    cross-attention op (attn_ring_kernel + attn_merge_kernel) `iters` times,
-    the batch-8 one (attn_ring_kernel alone: no key split) `iters` times,
-    then a plain 256 MiB device-to-device copy `iters` times -- the
-    calibration kernel whose FETCH_SIZE / WRITE_SIZE per dispatch give the
-    counter's scale (256 MiB read, 256 MiB written).  Eager launches, so each
-    dispatch is one kernel-trace / PMC record."""
+    """Runs only what the roofline profiles measure, through the same
+    graph-timed function the bench line uses (bench_attention: 20 calls per
+    graph, HIP events on the capturing stream): the batch-1 image
+    cross-attention op (attn_ring_kernel + attn_merge_kernel) and the
+    batch-8 one (attn_ring_kernel alone: no key split), then a plain 256 MiB
+    device-to-device copy `iters` times -- the calibration kernel whose
+    FETCH_SIZE / WRITE_SIZE per dispatch give the counters' scale (256 MiB
+    read, 256 MiB written)."""
     import torch
 
-    from servoflow_amd.attention import attention, make_desc, workspace_bytes
-
+    for B in (1, 8):
+        r = bench_attention(B, 4374, steps=5, warmup=1)
+        print(f"profile: cross-attention {B}x32x67x4374x64, graph-timed {r['us']:.2f} us per op "
+              f"(under the profiler)", flush=True)
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(1235)
-    q = torch.randn(1, 32, 67, 64, device=dev, generator=g).to(torch.bfloat16)
-    k = torch.randn(1, 32, 4374, 64, device=dev, generator=g).to(torch.bfloat16)
-    v = torch.randn(1, 32, 4374, 64, device=dev, generator=g).to(torch.bfloat16)
-    out = torch.empty(1, 67, 32, 64, device=dev, dtype=torch.bfloat16).permute(0, 2, 1, 3)
-    ws = torch.empty(max(workspace_bytes(make_desc(q, k, v, out)), 16), dtype=torch.uint8, device=dev)
-    for _ in range(iters):
-        attention(q, k, v, out=out, workspace=ws)
-    torch.cuda.synchronize()
-    print(f"profile: {iters} cross-attention ops 1x32x67x4374x64 done", flush=True)
-    q8 = torch.randn(8, 32, 67, 64, device=dev, generator=g).to(torch.bfloat16)
-    k8 = torch.randn(8, 32, 4374, 64, device=dev, generator=g).to(torch.bfloat16)
-    v8 = torch.randn(8, 32, 4374, 64, device=dev, generator=g).to(torch.bfloat16)
-    out8 = torch.empty(8, 67, 32, 64, device=dev, dtype=torch.bfloat16).permute(0, 2, 1, 3)
-    ws8 = torch.empty(max(workspace_bytes(make_desc(q8, k8, v8, out8)), 16), dtype=torch.uint8, device=dev)
-    for _ in range(iters):
-        attention(q8, k8, v8, out=out8, workspace=ws8)
-    torch.cuda.synchronize()
-    print(f"profile: {iters} cross-attention ops 8x32x67x4374x64 done", flush=True)
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     for _ in range(iters):
