@@ -17,7 +17,11 @@ bytes (K and V once, Q in, O out) over its measured duration against the 8 TB/s
 HBM peak.  `extra` reports the other configs: cross-attention batch 8 and
 language keys with valid lengths (config 2), the block stack (config 3), the
 loop at batch 16 (config 4) and the int8-weight loop at batch 32 (config 5),
-and the one-time condition encode.
+and the one-time condition encode, plus the MFMA utilisation the north star
+asks for: the self-attention op and the block projections (`GEMM_SHAPES`:
+batch 1 split-K, batch 16/32 and the condition projection on the library
+path) as algorithmic TFLOP/s over the 2.5 PFLOP/s dense bf16 peak, and for
+the batch-1 (weight-streaming) shapes their HBM rate.
 
 `cpu_baseline` is the CPU oracle (oracle/, the fp32 restatement of the
 reference's RDTBlock / denoise_step / naive attention) timed on the host
@@ -36,6 +40,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "RDT-1B denoise-loop latency ms (bs=1) + cross-attn HBM GB/s vs roofline"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 # HBM bytes per roofline op measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (x2.0 / x1.0, scales read off a 256 MiB copy kernel) on `bench.py
 # --profile-roofline`: ring kernel 38.13 MB read + 3.97 MB written, merge
@@ -116,6 +121,74 @@ def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=Fals
     return {"us": ms * 1e3, "bytes": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9,
             "TFLOPs": attn_flops(H, Sq, sk_total) / (ms * 1e-3) / 1e12,
             "frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
+    """Graph-timed block projection C[M,N] = A[M,K] W[N,K]^T + bias through
+    sf_gemm with a caller workspace (split-K kernel + reduce for M <= 160,
+    hipBLASLt product + reduce above; the shape is prepared first, as the
+    model runtime does).  epilogue: "plain" (bf16 out) or "addnorm" (fp32
+    residual += product, then RMSNorm to bf16).  Returns time, MFMA rate
+    against the dense bf16 peak and the weight-streaming HBM rate."""
+    import ctypes
+
+    import torch
+
+    from servoflow_amd import abi, kernels
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(M + N + K)
+    a = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    if int8:
+        w = torch.randint(-127, 128, (N, K), device=dev, generator=g, dtype=torch.int32).to(torch.int8)
+        ws = torch.rand(N, device=dev, generator=g) * 1e-3
+    else:
+        w = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        ws = None
+    bias = torch.randn(N, device=dev, generator=g) * 0.02
+    d = kernels._desc(a, w, bias, abi.SF_ACT_NONE, ws)
+    wsp = torch.empty(max(int(abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d))), 16),
+                      dtype=torch.uint8, device=dev)
+    if epilogue == "addnorm":
+        res = torch.randn(M, N, device=dev, generator=g)
+        gamma = torch.ones(N, device=dev)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        d.epilogue = abi.SF_EPI_ADD_NORM
+        d.C, d.ldc, d.c_dtype = res.data_ptr(), res.stride(0), abi.SF_F32
+        d.eps = 1e-6
+        d.norm_gamma, d.norm_out = gamma.data_ptr(), out.data_ptr()
+        d.norm_ldo, d.norm_dtype = out.stride(0), abi.SF_BF16
+    else:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        d.epilogue = abi.SF_EPI_PLAIN
+        d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), abi.SF_BF16
+    d.workspace, d.workspace_bytes = wsp.data_ptr(), wsp.numel()
+    abi.check(abi.lib().sf_gemm_prepare(ctypes.byref(d)), "sf_gemm_prepare")
+
+    def fn():
+        abi.check(abi.lib().sf_gemm(ctypes.byref(d), torch.cuda.current_stream(dev).cuda_stream), "sf_gemm")
+
+    ms = time_graph(fn, steps, warmup)
+    flops = 2.0 * M * N * K
+    wbytes = N * K * (1 if int8 else 2)
+    nbytes = wbytes + M * K * 2 + M * N * 2
+    return {"us": ms * 1e3, "TFLOPs": flops / (ms * 1e-3) / 1e12,
+            "mfma_frac": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "GBps": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+# Projection shapes of the block (M = batch * 67 tokens): the 2048-wide
+# projections (proj, cross-q, cross-proj, fc1, fc2), the fused QKV, and the
+# one-time condition K/V projection of the image tokens (M = 4374 per batch).
+GEMM_SHAPES = (
+    ("proj_b1", 67, 2048, 2048, False),
+    ("qkv_b1", 67, 6144, 2048, False),
+    ("proj_b16", 1072, 2048, 2048, False),
+    ("qkv_b16", 1072, 6144, 2048, False),
+    ("proj_int8_b32", 2144, 2048, 2048, True),
+    ("kv_img_b1", 4374, 4096, 2048, False),
+)
 
 
 def make_model(B, int8=False, seed=1234):
@@ -311,6 +384,20 @@ def profile_roofline(iters=50):
     print(f"profile: {iters} copies of 256 MiB done", flush=True)
 
 
+def profile_mfma():
+    """Runs only what the MFMA-utilisation profile measures, through the same
+    graph-timed functions the bench line uses: the batch-1 self-attention op
+    (attn_short_kernel, 1x32x67x67x64) and the block projections of
+    GEMM_SHAPES (split-K kernel + reduce at M = 67, hipBLASLt + reduce
+    above)."""
+    r = bench_attention(1, 67, steps=5, warmup=1)
+    print(f"profile: self-attention 1x32x67x67x64, graph-timed {r['us']:.2f} us per op", flush=True)
+    for name, M, N, K, int8 in GEMM_SHAPES:
+        r = bench_gemm(M, N, K, steps=5, warmup=1, int8=int8)
+        print(f"profile: gemm {name} {M}x{N}x{K}{' int8' if int8 else ''}, graph-timed "
+              f"{r['us']:.2f} us per call", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -320,6 +407,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline and roofline only")
     ap.add_argument("--profile-roofline", action="store_true",
                     help="run only the roofline op and the copy calibration kernel (for rocprofv3)")
+    ap.add_argument("--profile-mfma", action="store_true",
+                    help="run only the self-attention op and the projection GEMMs (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -332,6 +421,9 @@ def main():
     torch.cuda.init()
     if args.profile_roofline:
         profile_roofline()
+        return
+    if args.profile_mfma:
+        profile_mfma()
         return
     extra = {}
     # ---- headline: batch-1 loop (config 4)
@@ -371,7 +463,17 @@ def main():
             "cross_lang_b8_GBps": round(lang8["GBps"], 1),
             "cross_lang_b1_L517_us": round(lang1["us"], 3),
             "self_b1_us": round(self1["us"], 3),
+            "self_b1_TFLOPs": round(self1["TFLOPs"], 2),
+            "self_b1_mfma_frac": round(self1["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS, 5),
         })
+        for name, M, N, K, int8 in GEMM_SHAPES:
+            r = bench_gemm(M, N, K, att_steps, args.warmup, int8=int8)
+            extra[f"gemm_{name}_us"] = round(r["us"], 3)
+            extra[f"gemm_{name}_TFLOPs"] = round(r["TFLOPs"], 1)
+            extra[f"gemm_{name}_mfma_frac"] = round(r["mfma_frac"], 4)
+            if M <= 160:   # weight streaming: the HBM rate is the bound that matters
+                extra[f"gemm_{name}_GBps"] = round(r["GBps"], 1)
+                extra[f"gemm_{name}_hbm_frac"] = round(r["hbm_frac"], 4)
         for B, int8, key in ((16, False, "loop_b16_ms"), (32, True, "loop_int8_b32_ms")):
             m, enc = make_model(B, int8=int8)
             extra[key] = round(bench_loop(m, max(3, args.steps // 10), 2), 3)
