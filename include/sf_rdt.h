@@ -131,6 +131,23 @@ int sf_rdt_denoise_step(sf_rdt* m, const float* x_t, float t, float* velocity, v
  * replays it afterwards (inputs are copied in and out around the graph). */
 int sf_rdt_sample(sf_rdt* m, float* x, int32_t use_graph, void* stream);
 
+/* InferenceEngine::infer (src/engine/inference_engine.cpp:99-175) on this
+ * runtime: (1) sf_rdt_encode_condition on the raw tokens when frame_id
+ * differs from the frame of the cached condition, or when none is cached
+ * (first call, or a condition set with sf_rdt_set_condition /
+ * sf_rdt_encode_condition, or weights changed since) -- the reference's
+ * mark_new_frame / frame-id test (:106-128); otherwise the token pointers
+ * are not read; (2) x_T [B, T, A] ~ N(0,1) from noise_seed, element i from
+ * (noise_seed, i) as sf_init_normal, or zeros for noise_seed == 0 (the
+ * reference's placeholder, :133-136); (3) the Euler loop as one hipGraph
+ * replay (sf_rdt_sample); (4) the action chunk, fp32 [B, T, A], copied to
+ * the HOST buffer action_out, and the stream synchronised before returning
+ * (decode_action is the identity for RDT-1B, rdt1b.h:35-37).  *encoded
+ * (optional) is set to 1 when the condition was encoded by this call. */
+int sf_rdt_infer(sf_rdt* m, uint64_t frame_id, const void* lang_tokens, const int32_t* lang_len,
+                 const void* img_tokens, const void* state, uint64_t noise_seed,
+                 float* action_out, int32_t* encoded, void* stream);
+
 /* Cross-attention K or V cache of block `layer` ([B, H, S, 64] bf16). */
 void* sf_rdt_cache_ptr(sf_rdt* m, int32_t layer, int32_t which_v);
 

@@ -118,11 +118,21 @@ struct sf_rdt {
     hipGraphExec_t graph_exec = nullptr;
     hipStream_t graph_stream = nullptr;
 
+    // sf_rdt_infer's condition cache: the frame id the cached condition was
+    // encoded for, valid until another condition or new weights replace it
+    float* x_infer = nullptr;      // [B*T*A] initial noise, then the action chunk
+    bool infer_cond_valid = false;
+    uint64_t infer_cond_frame = 0;
+
     std::string last_error;
 };
 
 void sf_rdt_set_error(sf_rdt* m, const std::string& msg) {
     if (m) m->last_error = msg;
+}
+
+void sf_rdt_weights_changed(sf_rdt* m) {
+    if (m) m->infer_cond_valid = false;
 }
 
 extern "C" const char* sf_rdt_last_error(const sf_rdt* m) { return m ? m->last_error.c_str() : ""; }
@@ -542,6 +552,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
         {(void**)&m->state_tok, (size_t)(B * D * 2)},
         {(void**)&m->vel_rows, (size_t)(B * S * A * 4)},
         {(void**)&m->x_state, (size_t)(B * T * A * 4)},
+        {(void**)&m->x_infer, (size_t)(B * T * A * 4)},
         {(void**)&m->lang_len, (size_t)(B * 4)},
         {(void**)&m->lang_c, (size_t)(B * c.lang_max * D * 2)},
         {(void**)&m->img_c, (size_t)(B * c.img_len * D * 2)},
@@ -635,6 +646,7 @@ extern "C" int sf_rdt_init_random(sf_rdt* m, uint64_t seed, float std, void* str
         }
     }
     release_graph(m);   // weights changed: a captured graph stays valid, but be explicit
+    m->infer_cond_valid = false;
     return SF_OK;
 }
 
@@ -677,6 +689,7 @@ extern "C" void* sf_rdt_cache_ptr(sf_rdt* m, int32_t layer, int32_t which_v) {
 extern "C" int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t* lang_len,
                                     const void* img_c, const void* state_tok, void* stream) {
     if (!m || !lang_c || !lang_len || !img_c || !state_tok) return SF_EINVAL;
+    m->infer_cond_valid = false;   // sf_rdt_infer re-encodes after a condition set here
     const sf_rdt_config& c = m->cfg;
     hipStream_t s = pick_stream(m, stream);
     const int D = c.hidden, B = c.batch;
@@ -787,5 +800,34 @@ extern "C" int sf_rdt_sample(sf_rdt* m, float* x, int32_t use_graph, void* strea
         SF_TRY(sample_body(m, s));
     }
     SF_HIP(hipMemcpyAsync(x, m->x_state, nbytes, hipMemcpyDeviceToDevice, s));
+    return SF_OK;
+}
+
+// InferenceEngine::infer (src/engine/inference_engine.cpp:99-175): encode
+// the condition when the frame changed (or nothing valid is cached), x_T,
+// the Euler loop as one graph replay, the action chunk to the host, and a
+// stream synchronisation before returning.  decode_action is the identity
+// for RDT-1B (include/servoflow/models/rdt1b/rdt1b.h:35-37).
+extern "C" int sf_rdt_infer(sf_rdt* m, uint64_t frame_id, const void* lang_tokens, const int32_t* lang_len,
+                            const void* img_tokens, const void* state, uint64_t noise_seed,
+                            float* action_out, int32_t* encoded, void* stream) {
+    if (!m || !action_out) return SF_EINVAL;
+    const sf_rdt_config& c = m->cfg;
+    hipStream_t s = pick_stream(m, stream);
+    const bool need_encode = !m->infer_cond_valid || m->infer_cond_frame != frame_id;
+    if (need_encode) {
+        SF_TRY(sf_rdt_encode_condition(m, lang_tokens, lang_len, img_tokens, state, stream));
+        m->infer_cond_valid = true;
+        m->infer_cond_frame = frame_id;
+    }
+    if (encoded) *encoded = need_encode ? 1 : 0;
+    const int64_t n = (int64_t)c.batch * c.horizon * c.action_dim;
+    // x_T ~ N(0, 1), element i from (noise_seed, i); seed 0 keeps the
+    // reference's zero placeholder (inference_engine.cpp:133-136)
+    if (noise_seed != 0) SF_TRY(sf_init_normal(m->x_infer, SF_F32, n, noise_seed, 1.f, s));
+    else SF_TRY(sf_fill_f32(m->x_infer, n, 0.f, s));
+    SF_TRY(sf_rdt_sample(m, m->x_infer, 1, s));
+    SF_HIP(hipMemcpyAsync(action_out, m->x_infer, (size_t)n * 4, hipMemcpyDeviceToHost, s));
+    SF_HIP(hipStreamSynchronize(s));
     return SF_OK;
 }

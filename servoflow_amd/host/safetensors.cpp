@@ -378,6 +378,7 @@ extern "C" int sf_rdt_load_safetensors(sf_rdt* m, const char* path, int32_t flag
     std::vector<char> seen(np, 0);
     std::vector<float> vals;
     int32_t n = 0;
+    sf_rdt_weights_changed(m);   // parameters are overwritten from here on
     for (const StTensor& t : ts) {
         const std::string key = remap_key(t.name);
         if (key.empty()) continue;

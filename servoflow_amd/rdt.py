@@ -67,6 +67,8 @@ def lib():
     L.sf_rdt_denoise_step.argtypes = [vp, vp, ctypes.c_float, vp, vp]
     L.sf_rdt_sample.argtypes = [vp, vp, i32, vp]
     L.sf_rdt_run_blocks.argtypes = [vp, vp, i32, i32, vp]
+    L.sf_rdt_infer.argtypes = [vp, ctypes.c_uint64, vp, vp, vp, vp, ctypes.c_uint64, vp,
+                               ctypes.POINTER(i32), vp]
     L.sf_safetensors_inspect.argtypes = [ctypes.c_char_p, ctypes.POINTER(StEntry), i32, ctypes.POINTER(i32)]
     L.sf_rdt_load_safetensors.argtypes = [vp, ctypes.c_char_p, i32, ctypes.POINTER(i32)]
     L.sf_rdt_last_error.argtypes = [vp]
@@ -210,6 +212,19 @@ class RdtModel:
         abi.check(lib().sf_rdt_denoise_step(self.h, x_t.data_ptr(), float(t), out.data_ptr(),
                                             self._stream()), "sf_rdt_denoise_step")
         return out
+
+    def infer(self, frame_id, lang_tokens, lang_len, img_tokens, state, noise_seed=0):
+        """sf_rdt_infer: returns (action chunk [B, T, A] as a host fp32 numpy
+        array, whether this call encoded the condition)."""
+        import numpy as np
+
+        c = self.cfg
+        out = np.empty((c.batch, c.horizon, c.action_dim), np.float32)
+        enc = ctypes.c_int32(-1)
+        abi.check(lib().sf_rdt_infer(self.h, int(frame_id), lang_tokens.data_ptr(), lang_len.data_ptr(),
+                                     img_tokens.data_ptr(), state.data_ptr(), int(noise_seed),
+                                     out.ctypes.data, ctypes.byref(enc), self._stream()), "sf_rdt_infer")
+        return out, bool(enc.value)
 
     def sample(self, x, use_graph=True):
         abi.check(lib().sf_rdt_sample(self.h, x.data_ptr(), 1 if use_graph else 0, self._stream()),

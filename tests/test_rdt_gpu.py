@@ -20,6 +20,8 @@ Tolerances:
 Full hidden width (2048, 32 heads), reduced depth and condition lengths so
 the oracle finishes in seconds; the full 28-layer shape is covered by
 invariants (graph replay == eager, finite, moves the state)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -254,6 +256,59 @@ def test_encode_condition_runs_adaptors():
     ref, floor = oracle_noise_floor(
         lambda: OR.denoise_step(p, x_t, 0.2, state_tok, caches, np.array([70], np.int32), oc, rb=True))
     assert_within_floor(v, ref, floor, "encode_condition + step")
+
+
+def test_infer_frame_cache_noise_and_host_output():
+    """sf_rdt_infer (InferenceEngine::infer, inference_engine.cpp:99-175):
+    the condition is encoded on the first call and whenever the frame id
+    changes, reused otherwise (the tokens passed are then not read: the frame
+    id decides, as mark_new_frame does); set_condition invalidates the cache;
+    x_T comes from the noise seed (sf_init_normal, zeros for seed 0, the
+    reference's placeholder); the host result equals encode_condition +
+    sample on the same x_T bit for bit (sample is tested against the oracle
+    in test_sample_graph_equals_eager_and_oracle)."""
+    c = small_cfg(batch=2)
+    m = build(c)
+
+    def tokens(seed):
+        lt = bf(O.randn(seed, (c.batch, c.lang_max, c.lang_token_dim)))
+        it = bf(O.randn(seed + 1, (c.batch, c.img_len, c.img_token_dim)))
+        st = bf(O.randn(seed + 2, (c.batch, c.state_dim)))
+        ll = torch.tensor([40, c.lang_max], dtype=torch.int32, device=DEV)
+        return lt, ll, it, st
+
+    A, Bt = tokens(31), tokens(41)
+    a1, e1 = m.infer(7, *A, noise_seed=11)
+    assert e1 and a1.shape == (c.batch, c.horizon, c.action_dim) and np.isfinite(a1).all()
+    a2, e2 = m.infer(7, *Bt, noise_seed=11)          # same frame: cached condition
+    assert not e2 and np.array_equal(a1, a2)
+    a3, e3 = m.infer(8, *Bt, noise_seed=11)          # new frame: re-encoded
+    assert e3 and not np.array_equal(a1, a3)
+    a4, e4 = m.infer(7, *A, noise_seed=11)
+    assert e4 and np.array_equal(a1, a4)
+    a5, e5 = m.infer(7, *A, noise_seed=12)           # other noise, cached condition
+    assert not e5 and not np.array_equal(a1, a5)
+
+    # the same composition by hand: encode, x_T from the seed, graph loop
+    n = c.batch * c.horizon * c.action_dim
+    m.encode_condition(*A)
+    x = torch.empty(c.batch, c.horizon, c.action_dim, device=DEV)
+    R.lib().sf_init_normal.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64,
+                                       ctypes.c_float, ctypes.c_void_p]
+    abi.check(R.lib().sf_init_normal(x.data_ptr(), abi.SF_F32, n, 11, 1.0,
+                                     torch.cuda.current_stream().cuda_stream), "sf_init_normal")
+    torch.cuda.synchronize()
+    assert abs(float(x.std()) - 1.0) < 0.1
+    m.sample(x, use_graph=True)
+    assert np.array_equal(x.cpu().numpy(), a1)
+    # set_condition replaced the condition, so infer encodes again
+    a6, e6 = m.infer(7, *A, noise_seed=11)
+    assert e6 and np.array_equal(a6, a1)
+    # seed 0: x_T = 0 (the reference's placeholder)
+    z = torch.zeros(c.batch, c.horizon, c.action_dim, device=DEV)
+    m.sample(z, use_graph=True)
+    a7, e7 = m.infer(7, *A, noise_seed=0)
+    assert not e7 and np.array_equal(a7, z.cpu().numpy())
 
 
 def test_full_rdt1b_shape_graph_loop():
