@@ -93,9 +93,19 @@ def time_graph(fn, steps, warmup, reps=20):
     return start.elapsed_time(stop) / (steps * reps)
 
 
-def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=False):
+# Working set of the graph-timed attention ops: K and V are cycled through
+# enough distinct copies that one graph's calls touch at least this many
+# bytes, twice the 256 MB memory-side cache (MALL), so every call streams its
+# K/V from HBM as the denoise loop does (each layer's cache is read once per
+# step, ~0.6 GB per step at batch 1).  Re-reading one K/V set call after call
+# would serve part of it from the MALL instead.
+COLD_SET_BYTES = 512 << 20
+
+
+def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=False, reps=20):
     """Graph-timed cross-attention op (exact_pv: the bf16 (hi, lo) P.V form
-    instead of the default fp16 one)."""
+    instead of the default fp16 one): `reps` calls per graph, call i reading
+    K/V copy i % n_sets (COLD_SET_BYTES)."""
     import numpy as np
     import torch
 
@@ -104,32 +114,46 @@ def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=Fals
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(1234 + B + Sk)
+    kv_bytes = 2 * B * H * Sk * 64 * 2
+    n_sets = int(min(reps, max(1, -(-COLD_SET_BYTES // kv_bytes))))
     q = torch.randn(B, H, Sq, 64, device=dev, generator=g).to(torch.bfloat16)
-    k = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
-    v = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    ks = [torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16) for _ in range(n_sets)]
+    vs = [torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16) for _ in range(n_sets)]
     # output straight into [B, Sq, H*D], the layout the block's projection reads
     out = torch.empty(B, Sq, H, 64, device=dev, dtype=torch.bfloat16).permute(0, 2, 1, 3)
     vl = None
     if valid is not None:
         vl = torch.from_numpy(np.asarray(valid, np.int32)).to(dev)
-    desc = make_desc(q, k, v, out, valid_len=vl)
+    desc = make_desc(q, ks[0], vs[0], out, valid_len=vl)
     ws = torch.zeros(max(workspace_bytes(desc), 16), dtype=torch.uint8, device=dev)
-    fn = lambda: attention(q, k, v, out=out, valid_len=vl, workspace=ws, exact_pv=exact_pv)  # noqa: E731
-    ms = time_graph(fn, steps, warmup)
+    calls = [0]
+
+    def fn():
+        i = calls[0] % n_sets
+        calls[0] += 1
+        attention(q, ks[i], vs[i], out=out, valid_len=vl, workspace=ws, exact_pv=exact_pv)
+
+    ms = time_graph(fn, steps, warmup, reps=reps)
     sk_total = B * Sk if valid is None else int(np.sum(valid))
     nbytes = attn_bytes(B, H, Sq, sk_total)
-    return {"us": ms * 1e3, "bytes": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9,
-            "TFLOPs": attn_flops(H, Sq, sk_total) / (ms * 1e-3) / 1e12,
-            "frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    res = {"us": ms * 1e3, "bytes": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9,
+           "TFLOPs": attn_flops(H, Sq, sk_total) / (ms * 1e-3) / 1e12,
+           "frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "kv_sets": n_sets}
+    del ks, vs
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
     """Graph-timed block projection C[M,N] = A[M,K] W[N,K]^T + bias through
     sf_gemm with a caller workspace (split-K kernel + reduce for M <= 160,
     hipBLASLt product + reduce above; the shape is prepared first, as the
-    model runtime does).  epilogue: "plain" (bf16 out) or "addnorm" (fp32
-    residual += product, then RMSNorm to bf16).  Returns time, MFMA rate
-    against the dense bf16 peak and the weight-streaming HBM rate."""
+    model runtime does).  The graph's calls cycle through distinct weight
+    copies totalling >= COLD_SET_BYTES (at most 64 calls), so weights stream
+    from HBM as in the loop, where each is read once per step.  epilogue:
+    "plain" (bf16 out) or "addnorm" (fp32 residual += product, then RMSNorm
+    to bf16).  Returns time, MFMA rate against the dense bf16 peak and the
+    weight-streaming HBM rate."""
     import ctypes
 
     import torch
@@ -139,15 +163,18 @@ def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(M + N + K)
+    wbytes = N * K * (1 if int8 else 2)
+    n_sets = int(min(64, max(1, -(-COLD_SET_BYTES // wbytes))))
     a = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
     if int8:
-        w = torch.randint(-127, 128, (N, K), device=dev, generator=g, dtype=torch.int32).to(torch.int8)
-        ws = torch.rand(N, device=dev, generator=g) * 1e-3
+        ws_ = [torch.randint(-127, 128, (N, K), device=dev, generator=g, dtype=torch.int32).to(torch.int8)
+               for _ in range(n_sets)]
+        scale = torch.rand(N, device=dev, generator=g) * 1e-3
     else:
-        w = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
-        ws = None
+        ws_ = [(torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16) for _ in range(n_sets)]
+        scale = None
     bias = torch.randn(N, device=dev, generator=g) * 0.02
-    d = kernels._desc(a, w, bias, abi.SF_ACT_NONE, ws)
+    d = kernels._desc(a, ws_[0], bias, abi.SF_ACT_NONE, scale)
     wsp = torch.empty(max(int(abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d))), 16),
                       dtype=torch.uint8, device=dev)
     if epilogue == "addnorm":
@@ -165,17 +192,28 @@ def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
         d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), abi.SF_BF16
     d.workspace, d.workspace_bytes = wsp.data_ptr(), wsp.numel()
     abi.check(abi.lib().sf_gemm_prepare(ctypes.byref(d)), "sf_gemm_prepare")
+    descs = []
+    for w in ws_:
+        di = abi.GemmDesc()
+        ctypes.pointer(di)[0] = d
+        di.W = w.data_ptr()
+        descs.append(di)
+    calls = [0]
 
     def fn():
-        abi.check(abi.lib().sf_gemm(ctypes.byref(d), torch.cuda.current_stream(dev).cuda_stream), "sf_gemm")
+        di = descs[calls[0] % n_sets]
+        calls[0] += 1
+        abi.check(abi.lib().sf_gemm(ctypes.byref(di), torch.cuda.current_stream(dev).cuda_stream), "sf_gemm")
 
-    ms = time_graph(fn, steps, warmup)
+    ms = time_graph(fn, steps, warmup, reps=max(20, n_sets))
+    del ws_
+    torch.cuda.empty_cache()
     flops = 2.0 * M * N * K
-    wbytes = N * K * (1 if int8 else 2)
     nbytes = wbytes + M * K * 2 + M * N * 2
     return {"us": ms * 1e3, "TFLOPs": flops / (ms * 1e-3) / 1e12,
             "mfma_frac": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-            "GBps": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+            "GBps": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "w_sets": n_sets}
 
 
 # Projection shapes of the block (M = batch * 67 tokens): the 2048-wide
