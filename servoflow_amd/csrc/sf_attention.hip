@@ -839,7 +839,8 @@ int query_chunks(const sf_attn_desc* d) { return (d->Sq + 16 * sfk::kQB - 1) / (
 // 20.3 us, 8 21.0, 12 22.1, 16 (two workgroups per CU) 24.8; at B = 2, 4
 // splits 26.5 us against 29.3 for 8: a workgroup alone on its CU contracts
 // its tiles at the CU's full rate, and fewer splits halve the partials the
-// merge pass reads.
+// merge pass reads.  At B = 1 on 1024 keys (8 tiles), 4 splits of 2 tiles
+// took 10.1 us against 10.8 for 8 of one tile.
 constexpr long kNumCUs = 256;
 
 int choose_splits(const sf_attn_desc* d) {
@@ -849,7 +850,9 @@ int choose_splits(const sf_attn_desc* d) {
     if (base >= kNumCUs) return 1;
     const long tiles = ((long)d->Sk + 127) / 128;
     long ns = kNumCUs / base;
-    if (ns > tiles) ns = tiles;
+    // at least two tiles per split: one-tile splits cost their fixed start
+    // and epilogue for one tile's work and double the partials to merge
+    if (ns > (tiles + 1) / 2) ns = (tiles + 1) / 2;
     if (ns < 1) ns = 1;
     const long longest = (tiles + ns - 1) / ns;
     ns = (tiles + longest - 1) / longest;
