@@ -289,6 +289,12 @@ __device__ __forceinline__ void ring_wait() {
     asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 }
 
+// Wait for the K half of the older tile only (issued before its V half, so
+// at most V of that tile and the 8 loads of the next tile are outstanding).
+__device__ __forceinline__ void ring_wait_k() {
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+}
+
 template <bool kExactPV>   // false: P.V in fp16 (V exact below 2^16); true: bf16 V, P as (hi, lo)
 __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     constexpr int QR = 16 * kQB;
@@ -445,17 +451,20 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     auto tile = [&](const int t, auto soff) {
         constexpr int SOFF = decltype(soff)::value;
         const int kt = kbeg + t * kKT;
-        ring_wait();   // tile t has landed; tile t + 1 may still stream in
+        // Tile t's K has landed (tile t's V and tile t + 1 may still stream
+        // in); with a key-padding mask the mask words of tile t sit behind
+        // its V in the load queue, so the whole tile is waited for.
+        if (a.kv_mask) ring_wait();
+        else ring_wait_k();
         if (kt + wkey < kend && !(a.causal && kt + wkey > q0 + QR - 1)) {
-            // K fragments, then V^T: K is waited for before the S contraction,
-            // V^T only before P.V, so the transpose reads overlap S.
+            // K fragments for the S contraction; V is waited for and read
+            // (V^T) only after S and the softmax statistics, so its DMA
+            // overlaps them and its transpose reads overlap the weights.
             u32x4 kw[4];
             lds_read_b128_x4<SOFF>(kw, ka);
-            u32x2v vt[8];
-            lds_read_tr16_x8<SOFF>(vt, va);
             // K landed (LDS reads return in order; no scalar loads are in
-            // flight in the loop, so the count is exact); V^T may not have
-            asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(kw[0]), "+v"(kw[1]), "+v"(kw[2]), "+v"(kw[3]) :: "memory");
+            // flight in the loop, so the count is exact)
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kw[0]), "+v"(kw[1]), "+v"(kw[2]), "+v"(kw[3]) :: "memory");
             bf16x8 kf[2][2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -517,47 +526,24 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                     for (int db = 0; db < 4; ++db) acc[qb][db] *= alpha;
                 }
             }
-            // V^T fragments: bf16 as read (exact form), or converted to fp16
-            // with rounding to nearest, which is exact for |v| < 2^16 (bf16's
-            // 8 significant bits fit fp16's 11) and gives +-inf above: an
-            // out-of-range (or infinite or NaN) v makes the output columns it
-            // reaches inf or NaN, never a saturated value.
-            bf16x8 vf[4];
-            f16x8 vh[4];
-            {
-                // V^T landed
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vt[0]), "+v"(vt[1]), "+v"(vt[2]), "+v"(vt[3]),
-                             "+v"(vt[4]), "+v"(vt[5]), "+v"(vt[6]), "+v"(vt[7]) :: "memory");
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const u32x4 vw = {vt[2 * db][0], vt[2 * db][1], vt[2 * db + 1][0], vt[2 * db + 1][1]};
-                    if constexpr (kExactPV) {
-                        vf[db] = u32x4_as_bf16x8(vw);
-                    } else {
-                        u32x4 hw;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float lo = __uint_as_float(vw[e] << 16);
-                            const float hi = __uint_as_float(vw[e] & 0xffff0000u);
-                            hw[e] = pack_f16x2_rn(lo, hi);
-                        }
-                        vh[db] = u32x4_as_f16x8(hw);
-                    }
-                }
-            }
+            // Tile t's V has landed; the transpose reads go out now and are
+            // waited for after the weights of every row block are formed.
+            ring_wait();
+            u32x2v vt[8];
+            lds_read_tr16_x8<SOFF>(vt, va);
+            // Weights: P rounded to the nearest fp16 (P <= 2^8 by the lazy
+            // rescale; l sums the same rounded weights), or a bf16 (hi, lo)
+            // pair in the exact form.
+            f16x8 p8[kQB];
+            bf16x8 ph8[kQB], pl8[kQB];
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb) {
                 if constexpr (!kExactPV) {
-                    // P rounded to the nearest fp16 (P <= 2^8 by the lazy
-                    // rescale); l sums the same rounded weights.
                     float pf[8];
 #pragma unroll
                     for (int j = 0; j < 8; ++j) pf[j] = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nm[qb]));
-                    const f16x8 p8 = u32x4_as_f16x8(u32x4{pack_f16x2_rn(pf[0], pf[1]), pack_f16x2_rn(pf[2], pf[3]),
-                                                          pack_f16x2_rn(pf[4], pf[5]), pack_f16x2_rn(pf[6], pf[7])});
-#pragma unroll
-                    for (int db = 0; db < 4; ++db) acc[qb][db] = mfma16x16x32_f16(vh[db], p8, acc[qb][db]);
-                    accl[qb] = mfma16x16x32_f16(ones_f16, p8, accl[qb]);
+                    p8[qb] = u32x4_as_f16x8(u32x4{pack_f16x2_rn(pf[0], pf[1]), pack_f16x2_rn(pf[2], pf[3]),
+                                                  pack_f16x2_rn(pf[4], pf[5]), pack_f16x2_rn(pf[6], pf[7])});
                 } else {
                     const float nmuse = m[qb] == -INFINITY ? 0.f : -m[qb];
                     uint32_t pb[8], lb[8];
@@ -567,23 +553,55 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                         pb[j] = __float_as_uint(p);
                         lb[j] = __float_as_uint(p - __uint_as_float(pb[j] & 0xffff0000u));
                     }
-                    const u32x4 phw = {__builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u),
-                                       __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
-                                       __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u),
-                                       __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)};
-                    const u32x4 plw = {__builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u),
-                                       __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u),
-                                       __builtin_amdgcn_perm(lb[5], lb[4], 0x07060302u),
-                                       __builtin_amdgcn_perm(lb[7], lb[6], 0x07060302u)};
-                    const bf16x8 ph8 = u32x4_as_bf16x8(phw);
-                    const bf16x8 pl8 = u32x4_as_bf16x8(plw);
+                    ph8[qb] = u32x4_as_bf16x8(u32x4{__builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u),
+                                                    __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
+                                                    __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u),
+                                                    __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)});
+                    pl8[qb] = u32x4_as_bf16x8(u32x4{__builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u),
+                                                    __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u),
+                                                    __builtin_amdgcn_perm(lb[5], lb[4], 0x07060302u),
+                                                    __builtin_amdgcn_perm(lb[7], lb[6], 0x07060302u)});
+                }
+            }
+            // V^T fragments: bf16 as read (exact form), or converted to fp16
+            // with rounding to nearest, which is exact for |v| < 2^16 (bf16's
+            // 8 significant bits fit fp16's 11) and gives +-inf above: an
+            // out-of-range (or infinite or NaN) v makes the output columns it
+            // reaches inf or NaN, never a saturated value.
+            bf16x8 vf[4];
+            f16x8 vh[4];
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vt[0]), "+v"(vt[1]), "+v"(vt[2]), "+v"(vt[3]),
+                         "+v"(vt[4]), "+v"(vt[5]), "+v"(vt[6]), "+v"(vt[7]) :: "memory");
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const u32x4 vw = {vt[2 * db][0], vt[2 * db][1], vt[2 * db + 1][0], vt[2 * db + 1][1]};
+                if constexpr (kExactPV) {
+                    vf[db] = u32x4_as_bf16x8(vw);
+                } else {
+                    u32x4 hw;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float lo = __uint_as_float(vw[e] << 16);
+                        const float hi = __uint_as_float(vw[e] & 0xffff0000u);
+                        hw[e] = pack_f16x2_rn(lo, hi);
+                    }
+                    vh[db] = u32x4_as_f16x8(hw);
+                }
+            }
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+                if constexpr (!kExactPV) {
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) acc[qb][db] = mfma16x16x32_f16(vh[db], p8[qb], acc[qb][db]);
+                    accl[qb] = mfma16x16x32_f16(ones_f16, p8[qb], accl[qb]);
+                } else {
 #pragma unroll
                     for (int db = 0; db < 4; ++db) {
-                        acc[qb][db] = mfma16x16x32(vf[db], ph8, acc[qb][db]);
-                        acc[qb][db] = mfma16x16x32(vf[db], pl8, acc[qb][db]);
+                        acc[qb][db] = mfma16x16x32(vf[db], ph8[qb], acc[qb][db]);
+                        acc[qb][db] = mfma16x16x32(vf[db], pl8[qb], acc[qb][db]);
                     }
-                    accl[qb] = mfma16x16x32(ones, ph8, accl[qb]);
-                    accl[qb] = mfma16x16x32(ones, pl8, accl[qb]);
+                    accl[qb] = mfma16x16x32(ones, ph8[qb], accl[qb]);
+                    accl[qb] = mfma16x16x32(ones, pl8[qb], accl[qb]);
                 }
             }
         }   // live keys
