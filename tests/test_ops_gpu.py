@@ -252,6 +252,21 @@ def test_gemm_library_path(M, N, Kd, w8):
     close(got, ref, f"library gemm {M}x{N}x{Kd} w8={w8}")
 
 
+@pytest.mark.parametrize("pad", [0, 8])
+def test_gemm_library_int8_row_stride(pad):
+    """Library path with int8 weights in a padded row stride (ldw = K + 8):
+    the codes are widened row by row from the strided rows, exactly."""
+    M, N, Kd = 200, 256, 512
+    a = rounded(91, (M, Kd))
+    q, s = O.quantize_int8_rows(O.randn(92, (N, Kd), 0.02))
+    qpad = np.zeros((N, Kd + pad), np.int8)
+    qpad[:, :Kd] = q
+    wdev = dev(qpad, torch.int8)[:, :Kd]
+    assert wdev.stride(0) == Kd + pad
+    got = host(K.gemm(dev(a), wdev, None, out_dtype=torch.float32, w_scale=dev(s, torch.float32)))
+    close(got, O.linear(a, O.dequant_int8(q, s), None), f"library int8 gemm, row stride {Kd + pad}")
+
+
 def test_gemm_library_heads_and_add_norm():
     """The condition K/V projection shape (rows B*4374, K|V heads, k_norm) and
     a batch-16 residual add + RMSNorm through the library path."""
