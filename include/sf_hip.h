@@ -79,8 +79,10 @@ typedef enum sf_dtype {
  * (at most 64).
  * exact_pv: 0 (default) runs the key-split kernel's (Sk > 128) P.V
  * contraction in fp16: V converted with rounding to nearest, exact for
- * |v| < 2^16 (bf16's 8 significant bits fit fp16's 11), and P rounded to
- * the nearest fp16, ~2e-4 mean relative error on the output.  A V element
+ * 2^-14 <= |v| < 2^16 (bf16's 8 significant bits fit fp16's 11; smaller
+ * magnitudes round to fp16's subnormal grid, an absolute error of at most
+ * 2^-25), and P rounded to the nearest fp16, ~2e-4 mean relative error on
+ * the output.  A V element
  * with |v| >= 2^16 converts to +-inf, so the output column (head dim) it
  * belongs to becomes inf or NaN in every row that attends to its key, never
  * a saturated value; the other columns are unaffected.  A NaN or inf in V

@@ -63,8 +63,9 @@ def attention(q, k, v, out=None, scale=0.0, is_causal=False, valid_len=None, num
     kv_mask: optional device bool [B, Sk] key-padding mask (True = attend);
     its rows must be readable for Sk rounded up to 4 bytes.
     exact_pv: bf16 V and P as a bf16 (hi, lo) pair instead of the fp16 P.V
-    contraction (exact for |V| < 2^16; a larger element makes its output
-    column inf/NaN; see sf_attn_desc)."""
+    contraction (which converts V exactly for 2^-14 <= |V| < 2^16, to within
+    2^-25 below; a larger element makes its output column inf/NaN; see
+    sf_attn_desc)."""
     if out is None:
         od = out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=od, device=q.device)

@@ -23,8 +23,9 @@
 //     accumulator layout (lane = query, 4 consecutive keys per lane) is
 //     directly the B operand P^T, so no shuffle sits between the two
 //     contractions.
-//   * P.V runs in fp16 by default (V converted exactly below 2^16, inf
-//     above, P rounded to the nearest fp16); the exact form carries P as a
+//   * P.V runs in fp16 by default (V converted exactly in fp16's normal
+//     range, to within 2^-25 below it, inf above 2^16; P rounded to the
+//     nearest fp16); the exact form carries P as a
 //     bf16 (hi, lo) pair against bf16 V (~16 mantissa bits of P: a single
 //     bf16 P costs ~1.1e-3 mean relative error on its own, the whole 1e-3
 //     budget).
@@ -295,7 +296,7 @@ __device__ __forceinline__ void ring_wait_k() {
     asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
 }
 
-template <bool kExactPV>   // false: P.V in fp16 (V exact below 2^16); true: bf16 V, P as (hi, lo)
+template <bool kExactPV>   // false: P.V in fp16 (V exact for 2^-14 <= |v| < 2^16); true: bf16 V, P as (hi, lo)
 __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     constexpr int QR = 16 * kQB;
     __shared__ __attribute__((aligned(16))) char ring[kRingStages * kStageBytes];
@@ -564,8 +565,9 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                 }
             }
             // V^T fragments: bf16 as read (exact form), or converted to fp16
-            // with rounding to nearest, which is exact for |v| < 2^16 (bf16's
-            // 8 significant bits fit fp16's 11) and gives +-inf above: an
+            // with rounding to nearest, which is exact for 2^-14 <= |v| < 2^16
+            // (bf16's 8 significant bits fit fp16's 11), within 2^-25 below
+            // (fp16's subnormal grid) and gives +-inf above: an
             // out-of-range (or infinite or NaN) v makes the output columns it
             // reaches inf or NaN, never a saturated value.
             bf16x8 vf[4];

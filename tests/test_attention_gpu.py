@@ -141,8 +141,8 @@ def test_pv_forms_against_oracle(B, Sk, ns, vl):
 
 @pytest.mark.parametrize("ns", [0, 1, 4])
 def test_v_beyond_fp16_range(ns):
-    """fp16 form: V is converted to fp16 with rounding to nearest, exact below
-    2^16 and +-inf above, so a V element with |v| >= 2^16 (or an inf or NaN)
+    """fp16 form: V is converted to fp16 with rounding to nearest, exact in
+    fp16's normal range and +-inf above 2^16, so a V element with |v| >= 2^16 (or an inf or NaN)
     makes its head-dim column non-finite (inf or NaN) in every output row,
     through the splits and their merge, and leaves every other column
     bit-identical to the run without it (the P.V contraction is column-wise).
@@ -362,3 +362,41 @@ def test_key_padding_mask(Sk):
     for b in range(B):
         m2[b, vl[b]:] = False
     assert_close_bf16(got2, _masked_reference(q, k, v, m2), f"key mask & valid Sk={Sk}")
+
+
+@pytest.mark.parametrize("exact_pv", [False, True])
+def test_full_size_b8_image_properties(exact_pv):
+    """The BASELINE batch-8 image shape (8x32x67x4374), checked through
+    properties that hold at any size: doubling V doubles the fp32 output bit
+    for bit (the fp16 conversion of V -- exact in fp16's normal range, so V
+    is kept at |v| >= 2^-13 here --, the bf16 (hi, lo) form and the fp32
+    accumulations all scale exactly by 2), and a V whose rows are all one
+    vector returns that vector in every query row (the weights sum to the
+    row sum they are divided by)."""
+    B, H, Sq, Sk = 8, 32, 67, 4374
+    dev = torch.device(DEV)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4374)
+    q = torch.randn(B, H, Sq, 64, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, Sk, 64, device=dev, generator=g)
+    v = (torch.sign(v) * v.abs().clamp(min=2.0 ** -13)).to(torch.bfloat16)
+    o1 = attention(q, k, v, out_dtype=torch.float32, exact_pv=exact_pv)
+    o2 = attention(q, k, (2 * v.float()).to(torch.bfloat16), out_dtype=torch.float32, exact_pv=exact_pv)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o1).all()
+    assert torch.equal(o2, 2 * o1)
+    row = torch.randn(B, H, 1, 64, device=dev, generator=g).to(torch.bfloat16)
+    oc = attention(q, k, row.expand(B, H, Sk, 64).contiguous(), out_dtype=torch.float32, exact_pv=exact_pv)
+    torch.cuda.synchronize()
+    ref = row.float().expand(B, H, Sq, 64)
+    assert float((oc - ref).abs().max()) <= 1e-5 * float(ref.abs().max())
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk", [(1, 2, 100, 65536), (1, 1, 1000, 2048)])
+def test_long_keys_and_many_query_chunks(B, H, Sq, Sk):
+    """65536 keys (512 tiles, 64 splits' worth: the split cap) and 1000
+    queries (13 query chunks of 80 rows) against the oracle."""
+    q, k, v = rounded(191, (B, H, Sq, 64)), rounded(192, (B, H, Sk, 64)), rounded(193, (B, H, Sk, 64))
+    got = run(q, k, v)
+    assert_close_bf16(got, O.attention_f32(q, k, v), f"long {B},{H},{Sq},{Sk}")
