@@ -110,6 +110,15 @@ def mlp_adaptor(p, name, x, depth, rb=True):
     return O.linear(h, p[f"{name}.{2 * (depth - 1)}.weight"], p[f"{name}.{2 * (depth - 1)}.bias"])
 
 
+def state_token(p, state, cfg, rb=True):
+    """The condition's state token of RDT1BModel::encode_condition
+    (rdt1b.cpp:202-229): state_adaptor(cat(state, zeros)), [B, D].  (The
+    reference's Python model feeds an all-ones mask instead,
+    test_rdt1b_alignment.py:204-208; the C++ form is the one restated.)"""
+    st_in = np.concatenate([state, np.zeros_like(state)], axis=-1)
+    return mlp_adaptor(p, "state_adaptor", st_in, 3, rb)
+
+
 def condition_tokens(p, lang_c, img_c, cfg, rb=True):
     """lang_c + lang_cond_pos_embed[:L], img_c + img_cond_pos_embed
     (rdt1b.cpp:342-349), rounded where the GPU stores them."""
