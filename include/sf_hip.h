@@ -78,7 +78,7 @@ typedef enum sf_dtype {
  * num_splits: 0 chooses the split-K factor automatically; n > 0 forces n
  * (at most 64).
  * exact_pv: 0 (default) runs the key-split kernel's (Sk > 128) P.V
- * contraction in fp16: V converted with rounding to nearest, exact for
+ * contraction in fp16: a bf16 V converted with rounding to nearest, exact for
  * 2^-14 <= |v| < 2^16 (bf16's 8 significant bits fit fp16's 11; smaller
  * magnitudes round to fp16's subnormal grid, an absolute error of at most
  * 2^-25), and P rounded to the nearest fp16, ~2e-4 mean relative error on
@@ -90,8 +90,16 @@ typedef enum sf_dtype {
  * (~1e-5) for any finite V, at ~15% more time per key tile.
  * scale must be >= 0 (SF_ENOTSUP otherwise).
  *
- * Supported: in_dtype SF_BF16, out_dtype SF_BF16 or SF_F32, D == 64,
- * pointers 16-byte aligned, s/h/b strides multiples of 8 elements.
+ * in_dtype: SF_BF16, SF_F16 or SF_F32 for Q, K and V (the reference's
+ * dispatch, attention.cu:183-197: fp16 -- its default compute dtype,
+ * config.h:57 -- to flash attention, fp32 to the naive kernel).  fp16 runs
+ * the same kernels with the fp16 MFMA for S = K.Q^T and V as loaded (exact_pv
+ * then carries P as an fp16 hi/lo pair); fp32 runs a kernel on the fp32 MFMA
+ * (v_mfma_f32_16x16x4_f32: nothing rounded below fp32; exact_pv ignored).
+ * out_dtype: SF_BF16, SF_F16 or SF_F32 (rounded to nearest from fp32).
+ *
+ * Supported: D == 64, pointers 16-byte aligned, every stride a non-negative
+ * multiple of 8 elements, s-strides >= D.
  */
 typedef struct sf_attn_desc {
     int32_t B, H, Sq, Sk, D;

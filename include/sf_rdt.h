@@ -67,7 +67,9 @@ int sf_euler_update(float* x, const float* v, int32_t B, int32_t T, int32_t A, i
 /* ---- model runtime (libsf_rdt.so) ---------------------------------------- */
 
 /* RDT1BConfig (include/servoflow/models/rdt1b/config.h:26-71) plus the batch
- * and weight format.  The FFN has no expansion (config.h:60-61). */
+ * and weight format.  The reference's FFN has no expansion (config.h:60-61);
+ * mlp_ratio > 1 builds the D -> mlp_ratio*D -> D variant (BASELINE's
+ * "MLP 4x" block, no reference counterpart). */
 typedef struct sf_rdt_config {
     int32_t hidden;              /* 2048 */
     int32_t layers;              /* 28 */
@@ -86,6 +88,7 @@ typedef struct sf_rdt_config {
     int32_t batch;
     int32_t int8_weights;        /* block projections as int8 + fp32 row scale */
     float eps;                   /* 1e-6 */
+    int32_t mlp_ratio;           /* FFN hidden = mlp_ratio * hidden (1; 0 means 1) */
 } sf_rdt_config;
 
 typedef struct sf_rdt sf_rdt;

@@ -61,19 +61,55 @@ struct AttnArgs {
     int B, H, Sq, Sk;
     int nsplit;
     int nqc;          // query chunks
-    int out_f32;
+    int out_kind;     // OutKind
     int causal;
     float scale_log2;   // scale * log2(e)
 };
 
+enum OutKind { kOutBF16 = 0, kOutF32 = 1, kOutF16 = 2 };
+
 __device__ __forceinline__ void store_out(const AttnArgs& a, int b, int h, int q,
                                           int d, float val) {
     const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + d;
-    if (a.out_f32) {
+    if (a.out_kind == kOutF32) {
         reinterpret_cast<float*>(a.o)[off] = val;
+    } else if (a.out_kind == kOutF16) {
+        reinterpret_cast<_Float16*>(a.o)[off] = (_Float16)val;
     } else {
         reinterpret_cast<uint16_t*>(a.o)[off] = (uint16_t)f32_to_bf16_bits(val);
     }
+}
+
+// Four consecutive head dims of one output row (element offset off, 4-aligned).
+__device__ __forceinline__ void store_out4(const AttnArgs& a, int64_t off, f32x4 o) {
+    if (a.out_kind == kOutF32) {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.o) + off) = o;
+    } else {
+        const uint2 pk = a.out_kind == kOutF16 ? uint2{pack_f16x2_rn(o[0], o[1]), pack_f16x2_rn(o[2], o[3])}
+                                               : uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.o) + off) = pk;
+    }
+}
+
+// 16-bit input element type of the MFMA kernels: bf16 (F16 = false) or fp16.
+template <bool F16> struct In16 { typedef bf16x8 v8; };
+template <> struct In16<true> { typedef f16x8 v8; };
+
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma_in(typename In16<F16>::v8 a, typename In16<F16>::v8 b, f32x4 c) {
+    if constexpr (F16) return mfma16x16x32_f16(a, b, c);
+    else return mfma16x16x32(a, b, c);
+}
+
+// p as an fp16 (hi, lo) pair, two weights per 32-bit word: hi = fp16(p),
+// lo = fp16(p - hi) (~22 significant bits of p for p >= 2^-14).
+__device__ __forceinline__ void split_f16x2(float p0, float p1, uint32_t& hi, uint32_t& lo) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 hv = __builtin_convertvector(f32x2v{p0, p1}, h2);
+    const f32x2v hf = __builtin_convertvector(hv, f32x2v);
+    const h2 lv = __builtin_convertvector(f32x2v{p0 - hf[0], p1 - hf[1]}, h2);
+    hi = __builtin_bit_cast(uint32_t, hv);
+    lo = __builtin_bit_cast(uint32_t, lv);
 }
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane j receives element
@@ -231,13 +267,7 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
         if (q >= a.Sq) continue;
         if (nsplit == 1) {
             o *= L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
-            const int64_t off = b * a.o_sb + h * a.o_sh + q * a.o_ss + d0;
-            if (a.out_f32) {
-                *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.o) + off) = o;
-            } else {
-                const uint2 pk2 = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.o) + off) = pk2;
-            }
+            store_out4(a, b * a.o_sb + h * a.o_sh + q * a.o_ss + d0, o);
         } else {
             *reinterpret_cast<f32x4*>(a.part_o + (pbase + q) * kD + d0) = o;
             if (W == 0 && g == 0)
@@ -296,8 +326,13 @@ __device__ __forceinline__ void ring_wait_k() {
     asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
 }
 
-template <bool kExactPV>   // false: P.V in fp16 (V exact for 2^-14 <= |v| < 2^16); true: bf16 V, P as (hi, lo)
+// kExactPV false: P.V in fp16 with P rounded to fp16 (a bf16 V converted,
+// exact for 2^-14 <= |v| < 2^16; an fp16 V as is).  true: V in its input
+// type and P as a (hi, lo) pair of that type.  kF16: Q/K/V are fp16 (S on
+// the fp16 MFMA) instead of bf16.
+template <bool kExactPV, bool kF16>
 __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
+    using v8 = typename In16<kF16>::v8;
     constexpr int QR = 16 * kQB;
     __shared__ __attribute__((aligned(16))) char ring[kRingStages * kStageBytes];
 
@@ -337,13 +372,13 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                   a.kv_mask ? (uint32_t)((a.Sk + 3) & ~3) : 0u);
 
     // Q fragments (B operand of S^T = K.Q^T): row 16qb + r, dims 32hh + 8g..
-    bf16x8 qf[kQB][2];
+    v8 qf[kQB][2];
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
             qf[qb][hh] = __builtin_bit_cast(
-                bf16x8, buffer_load16(qrs, (uint32_t)(((q0 + 16 * qb + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
+                v8, buffer_load16(qrs, (uint32_t)(((q0 + 16 * qb + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
 
     // DMA of one tile into a stage: wave w, op j fills LDS chunks
     // (4w + j) * 64 + lane = key * 8 + slot of K (and of V), loading global
@@ -466,11 +501,11 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
             // K landed (LDS reads return in order; no scalar loads are in
             // flight in the loop, so the count is exact)
             asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kw[0]), "+v"(kw[1]), "+v"(kw[2]), "+v"(kw[3]) :: "memory");
-            bf16x8 kf[2][2];
+            v8 kf[2][2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) kf[kb][hh] = u32x4_as_bf16x8(kw[2 * kb + hh]);
+                for (int hh = 0; hh < 2; ++hh) kf[kb][hh] = __builtin_bit_cast(v8, kw[2 * kb + hh]);
             const bool need_mask = a.causal || kt + kKT > kend || a.kv_mask;
             const uint32_t mw[2] = {mw_next[0], mw_next[1]};
             f32x4 s[kQB][2];
@@ -479,8 +514,8 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
                     f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                    z = mfma16x16x32(kf[kb][0], qf[qb][0], z);
-                    s[qb][kb] = mfma16x16x32(kf[kb][1], qf[qb][1], z);
+                    z = mfma_in<kF16>(kf[kb][0], qf[qb][0], z);
+                    s[qb][kb] = mfma_in<kF16>(kf[kb][1], qf[qb][1], z);
                 }
             }
             if (need_mask) {
@@ -533,10 +568,11 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
             u32x2v vt[8];
             lds_read_tr16_x8<SOFF>(vt, va);
             // Weights: P rounded to the nearest fp16 (P <= 2^8 by the lazy
-            // rescale; l sums the same rounded weights), or a bf16 (hi, lo)
-            // pair in the exact form.
+            // rescale; l sums the same rounded weights), or a (hi, lo) pair
+            // of the input type in the exact form.
             f16x8 p8[kQB];
             bf16x8 ph8[kQB], pl8[kQB];
+            f16x8 hh8[kQB], hl8[kQB];
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb) {
                 if constexpr (!kExactPV) {
@@ -545,6 +581,16 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                     for (int j = 0; j < 8; ++j) pf[j] = fast_exp2(fmaf(s[qb][j >> 2][j & 3], a.scale_log2, nm[qb]));
                     p8[qb] = u32x4_as_f16x8(u32x4{pack_f16x2_rn(pf[0], pf[1]), pack_f16x2_rn(pf[2], pf[3]),
                                                   pack_f16x2_rn(pf[4], pf[5]), pack_f16x2_rn(pf[6], pf[7])});
+                } else if constexpr (kF16) {
+                    const float nmuse = m[qb] == -INFINITY ? 0.f : -m[qb];
+                    uint32_t hw[4], lw[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        split_f16x2(fast_exp2(fmaf(s[qb][(2 * e) >> 2][(2 * e) & 3], a.scale_log2, nmuse)),
+                                    fast_exp2(fmaf(s[qb][(2 * e + 1) >> 2][(2 * e + 1) & 3], a.scale_log2, nmuse)),
+                                    hw[e], lw[e]);
+                    hh8[qb] = u32x4_as_f16x8(u32x4{hw[0], hw[1], hw[2], hw[3]});
+                    hl8[qb] = u32x4_as_f16x8(u32x4{lw[0], lw[1], lw[2], lw[3]});
                 } else {
                     const float nmuse = m[qb] == -INFINITY ? 0.f : -m[qb];
                     uint32_t pb[8], lb[8];
@@ -577,7 +623,9 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const u32x4 vw = {vt[2 * db][0], vt[2 * db][1], vt[2 * db + 1][0], vt[2 * db + 1][1]};
-                if constexpr (kExactPV) {
+                if constexpr (kF16) {
+                    vh[db] = u32x4_as_f16x8(vw);   // fp16 V as loaded
+                } else if constexpr (kExactPV) {
                     vf[db] = u32x4_as_bf16x8(vw);
                 } else {
                     u32x4 hw;
@@ -596,6 +644,14 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 #pragma unroll
                     for (int db = 0; db < 4; ++db) acc[qb][db] = mfma16x16x32_f16(vh[db], p8[qb], acc[qb][db]);
                     accl[qb] = mfma16x16x32_f16(ones_f16, p8[qb], accl[qb]);
+                } else if constexpr (kF16) {
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) {
+                        acc[qb][db] = mfma16x16x32_f16(vh[db], hh8[qb], acc[qb][db]);
+                        acc[qb][db] = mfma16x16x32_f16(vh[db], hl8[qb], acc[qb][db]);
+                    }
+                    accl[qb] = mfma16x16x32_f16(ones_f16, hh8[qb], accl[qb]);
+                    accl[qb] = mfma16x16x32_f16(ones_f16, hl8[qb], accl[qb]);
                 } else {
 #pragma unroll
                     for (int db = 0; db < 4; ++db) {
@@ -704,8 +760,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
 constexpr int kShortMaxKeys = 128;
 constexpr int kVPitch = 80;   // LDS row pitch of V (bf16): 160 B keeps the four rows of a read apart
 
-template <int KB>   // 16-key blocks covering Sk (even, <= 8)
+template <int KB, bool kF16>   // 16-key blocks covering Sk (even, <= 8); fp16 (else bf16) Q/K/V
 __global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
+    using v8 = typename In16<kF16>::v8;
     constexpr int KROWS = 16 * KB;
     __shared__ __attribute__((aligned(16))) uint16_t vl[KROWS * kVPitch];
     const int lane = threadIdx.x;
@@ -738,19 +795,19 @@ __global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
         const int c = lane + 64 * j;          // 16-byte chunk: key c/8, dims 8(c%8)..
         vv[j] = buffer_load16(vrs, (uint32_t)(((c >> 3) * a.v_ss + (c & 7) * 8) * 2));
     }
-    bf16x8 kf[KB][2];
+    v8 kf[KB][2];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
             kf[kb][hh] = __builtin_bit_cast(
-                bf16x8, buffer_load16(krs, (uint32_t)(((16 * kb + r) * a.k_ss + 32 * hh + 8 * g) * 2)));
+                v8, buffer_load16(krs, (uint32_t)(((16 * kb + r) * a.k_ss + 32 * hh + 8 * g) * 2)));
     }
-    bf16x8 qf[2];
+    v8 qf[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
         qf[hh] = __builtin_bit_cast(
-            bf16x8, buffer_load16(qrs, (uint32_t)(((q0 + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
+            v8, buffer_load16(qrs, (uint32_t)(((q0 + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
 #pragma unroll
     for (int j = 0; j < 2 * KB; ++j) {
         const int c = lane + 64 * j;
@@ -763,8 +820,8 @@ __global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
         f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        z = mfma16x16x32(kf[kb][0], qf[0], z);
-        s[kb] = mfma16x16x32(kf[kb][1], qf[1], z);
+        z = mfma_in<kF16>(kf[kb][0], qf[0], z);
+        s[kb] = mfma_in<kF16>(kf[kb][1], qf[1], z);
     }
     const int qrow = q0 + r;
     uint32_t mw[KB];
@@ -785,38 +842,51 @@ __global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float nm = mx == -INFINITY ? 0.f : -mx * a.scale_log2;
 
-    // P^T as bf16 (hi, lo) pairs, O^T += V^T . P^T per 32-key step
+    // P^T as (hi, lo) pairs of the input type, O^T += V^T . P^T per 32-key step
     f32x4 acc[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     float ls = 0.f;
 #pragma unroll
     for (int j = 0; j < KB / 2; ++j) {
-        uint32_t pb[8], lb[8];
+        float pf[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const float p = fast_exp2(fmaf(s[2 * j + (t >> 2)][t & 3], a.scale_log2, nm));
-            ls += p;
-            pb[t] = __float_as_uint(p);
-            lb[t] = __float_as_uint(p - __uint_as_float(pb[t] & 0xffff0000u));
+            pf[t] = fast_exp2(fmaf(s[2 * j + (t >> 2)][t & 3], a.scale_log2, nm));
+            ls += pf[t];
         }
-        const bf16x8 ph = u32x4_as_bf16x8(u32x4{__builtin_amdgcn_perm(pb[1], pb[0], 0x07060302u),
-                                                __builtin_amdgcn_perm(pb[3], pb[2], 0x07060302u),
-                                                __builtin_amdgcn_perm(pb[5], pb[4], 0x07060302u),
-                                                __builtin_amdgcn_perm(pb[7], pb[6], 0x07060302u)});
-        const bf16x8 pl = u32x4_as_bf16x8(u32x4{__builtin_amdgcn_perm(lb[1], lb[0], 0x07060302u),
-                                                __builtin_amdgcn_perm(lb[3], lb[2], 0x07060302u),
-                                                __builtin_amdgcn_perm(lb[5], lb[4], 0x07060302u),
-                                                __builtin_amdgcn_perm(lb[7], lb[6], 0x07060302u)});
+        uint32_t hw[4], lw[4];
+        if constexpr (kF16) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) split_f16x2(pf[2 * e], pf[2 * e + 1], hw[e], lw[e]);
+        } else {
+            uint32_t pb[8], lb[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                pb[t] = __float_as_uint(pf[t]);
+                lb[t] = __float_as_uint(pf[t] - __uint_as_float(pb[t] & 0xffff0000u));
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hw[e] = __builtin_amdgcn_perm(pb[2 * e + 1], pb[2 * e], 0x07060302u);
+                lw[e] = __builtin_amdgcn_perm(lb[2 * e + 1], lb[2 * e], 0x07060302u);
+            }
+        }
         // keys 32j + 4g + (0..3) and 32j + 16 + 4g + (0..3): the P^T slot order
         const uint16_t* vrow = vl + (32 * j + 4 * g + (r >> 2)) * kVPitch + 4 * (r & 3);
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
             const uint2 lo4 = lds_read_tr16(vrow + 16 * db);
             const uint2 hi4 = lds_read_tr16(vrow + 16 * kVPitch + 16 * db);
-            const bf16x8 vf = u32x4_as_bf16x8(u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
-            acc[db] = mfma16x16x32(vf, ph, acc[db]);
-            acc[db] = mfma16x16x32(vf, pl, acc[db]);
+            const u32x4 vw = {lo4.x, lo4.y, hi4.x, hi4.y};
+            const u32x4 hv = {hw[0], hw[1], hw[2], hw[3]}, lv = {lw[0], lw[1], lw[2], lw[3]};
+            if constexpr (kF16) {
+                acc[db] = mfma16x16x32_f16(u32x4_as_f16x8(vw), u32x4_as_f16x8(hv), acc[db]);
+                acc[db] = mfma16x16x32_f16(u32x4_as_f16x8(vw), u32x4_as_f16x8(lv), acc[db]);
+            } else {
+                acc[db] = mfma16x16x32(u32x4_as_bf16x8(vw), u32x4_as_bf16x8(hv), acc[db]);
+                acc[db] = mfma16x16x32(u32x4_as_bf16x8(vw), u32x4_as_bf16x8(lv), acc[db]);
+            }
         }
     }
     ls += __shfl_xor(ls, 16, 64);
@@ -825,17 +895,133 @@ __global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
     const float inv = ls > 0.f ? 1.f / ls : 0.f;
     // O^T lane layout: head dims 16db + 4g + i of query qrow
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-        const f32x4 o = acc[db] * inv;
-        const int64_t off = b * a.o_sb + h * a.o_sh + qrow * a.o_ss + 16 * db + 4 * g;
-        if (a.out_f32) {
-            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.o) + off) = o;
-        } else {
-            uint2 pk2;
-            pk2.x = pack_bf16x2(o[0], o[1]);
-            pk2.y = pack_bf16x2(o[2], o[3]);
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.o) + off) = pk2;
+    for (int db = 0; db < 4; ++db)
+        store_out4(a, b * a.o_sb + h * a.o_sh + qrow * a.o_ss + 16 * db + 4 * g, acc[db] * inv);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 Q/K/V (the reference sends fp32 to its naive kernel,
+// attention.cu:90-139, 183-197): fp32 products on the fp32 MFMA
+// (v_mfma_f32_16x16x4_f32), so nothing is rounded below fp32.
+//
+// One wave per (b, h, 16-query block, key split), K and V read straight from
+// global memory (L2 serves the five query blocks of a head).  Per 16-key
+// block: S^T = K.Q^T in 16 steps of 4 head dims, where step s takes dims
+// 16g + s from lane group g, so each lane reads 16 contiguous dims of its
+// key row and of its query row; then O^T += V^T.P^T in 4 steps, where step i
+// contracts keys {4g + i}: exactly the keys whose scores the S^T accumulator
+// holds in element i of lane group g, so P^T needs no shuffle, and V element
+// (key 4g + i, dim 16db + r) comes from 16 consecutive floats per lane group.
+// Online softmax in log2 units as in the other kernels; multi-split partials
+// go to the same workspace layout and merge kernel.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mfma16x16x4_f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(64) void attn_f32_kernel(const AttnArgs a) {
+    const int lane = threadIdx.x;
+    const int g = lane >> 4;
+    const int r = lane & 15;
+    const int nsplit = a.nsplit;
+    const int split = blockIdx.x % nsplit;
+    const int q0 = 16 * (int)(blockIdx.x / nsplit);
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
+    const int qrow = q0 + r;
+
+    int valid = a.Sk;
+    if (a.valid_len) {
+        const int vl = a.valid_len[b];
+        valid = vl < 0 ? 0 : (vl > a.Sk ? a.Sk : vl);
+    }
+    int per = (valid + nsplit - 1) / nsplit;
+    per = (per + 15) & ~15;
+    const int kbeg = split * per;
+    int kend = min(valid, kbeg + per);
+    if (a.causal) kend = min(kend, min(a.Sq, q0 + 16));
+
+    const float* qp = reinterpret_cast<const float*>(a.q) + b * a.q_sb + h * a.q_sh;
+    const float* kp = reinterpret_cast<const float*>(a.k) + b * a.k_sb + h * a.k_sh;
+    const float* vp = reinterpret_cast<const float*>(a.v) + b * a.v_sb + h * a.v_sh;
+    // rows outside [0, Sq) and keys outside [0, kend) read as zeros
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qp, (uint32_t)(a.Sq * a.q_ss * 4));
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kp, (uint32_t)(max(kend, 0) * a.k_ss * 4));
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vp, (uint32_t)(max(kend, 0) * a.v_ss * 4));
+    const __amdgpu_buffer_rsrc_t mrs =
+        make_rsrc(a.kv_mask ? static_cast<const void*>(a.kv_mask + b * a.kv_mask_stride) : static_cast<const void*>(a.q),
+                  a.kv_mask ? (uint32_t)((a.Sk + 3) & ~3) : 0u);
+
+    float qv[16];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u32x4 w = buffer_load16(qrs, (uint32_t)((qrow * a.q_ss + 16 * g + 4 * c) * 4));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qv[4 * c + e] = __uint_as_float(w[e]);
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY;   // running row max, log2 units
+    float l = 0.f;         // this lane's share of the row sum
+    for (int kt = kbeg; kt < kend; kt += 16) {
+        float kv[16], vv[16];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4 w = buffer_load16(krs, (uint32_t)(((kt + r) * a.k_ss + 16 * g + 4 * c) * 4));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kv[4 * c + e] = __uint_as_float(w[e]);
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+                vv[4 * i + db] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    vrs, (uint32_t)(((kt + 4 * g + i) * a.v_ss + 16 * db + r) * 4), 0, 0));
+        const uint32_t mw = a.kv_mask ? mask_word(mrs, kt + 4 * g) : 0xffffffffu;
+        f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 16; ++st) sc = mfma16x16x4_f32(kv[st], qv[st], sc);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = kt + 4 * g + i;
+            const bool dead = key >= kend || (a.causal && key > qrow) || ((mw >> (8 * i)) & 0xffu) == 0;
+            sc[i] = dead ? -INFINITY : sc[i] * a.scale_log2;
+            mx = fmaxf(mx, sc[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m, mx);
+        const float muse = mnew == -INFINITY ? 0.f : mnew;
+        const float alpha = fast_exp2(m - muse);
+        m = mnew;
+        l *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float p = fast_exp2(sc[i] - muse);
+            l += p;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] = mfma16x16x4_f32(vv[4 * i + db], p, acc[db]);
+        }
+    }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (qrow >= a.Sq) return;
+    // O^T lane layout: head dims 16db + 4g + i of query qrow
+    if (nsplit == 1) {
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+            store_out4(a, b * a.o_sb + h * a.o_sh + qrow * a.o_ss + 16 * db + 4 * g, acc[db] * inv);
+    } else {
+        const size_t row = (((size_t)b * a.H + h) * nsplit + split) * (size_t)a.Sq + qrow;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+            *reinterpret_cast<f32x4*>(a.part_o + row * kD + 16 * db + 4 * g) = acc[db];
+        if (g == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = float2{m, l};
     }
 }
 
@@ -886,24 +1072,28 @@ int validate(const sf_attn_desc* d) {
     if (!d) return SF_EINVAL;
     if (d->B < 0 || d->H < 0 || d->Sq < 0 || d->Sk < 0) return SF_EINVAL;
     if (d->D != sfk::kD) return SF_ENOTSUP;
-    if (d->in_dtype != SF_BF16) return SF_ENOTSUP;
-    if (d->out_dtype != SF_BF16 && d->out_dtype != SF_F32) return SF_ENOTSUP;
+    if (d->in_dtype != SF_BF16 && d->in_dtype != SF_F16 && d->in_dtype != SF_F32) return SF_ENOTSUP;
+    if (d->out_dtype != SF_BF16 && d->out_dtype != SF_F32 && d->out_dtype != SF_F16) return SF_ENOTSUP;
     if (d->num_splits < 0) return SF_EINVAL;
     if (!(d->scale >= 0.f)) return SF_ENOTSUP;   // negative or NaN scale
+    // Every stride a non-negative multiple of 8 elements (16-byte rows for
+    // the vector loads and stores); rows along s at least D apart (the
+    // kernels address a head's rows through one buffer range of S * s-stride).
     const int64_t* st[4] = {d->q_stride, d->k_stride, d->v_stride, d->o_stride};
-    for (int i = 0; i < 3; ++i)
+    for (int i = 0; i < 4; ++i) {
         for (int j = 0; j < 3; ++j)
             if (st[i][j] < 0 || (st[i][j] & 7)) return SF_EINVAL;
-    for (int j = 0; j < 3; ++j)
-        if (d->o_stride[j] < 0) return SF_EINVAL;
+        if (st[i][2] < d->D) return SF_EINVAL;
+    }
     if (d->Sk == 0 && d->B > 0 && d->H > 0 && d->Sq > 0) return SF_EINVAL;
     if (d->kv_mask && ((reinterpret_cast<uintptr_t>(d->kv_mask) & 3) || (d->kv_mask_stride & 3) ||
                        (d->B > 1 && d->kv_mask_stride < d->Sk)))
         return SF_EINVAL;
     // Per-head byte ranges are addressed with 32-bit buffer offsets.
-    if ((int64_t)d->Sq * d->q_stride[2] * 2 > 0x7fffffffLL ||
-        (int64_t)d->Sk * d->k_stride[2] * 2 > 0x7fffffffLL ||
-        (int64_t)d->Sk * d->v_stride[2] * 2 > 0x7fffffffLL)
+    const int64_t es = d->in_dtype == SF_F32 ? 4 : 2;
+    if ((int64_t)d->Sq * d->q_stride[2] * es > 0x7fffffffLL ||
+        (int64_t)d->Sk * d->k_stride[2] * es > 0x7fffffffLL ||
+        (int64_t)d->Sk * d->v_stride[2] * es > 0x7fffffffLL)
         return SF_ENOTSUP;
     return SF_OK;
 }
@@ -967,7 +1157,7 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     a.B = d->B; a.H = d->H; a.Sq = d->Sq; a.Sk = d->Sk;
     a.nsplit = ns;
     a.nqc = nqc;
-    a.out_f32 = d->out_dtype == SF_F32;
+    a.out_kind = d->out_dtype == SF_F32 ? sfk::kOutF32 : (d->out_dtype == SF_F16 ? sfk::kOutF16 : sfk::kOutBF16);
     a.causal = d->is_causal != 0;
     const float scale = d->scale != 0.f ? d->scale : 1.f / sqrtf((float)d->D);
     a.scale_log2 = scale * 1.4426950408889634f;
@@ -980,19 +1170,36 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     if ((long)ns * nqc > 0x7fffffffL) return SF_ENOTSUP;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (short_keys) {
+    const bool f16 = d->in_dtype == SF_F16;
+    if (d->in_dtype == SF_F32) {
+        const long qblocks = (d->Sq + 15) / 16;
+        if ((long)ns * qblocks > 0x7fffffffL) return SF_ENOTSUP;
+        hipLaunchKernelGGL(sfk::attn_f32_kernel, dim3((unsigned)(ns * qblocks), d->H, d->B), dim3(64), 0, s, a);
+    } else if (short_keys) {
         const dim3 grid((d->Sq + 15) / 16, d->H, d->B);
         const int kb = ((d->Sk + 31) / 32) * 2;
-        if (kb <= 2) hipLaunchKernelGGL(sfk::attn_short_kernel<2>, grid, dim3(64), 0, s, a);
-        else if (kb <= 4) hipLaunchKernelGGL(sfk::attn_short_kernel<4>, grid, dim3(64), 0, s, a);
-        else if (kb <= 6) hipLaunchKernelGGL(sfk::attn_short_kernel<6>, grid, dim3(64), 0, s, a);
-        else hipLaunchKernelGGL(sfk::attn_short_kernel<8>, grid, dim3(64), 0, s, a);
+        if (f16) {
+            if (kb <= 2) hipLaunchKernelGGL((sfk::attn_short_kernel<2, true>), grid, dim3(64), 0, s, a);
+            else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, true>), grid, dim3(64), 0, s, a);
+            else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, true>), grid, dim3(64), 0, s, a);
+            else hipLaunchKernelGGL((sfk::attn_short_kernel<8, true>), grid, dim3(64), 0, s, a);
+        } else {
+            if (kb <= 2) hipLaunchKernelGGL((sfk::attn_short_kernel<2, false>), grid, dim3(64), 0, s, a);
+            else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, false>), grid, dim3(64), 0, s, a);
+            else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, false>), grid, dim3(64), 0, s, a);
+            else hipLaunchKernelGGL((sfk::attn_short_kernel<8, false>), grid, dim3(64), 0, s, a);
+        }
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+    } else {
+        const dim3 grid(ns * nqc, d->H, d->B);
+        if (d->exact_pv) {
+            if (f16) hipLaunchKernelGGL((sfk::attn_ring_kernel<true, true>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((sfk::attn_ring_kernel<true, false>), grid, dim3(256), 0, s, a);
+        } else {
+            if (f16) hipLaunchKernelGGL((sfk::attn_ring_kernel<false, true>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((sfk::attn_ring_kernel<false, false>), grid, dim3(256), 0, s, a);
+        }
     }
-    if (d->exact_pv)
-        hipLaunchKernelGGL(sfk::attn_ring_kernel<true>, dim3(ns * nqc, d->H, d->B), dim3(256), 0, s, a);
-    else
-        hipLaunchKernelGGL(sfk::attn_ring_kernel<false>, dim3(ns * nqc, d->H, d->B), dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     if (ns > 1) {
         hipLaunchKernelGGL(sfk::attn_merge_kernel, dim3((d->Sq + 3) / 4, d->H, d->B), dim3(256), 0,

@@ -917,6 +917,9 @@ bool splittable(const sf_gemm_desc* d) {
 }
 
 int gemm_single_pass(const sf_gemm_desc* d, const sfk::EpiArgs& e, hipStream_t s) {
+    // one buffer range covers the whole weight (32-bit byte offsets)
+    const int64_t wbytes = d->w_dtype == SF_I8 ? 1 : 2;
+    if ((int64_t)d->N * d->ldw * wbytes > 0x7fffffffLL) return SF_ENOTSUP;
     sfk::GemmArgs g{};
     g.a = static_cast<const uint16_t*>(d->A);
     g.w = d->W;

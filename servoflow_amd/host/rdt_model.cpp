@@ -156,6 +156,10 @@ int add_matrix(sf_rdt* m, const std::string& name, int64_t N, int64_t K, bool qu
     return add_param(m, name, i8 ? SF_I8 : SF_BF16, {N, K});
 }
 
+int64_t ffn_dim(const sf_rdt_config& c) {
+    return (int64_t)(c.mlp_ratio > 1 ? c.mlp_ratio : 1) * c.hidden;
+}
+
 void build_param_table(sf_rdt* m) {
     const sf_rdt_config& c = m->cfg;
     const int64_t D = c.hidden;
@@ -212,9 +216,11 @@ void build_param_table(sf_rdt* m) {
         L.ck_norm = vec(p + "cross_attn.k_norm.weight", 64, true);
         L.cproj_w = add_matrix(m, p + "cross_attn.proj.weight", D, D, true);
         L.cproj_b = vec(p + "cross_attn.proj.bias", D);
-        L.fc1_w = add_matrix(m, p + "ffn.fc1.weight", D, D, true);
-        L.fc1_b = vec(p + "ffn.fc1.bias", D);
-        L.fc2_w = add_matrix(m, p + "ffn.fc2.weight", D, D, true);
+        // FFN D -> F -> D, F = mlp_ratio * D (the reference: F = D,
+        // config.h:60-61, dit_block.cu:345-346)
+        L.fc1_w = add_matrix(m, p + "ffn.fc1.weight", ffn_dim(c), D, true);
+        L.fc1_b = vec(p + "ffn.fc1.bias", ffn_dim(c));
+        L.fc2_w = add_matrix(m, p + "ffn.fc2.weight", D, ffn_dim(c), true);
         L.fc2_b = vec(p + "ffn.fc2.bias", D);
     }
     // final layer (dit_block.cu:392-412)
@@ -406,7 +412,8 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
                      lang ? m->lang_len : nullptr, m->a, s));
     SF_TRY(linear_add_norm(m, m->a, M, L.cproj_w, L.cproj_b, L.norm3, s));
     // FFN branch (Mlp::forward, dit_block.cu:143-163)
-    SF_TRY(linear(m, m->n, D, M, L.fc1_w, L.fc1_b, SF_ACT_GELU_TANH, m->h, D, SF_BF16, false, s));
+    const int F = (int)ffn_dim(c);
+    SF_TRY(linear(m, m->n, D, M, L.fc1_w, L.fc1_b, SF_ACT_GELU_TANH, m->h, F, SF_BF16, false, s));
     return linear_add_norm(m, m->h, M, L.fc2_w, L.fc2_b, next_norm(m, i), s);
 }
 
@@ -499,6 +506,7 @@ extern "C" void sf_rdt_config_default(sf_rdt_config* c) {
     c->batch = 1;
     c->int8_weights = 0;
     c->eps = 1e-6f;
+    c->mlp_ratio = 1;
 }
 
 extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
@@ -508,6 +516,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     if (c.hidden <= 0 || c.heads <= 0 || c.hidden != c.heads * 64) return SF_ENOTSUP;
     if (c.layers < 0 || c.batch <= 0 || c.horizon <= 0 || c.action_dim <= 0 || c.num_steps <= 0)
         return SF_EINVAL;
+    if (c.mlp_ratio < 0 || c.mlp_ratio > 8) return SF_EINVAL;
     if (c.lang_max <= 0 || c.img_len <= 0 || c.freq_dim <= 0 || c.num_train_timesteps <= 0)
         return SF_EINVAL;
     if ((c.hidden | c.freq_dim | c.lang_token_dim | c.img_token_dim | (2 * c.state_dim) |
@@ -540,7 +549,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
         {(void**)&m->k, (size_t)(B * H * S * 64 * 2)},
         {(void**)&m->v, (size_t)(B * H * S * 64 * 2)},
         {(void**)&m->a, (size_t)(B * S * D * 2)},
-        {(void**)&m->h, (size_t)(B * S * D * 2)},
+        {(void**)&m->h, (size_t)(B * S * ffn_dim(c) * 2)},
         {(void**)&m->act_in, (size_t)(B * T * 2 * A * 2)},
         {(void**)&m->sa0, (size_t)(B * T * D * 2)},
         {(void**)&m->sa1, (size_t)(B * T * D * 2)},

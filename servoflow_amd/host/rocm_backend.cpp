@@ -2,9 +2,9 @@
 //
 // Mirrors CUDABackend::attention (src/backend/cuda/cuda_backend.cu:470-501):
 // device checks, a workspace, one kernel launch on the caller's stream; with
-// the differences that the workspace persists across calls instead of a
-// per-call cudaMallocAsync / cudaFreeAsync (:483-490), and that the mask is
-// applied instead of ignored.
+// the differences that each stream's workspace persists across calls instead
+// of a per-call cudaMallocAsync / cudaFreeAsync (:483-490), and that the mask
+// is applied instead of ignored.
 #include "rocm_backend.h"
 
 #include <hip/hip_runtime.h>
@@ -111,30 +111,47 @@ void apply_mask(const TensorRef& m, int64_t B, int64_t Sk, sf_attn_desc& d) {
 }  // namespace
 
 RocmBackend::~RocmBackend() {
-    if (ws_) (void)hipFree(ws_);
+    for (auto& kv : ws_)
+        if (kv.second.ptr) (void)hipFree(kv.second.ptr);
 }
 
 size_t RocmBackend::attention_workspace_bytes(const TensorRef& Q, const TensorRef& K) {
     if (Q.ndim() != 4 || K.ndim() != 4) return 0;
     sf_attn_desc d;
+    // the partials' size does not depend on the element type
     sf_attn_desc_init_bhsd(&d, (int32_t)Q.shape[0], (int32_t)Q.shape[1], (int32_t)Q.shape[2],
                            (int32_t)K.shape[2], (int32_t)Q.shape[3], SF_BF16, SF_BF16);
     return sf_attn_workspace_bytes(&d);
 }
 
-void RocmBackend::reserve_attention_workspace(size_t bytes) {
-    std::lock_guard<std::mutex> lock(mu_);
-    if (bytes <= ws_bytes_) return;
-    if (ws_) {
-        if (hipFree(ws_) != hipSuccess) throw std::runtime_error("RocmBackend: hipFree failed");
-        ws_ = nullptr;
-        ws_bytes_ = 0;
+void RocmBackend::grow(Workspace& ws, size_t bytes, StreamHandle stream) {
+    if (bytes <= ws.bytes) return;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess)
+        throw std::runtime_error("RocmBackend::attention: hipStreamIsCapturing failed");
+    if (cs != hipStreamCaptureStatusNone)
+        throw std::runtime_error(
+            "RocmBackend::attention: workspace too small inside graph capture; call "
+            "reserve_attention_workspace() for this stream before capturing");
+    if (ws.ptr) {
+        // earlier calls queued on this stream may still read the old buffer
+        if (hipStreamSynchronize(s) != hipSuccess)
+            throw std::runtime_error("RocmBackend: hipStreamSynchronize failed");
+        if (hipFree(ws.ptr) != hipSuccess) throw std::runtime_error("RocmBackend: hipFree failed");
+        ws.ptr = nullptr;
+        ws.bytes = 0;
     }
-    if (hipMalloc(&ws_, bytes) != hipSuccess) {
-        ws_ = nullptr;
+    if (hipMalloc(&ws.ptr, bytes) != hipSuccess) {
+        ws.ptr = nullptr;
         throw std::runtime_error("RocmBackend: workspace allocation failed");
     }
-    ws_bytes_ = bytes;
+    ws.bytes = bytes;
+}
+
+void RocmBackend::reserve_attention_workspace(size_t bytes, StreamHandle stream) {
+    std::lock_guard<std::mutex> lock(mu_);
+    grow(ws_[stream], bytes, stream);
 }
 
 void RocmBackend::attention(const TensorRef& Q, const TensorRef& K, const TensorRef& V,
@@ -148,8 +165,8 @@ void RocmBackend::attention(const TensorRef& Q, const TensorRef& K, const Tensor
     if (K.shape != std::vector<int64_t>{B, H, Sk, D} || V.shape != K.shape || out.shape != Q.shape)
         bad("shape mismatch between Q, K, V and out");
     if (Q.dtype != K.dtype || Q.dtype != V.dtype) bad("Q, K and V must share a dtype");
-    if (Q.dtype != DType::BFloat16) bad("Q, K and V must be BFloat16");
-    if (out.dtype != DType::BFloat16 && out.dtype != DType::Float32) bad("out must be BFloat16 or Float32");
+    if (sf_type(Q.dtype) < 0) bad("Q, K and V must be Float32, Float16 or BFloat16");
+    if (sf_type(out.dtype) < 0) bad("out must be Float32, Float16 or BFloat16");
 
     sf_attn_desc d;
     sf_attn_desc_init_bhsd(&d, (int32_t)B, (int32_t)H, (int32_t)S, (int32_t)Sk, (int32_t)D,
@@ -160,29 +177,13 @@ void RocmBackend::attention(const TensorRef& Q, const TensorRef& K, const Tensor
     elem_strides(out, "out", d.o_stride);
     d.scale = scale;
     d.is_causal = is_causal ? 1 : 0;
+    d.exact_pv = precision_ == AttentionPrecision::Exact ? 1 : 0;
     if (mask) apply_mask(*mask, B, Sk, d);
 
-    hipStream_t s = static_cast<hipStream_t>(stream);
     std::lock_guard<std::mutex> lock(mu_);
-    const size_t need = sf_attn_workspace_bytes(&d);
-    if (need > ws_bytes_) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(s, &cs) != hipSuccess)
-            throw std::runtime_error("RocmBackend::attention: hipStreamIsCapturing failed");
-        if (cs != hipStreamCaptureStatusNone)
-            throw std::runtime_error(
-                "RocmBackend::attention: workspace too small inside graph capture; call "
-                "reserve_attention_workspace() before capturing");
-        if (ws_ && hipFree(ws_) != hipSuccess) throw std::runtime_error("RocmBackend: hipFree failed");
-        ws_ = nullptr;
-        ws_bytes_ = 0;
-        if (hipMalloc(&ws_, need) != hipSuccess) {
-            ws_ = nullptr;
-            throw std::runtime_error("RocmBackend: workspace allocation failed");
-        }
-        ws_bytes_ = need;
-    }
-    check_status(sf_attn_fwd(&d, Q.data, K.data, V.data, out.data, ws_, ws_bytes_, stream));
+    Workspace& ws = ws_[stream];
+    grow(ws, sf_attn_workspace_bytes(&d), stream);
+    check_status(sf_attn_fwd(&d, Q.data, K.data, V.data, out.data, ws.ptr, ws.bytes, stream));
 }
 
 }  // namespace sf_amd

@@ -21,14 +21,17 @@
 //                                    Sk rounded up to 4 bytes
 //   anything else                    std::invalid_argument
 //
-// Thread-compatible like the reference (backend.h:35-42): the workspace is
-// guarded by a mutex; a stream must not be shared across threads.  The
-// workspace grows on demand outside graph capture; before capturing, size it
-// with reserve_attention_workspace().
+// Thread-compatible like the reference (backend.h:35-42): a stream must not
+// be shared across threads.  Each stream gets its own split-K workspace (so
+// calls on different streams never share partials), guarded by a mutex; a
+// stream's workspace grows on demand outside graph capture (after that
+// stream's queued work has finished); before capturing, size it with
+// reserve_attention_workspace() for the capturing stream.
 #pragma once
 
 #include <cstddef>
 #include <cstdint>
+#include <map>
 #include <mutex>
 #include <vector>
 
@@ -65,31 +68,51 @@ struct TensorRef {
 
 size_t dtype_size(DType dt);
 
+// Precision of the P.V contraction for 16-bit inputs.  Exact (the default):
+// V in its input type and P carried as a (hi, lo) pair, finite for any
+// finite V, like the reference's fp32 naive kernel.  Fast: P rounded to fp16
+// (~2e-4 relative error); a BFloat16 V is then converted to fp16, so a V
+// element with |v| >= 2^16 makes its output column inf/NaN (the range of the
+// reference's fp16 flash-attention path, attention.cu:29-80).  Float32
+// inputs ignore this (fp32 products throughout).
+enum class AttentionPrecision { Exact, Fast };
+
 class RocmBackend {
 public:
-    RocmBackend() = default;
+    explicit RocmBackend(AttentionPrecision precision = AttentionPrecision::Exact)
+        : precision_(precision) {}
     ~RocmBackend();
     RocmBackend(const RocmBackend&) = delete;
     RocmBackend& operator=(const RocmBackend&) = delete;
 
     // out = softmax(Q K^T * scale [masked]) V per (b, h).
-    // Q [B,H,S,D], K/V [B,H,Sk,D] bf16; out [B,H,S,D] bf16 or fp32 (any
-    // strides with a contiguous head dim, e.g. a [B,S,H,D] buffer viewed as
-    // BHSD).  D = 64.
+    // Q [B,H,S,D], K/V [B,H,Sk,D] all Float32, Float16 or BFloat16 (one
+    // dtype: Float32 is the reference's fp32 path, attention.cu:183-197);
+    // out [B,H,S,D] Float32, Float16 or BFloat16 (any strides with a
+    // contiguous head dim, e.g. a [B,S,H,D] buffer viewed as BHSD).  D = 64.
     void attention(const TensorRef& Q, const TensorRef& K, const TensorRef& V, TensorRef& out,
                    const TensorRef* mask = nullptr, float scale = 0.f, bool is_causal = false,
                    StreamHandle stream = nullptr);
 
-    // Makes sure the split-K workspace holds at least `bytes` (allocates
-    // now, outside any capture).  attention_workspace_bytes() gives the size
-    // a call needs.
-    void reserve_attention_workspace(size_t bytes);
+    // Makes sure `stream`'s split-K workspace holds at least `bytes`
+    // (allocates now, outside any capture).  attention_workspace_bytes()
+    // gives the size a call needs.
+    void reserve_attention_workspace(size_t bytes, StreamHandle stream = nullptr);
     static size_t attention_workspace_bytes(const TensorRef& Q, const TensorRef& K);
 
+    AttentionPrecision precision() const { return precision_; }
+
 private:
+    struct Workspace {
+        void* ptr = nullptr;
+        size_t bytes = 0;
+    };
+    // Grows ws to `bytes` outside capture; mu_ held.
+    void grow(Workspace& ws, size_t bytes, StreamHandle stream);
+
+    AttentionPrecision precision_;
     std::mutex mu_;
-    void* ws_ = nullptr;
-    size_t ws_bytes_ = 0;
+    std::map<StreamHandle, Workspace> ws_;
 };
 
 }  // namespace sf_amd

@@ -128,10 +128,13 @@ struct Json {
         *out = neg ? -(int64_t)v : (int64_t)v;
         return true;
     }
-    // Skips any JSON value (metadata is ignored).
-    void skip() {
+    // Skips any JSON value (metadata is ignored).  Nesting deeper than
+    // kMaxDepth is a header error, so a hostile header cannot exhaust the
+    // stack through the recursion.
+    static constexpr int kMaxDepth = 64;
+    void skip(int depth = 0) {
         ws();
-        if (p >= e) { fail(); return; }
+        if (p >= e || depth >= kMaxDepth) { fail(); return; }
         if (*p == '"') { (void)str(); return; }
         if (*p == '{') {
             ++p;
@@ -139,7 +142,7 @@ struct Json {
             do {
                 (void)str();
                 if (!eat(':')) { fail(); return; }
-                skip();
+                skip(depth + 1);
             } while (ok && eat(','));
             if (!eat('}')) fail();
             return;
@@ -147,7 +150,7 @@ struct Json {
         if (*p == '[') {
             ++p;
             if (eat(']')) return;
-            do skip(); while (ok && eat(','));
+            do skip(depth + 1); while (ok && eat(','));
             if (!eat(']')) fail();
             return;
         }

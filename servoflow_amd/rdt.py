@@ -21,7 +21,8 @@ class RdtConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "hidden", "layers", "heads", "action_dim", "horizon", "freq_dim", "state_dim",
         "lang_max", "img_len", "lang_token_dim", "img_token_dim", "num_train_timesteps",
-        "ctrl_freq", "num_steps", "batch", "int8_weights")] + [("eps", ctypes.c_float)]
+        "ctrl_freq", "num_steps", "batch", "int8_weights")] + [("eps", ctypes.c_float),
+                                                             ("mlp_ratio", ctypes.c_int32)]
 
 
 class StEntry(ctypes.Structure):

@@ -296,7 +296,7 @@ void test_graph_capture_with_reserved_workspace() {
         CHECK(threw, "capture without reserve must throw std::runtime_error");
     }
     RocmBackend be;
-    be.reserve_attention_workspace(RocmBackend::attention_workspace_bytes(q.ref(), k.ref()));
+    be.reserve_attention_workspace(RocmBackend::attention_workspace_bytes(q.ref(), k.ref()), st);
     be.attention(q.ref(), k.ref(), v.ref(), eager, nullptr, 0.f, false, st);
     HIP_OK(hipStreamSynchronize(st));
     hipGraph_t g;
@@ -318,6 +318,169 @@ void test_graph_capture_with_reserved_workspace() {
     (void)hipStreamDestroy(st);
 }
 
+// A tensor of any input dtype: N(0,1) rounded to that dtype on the host
+// (fp32 copy for the oracle), stored on the device in that dtype.
+struct AnyTensor {
+    std::vector<float> host;
+    DevBuf dev;
+    std::vector<int64_t> shape;
+    DType dt;
+    AnyTensor(uint64_t seed, std::vector<int64_t> shp, DType t)
+        : host(Bf16Tensor::numel(shp)), dev(Bf16Tensor::numel(shp) * sf_amd::dtype_size(t)), shape(shp), dt(t) {
+        sfo_randn(seed, (int64_t)host.size(), 1.f, host.data());
+        std::vector<uint16_t> h16(host.size());
+        for (size_t i = 0; i < host.size(); ++i) {
+            if (t == DType::Float16) {
+                const _Float16 x = (_Float16)host[i];
+                host[i] = (float)x;
+                std::memcpy(&h16[i], &x, 2);
+            } else if (t == DType::BFloat16) {
+                host[i] = sfo_bf16_round(host[i]);
+                h16[i] = to_bf16(host[i]);
+            }
+        }
+        const void* src = t == DType::Float32 ? static_cast<const void*>(host.data()) : h16.data();
+        if (hipMemcpy(dev.p, src, dev.n, hipMemcpyHostToDevice) != hipSuccess) throw std::runtime_error("hipMemcpy");
+    }
+    TensorRef ref() const { return TensorRef::contiguous(dev.p, dt, shape); }
+};
+
+// fp32 output of RocmBackend::attention for one input dtype vs the oracle.
+void dtype_case(DType dt, int B, int H, int S, int Sk, const int32_t* lens, double max_abs, double mean_rel,
+                const char* what) {
+    RocmBackend be;
+    AnyTensor q(81 + Sk, {B, H, S, 64}, dt), k(82 + Sk, {B, H, Sk, 64}, dt), v(83 + Sk, {B, H, Sk, 64}, dt);
+    DevBuf ob((size_t)B * H * S * 64 * 4);
+    TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {B, H, S, 64});
+    DevBuf lb(lens ? (size_t)B * 4 : 4);
+    TensorRef mask;
+    if (lens) {
+        HIP_OK(hipMemcpy(lb.p, lens, (size_t)B * 4, hipMemcpyHostToDevice));
+        mask = TensorRef::contiguous(lb.p, DType::Int32, {B});
+    }
+    be.attention(q.ref(), k.ref(), v.ref(), out, lens ? &mask : nullptr);
+    HIP_OK(hipDeviceSynchronize());
+    std::vector<float> ref(q.host.size());
+    sfo_attention_f32(q.host.data(), k.host.data(), v.host.data(), ref.data(), B, H, S, Sk, 64, 0.f, 0, lens);
+    const std::vector<float> got = download_f32(ob, ref.size());
+    double sd = 0, sr = 0, mx = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        CHECK(std::isfinite(got[i]), what);
+        const double d = std::fabs((double)got[i] - ref[i]);
+        sd += d;
+        sr += std::fabs((double)ref[i]);
+        mx = d > mx ? d : mx;
+    }
+    if (!(mx <= max_abs && sd / sr <= mean_rel)) {
+        char buf[200];
+        std::snprintf(buf, sizeof buf, "%s: max-abs %.3e mean-rel %.3e", what, mx, sd / sr);
+        throw std::runtime_error(buf);
+    }
+}
+
+void test_float16_tensors() {
+    // the reference's default compute dtype (config.h:57); exact P.V form
+    dtype_case(DType::Float16, 1, 32, 67, 67, nullptr, 2e-2, 2e-5, "Float16 self 1x32x67x67");
+    dtype_case(DType::Float16, 1, 32, 67, 4374, nullptr, 2e-2, 2e-5, "Float16 image 1x32x67x4374");
+    const int32_t lens[2] = {1024, 333};
+    dtype_case(DType::Float16, 2, 32, 67, 1024, lens, 2e-2, 2e-5, "Float16 language, valid lengths");
+}
+
+void test_float32_tensors() {
+    // the reference's fp32 path (naive kernel, attention.cu:90-139)
+    dtype_case(DType::Float32, 1, 32, 67, 67, nullptr, 1e-4, 1e-5, "Float32 self 1x32x67x67");
+    const int32_t lens[2] = {700, 32};
+    dtype_case(DType::Float32, 2, 32, 67, 1024, lens, 1e-4, 1e-5, "Float32 language, valid lengths");
+    dtype_case(DType::Float32, 1, 32, 67, 4374, nullptr, 1e-4, 1e-5, "Float32 image 1x32x67x4374");
+}
+
+void test_float16_output() {
+    RocmBackend be;
+    AnyTensor q(91, {1, 8, 67, 64}, DType::Float16), k(92, {1, 8, 900, 64}, DType::Float16),
+        v(93, {1, 8, 900, 64}, DType::Float16);
+    DevBuf o16((size_t)8 * 67 * 64 * 2), o32((size_t)8 * 67 * 64 * 4);
+    TensorRef out16 = TensorRef::contiguous(o16.p, DType::Float16, {1, 8, 67, 64});
+    TensorRef out32 = TensorRef::contiguous(o32.p, DType::Float32, {1, 8, 67, 64});
+    be.attention(q.ref(), k.ref(), v.ref(), out16);
+    be.attention(q.ref(), k.ref(), v.ref(), out32);
+    HIP_OK(hipDeviceSynchronize());
+    const size_t n = (size_t)8 * 67 * 64;
+    std::vector<uint16_t> h16(n);
+    HIP_OK(hipMemcpy(h16.data(), o16.p, n * 2, hipMemcpyDeviceToHost));
+    const std::vector<float> f32 = download_f32(o32, n);
+    for (size_t i = 0; i < n; ++i) {
+        _Float16 x;
+        std::memcpy(&x, &h16[i], 2);
+        const double ulp = std::fabs(f32[i]) * std::ldexp(1.0, -10) + std::ldexp(1.0, -24);
+        CHECK(std::fabs((double)(float)x - f32[i]) <= ulp, "Float16 out = fp32 out rounded");
+    }
+}
+
+void test_streams_have_separate_workspaces() {
+    // two image cross-attentions (7 key splits each, so both need partials)
+    // queued on two streams before either is waited for
+    const int B = 1, H = 32, S = 67, Sk = 4374;
+    Bf16Tensor q1(101, {B, H, S, 64}), k1(102, {B, H, Sk, 64}), v1(103, {B, H, Sk, 64});
+    Bf16Tensor q2(104, {B, H, S, 64}), k2(105, {B, H, Sk, 64}), v2(106, {B, H, Sk, 64});
+    DevBuf o1((size_t)B * H * S * 64 * 4), o2((size_t)B * H * S * 64 * 4);
+    TensorRef out1 = TensorRef::contiguous(o1.p, DType::Float32, {B, H, S, 64});
+    TensorRef out2 = TensorRef::contiguous(o2.p, DType::Float32, {B, H, S, 64});
+    hipStream_t s1, s2;
+    HIP_OK(hipStreamCreate(&s1));
+    HIP_OK(hipStreamCreate(&s2));
+    RocmBackend be;
+    for (int rep = 0; rep < 4; ++rep) {
+        be.attention(q1.ref(), k1.ref(), v1.ref(), out1, nullptr, 0.f, false, s1);
+        be.attention(q2.ref(), k2.ref(), v2.ref(), out2, nullptr, 0.f, false, s2);
+    }
+    HIP_OK(hipStreamSynchronize(s1));
+    HIP_OK(hipStreamSynchronize(s2));
+    std::vector<float> r1(q1.host.size()), r2(q2.host.size());
+    sfo_attention_f32(q1.host.data(), k1.host.data(), v1.host.data(), r1.data(), B, H, S, Sk, 64, 0.f, 0, nullptr);
+    sfo_attention_f32(q2.host.data(), k2.host.data(), v2.host.data(), r2.data(), B, H, S, Sk, 64, 0.f, 0, nullptr);
+    expect_close(download_f32(o1, r1.size()), r1, "stream 1");
+    expect_close(download_f32(o2, r2.size()), r2, "stream 2");
+    (void)hipStreamDestroy(s1);
+    (void)hipStreamDestroy(s2);
+}
+
+void test_precision_option_and_large_v() {
+    // a V element of 2^17 (finite in bf16): the default (exact) precision
+    // returns finite values matching the oracle; the fast form documents
+    // inf/NaN in that head dim's column
+    const int B = 1, H = 2, S = 67, Sk = 600;
+    Bf16Tensor q(111, {B, H, S, 64}), k(112, {B, H, Sk, 64}), v(113, {B, H, Sk, 64});
+    const size_t big = ((size_t)0 * Sk + 17) * 64 + 5;   // head 0, key 17, dim 5
+    v.host[big] = 131072.f;
+    const uint16_t bits = to_bf16(131072.f);
+    HIP_OK(hipMemcpy(static_cast<uint16_t*>(v.dev.p) + big, &bits, 2, hipMemcpyHostToDevice));
+    DevBuf ob((size_t)B * H * S * 64 * 4);
+    TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {B, H, S, 64});
+    RocmBackend exact;
+    CHECK(exact.precision() == sf_amd::AttentionPrecision::Exact, "default precision is exact");
+    exact.attention(q.ref(), k.ref(), v.ref(), out);
+    HIP_OK(hipDeviceSynchronize());
+    std::vector<float> ref(q.host.size());
+    sfo_attention_f32(q.host.data(), k.host.data(), v.host.data(), ref.data(), B, H, S, Sk, 64, 0.f, 0, nullptr);
+    const std::vector<float> got = download_f32(ob, ref.size());
+    double sd = 0, sr = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        CHECK(std::isfinite(got[i]), "exact precision: finite output for large V");
+        sd += std::fabs((double)got[i] - ref[i]);
+        sr += std::fabs((double)ref[i]);
+    }
+    CHECK(sd / sr <= 1e-4, "exact precision matches the oracle with large V");
+    RocmBackend fast(sf_amd::AttentionPrecision::Fast);
+    fast.attention(q.ref(), k.ref(), v.ref(), out);
+    HIP_OK(hipDeviceSynchronize());
+    const std::vector<float> gf = download_f32(ob, ref.size());
+    bool col_nonfinite = false;
+    for (int s = 0; s < S; ++s) col_nonfinite |= !std::isfinite(gf[(size_t)s * 64 + 5]);
+    CHECK(col_nonfinite, "fast precision: |v| >= 2^16 reaches its column as inf/NaN");
+    for (size_t i = 0; i < gf.size(); ++i)
+        if (i % 64 != 5) CHECK(std::isfinite(gf[i]), "fast precision: other columns finite");
+}
+
 }  // namespace
 
 int main() {
@@ -333,6 +496,11 @@ int main() {
     run_case("causal", test_causal);
     run_case("errors_use_reference_exception_types", test_errors_use_reference_exception_types);
     run_case("graph_capture_with_reserved_workspace", test_graph_capture_with_reserved_workspace);
+    run_case("float16_tensors", test_float16_tensors);
+    run_case("float32_tensors", test_float32_tensors);
+    run_case("float16_output", test_float16_output);
+    run_case("streams_have_separate_workspaces", test_streams_have_separate_workspaces);
+    run_case("precision_option_and_large_v", test_precision_option_and_large_v);
     if (g_failed) {
         std::printf("%d case(s) failed\n", g_failed);
         return 1;

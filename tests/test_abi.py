@@ -66,7 +66,7 @@ def test_desc_init_bhsd_strides():
 def test_rejects_unsupported_before_launch():
     d = abi.attn_desc_bhsd(1, 2, 67, 67, D=128)
     assert _fwd(d) == abi.SF_ENOTSUP
-    d = abi.attn_desc_bhsd(1, 2, 67, 67, in_dtype=abi.SF_F16)
+    d = abi.attn_desc_bhsd(1, 2, 67, 67, in_dtype=abi.SF_I8)
     assert _fwd(d) == abi.SF_ENOTSUP
     d = abi.attn_desc_bhsd(1, 2, 67, 67, out_dtype=abi.SF_I8)
     assert _fwd(d) == abi.SF_ENOTSUP
@@ -84,6 +84,35 @@ def test_rejects_bad_arguments_before_launch():
     d = abi.attn_desc_bhsd(1, 2, 67, 67)
     d.num_splits = -1
     assert _fwd(d) == abi.SF_EINVAL
+    # the output strides follow the same rules as the inputs
+    d = abi.attn_desc_bhsd(1, 2, 67, 67)
+    d.o_stride[2] = 68
+    assert _fwd(d) == abi.SF_EINVAL
+    d = abi.attn_desc_bhsd(1, 2, 67, 67)
+    d.o_stride[1] = 4
+    assert _fwd(d) == abi.SF_EINVAL
+    # rows closer than D apart (a zero s-stride would give an empty buffer range)
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        for bad in (0, 56):
+            d = abi.attn_desc_bhsd(1, 2, 67, 4374)
+            getattr(d, name)[2] = bad
+            assert _fwd(d) == abi.SF_EINVAL, (name, bad)
+
+
+def test_gemm_single_pass_rejects_weights_beyond_32bit_range():
+    """The workspace-free path addresses the whole weight through one 32-bit
+    buffer range: a weight over 2 GiB is SF_ENOTSUP, not rows read as zeros."""
+    g = abi.GemmDesc()
+    g.M, g.N, g.K = 67, 1 << 20, 2048
+    g.A, g.lda, g.a_dtype = 256, 2048, abi.SF_BF16
+    g.W, g.ldw, g.w_dtype = 256, 2048, abi.SF_BF16
+    g.epilogue, g.C, g.ldc, g.c_dtype = abi.SF_EPI_PLAIN, 256, 1 << 20, abi.SF_F32
+    assert abi.lib().sf_gemm(ctypes.byref(g), None) == abi.SF_ENOTSUP
+    g.w_dtype = abi.SF_I8                  # int8: 1 byte per weight, 2^31 + 2^20 bytes
+    g.w_scale = 256
+    g.N = (1 << 20) + 512
+    g.ldc = g.N
+    assert abi.lib().sf_gemm(ctypes.byref(g), None) == abi.SF_ENOTSUP
 
 
 def test_empty_problem_is_a_noop():

@@ -64,3 +64,18 @@ def test_malformed_files_are_rejected(tmp_path, content):
 def test_missing_file_is_an_error(tmp_path):
     with pytest.raises(abi.SfError):
         R.inspect_safetensors(str(tmp_path / "nope.safetensors"))
+
+
+@pytest.mark.parametrize("depth,ok", [(10, True), (63, True), (200, False), (100000, False)])
+def test_metadata_nesting_depth_is_bounded(tmp_path, depth, ok):
+    """Nested metadata is skipped recursively; past 64 levels the header is
+    rejected instead of recursing without bound."""
+    meta = "[" * depth + "]" * depth
+    hdr = ('{"__metadata__": ' + meta + ', "t": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}').encode()
+    path = tmp_path / "nest.safetensors"
+    path.write_bytes(struct.pack("<Q", len(hdr)) + hdr + b"\0" * 8)
+    if ok:
+        assert [e[0] for e in R.inspect_safetensors(str(path))] == ["t"]
+    else:
+        with pytest.raises(abi.SfError):
+            R.inspect_safetensors(str(path))
