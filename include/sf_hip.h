@@ -39,7 +39,8 @@ typedef enum sf_status {
     SF_ENOTSUP    = -2,  /* valid request this library does not implement  */
     SF_EWORKSPACE = -3,  /* workspace missing or smaller than required     */
     SF_ELAUNCH    = -4,  /* kernel launch failed (hipGetLastError)         */
-    SF_EDEVICE    = -5   /* HIP runtime error outside a launch             */
+    SF_EDEVICE    = -5,  /* HIP runtime error outside a launch             */
+    SF_ESCRATCH   = -6   /* request exceeds a fixed device scratch buffer  */
 } sf_status;
 
 /* Element types.  The numeric values equal servoflow's sf::DType
@@ -137,6 +138,23 @@ int32_t sf_attn_num_splits(const sf_attn_desc* desc);
 int sf_attn_fwd(const sf_attn_desc* desc, const void* q, const void* k,
                 const void* v, void* out, void* workspace,
                 size_t workspace_bytes, void* stream);
+
+/* Allocation-free form of sf_attn_fwd.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * split-K partials go to a fixed device array of
+ * SF_ATTN_NOALLOC_SCRATCH_BYTES held by the library on every GPU it runs on
+ * until the process ends (looked up on the first call on each device: make
+ * that first call outside a capture).  Same results as sf_attn_fwd with a
+ * caller workspace.  A call whose partials (sf_attn_workspace_bytes) exceed
+ * the array returns SF_ESCRATCH without launching anything; every split
+ * count chosen automatically fits, only a large forced num_splits does not.
+ * All calls on one GPU share its array and nothing in it needs to start at
+ * zero: calls that may overlap on one GPU (different streams, or another
+ * thread) race on it and must be serialised by the caller. */
+#define SF_ATTN_NOALLOC_SCRATCH_BYTES (8u << 20)
+int sf_attn_fwd_noalloc(const sf_attn_desc* desc, const void* q, const void* k,
+                        const void* v, void* out, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Projections: C[M,N] = act(A[M,K] . W[N,K]^T + bias[N]).

@@ -18,6 +18,8 @@ SF_ENOTSUP = -2
 SF_EWORKSPACE = -3
 SF_ELAUNCH = -4
 SF_EDEVICE = -5
+SF_ESCRATCH = -6
+SF_ATTN_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 SF_F32 = 0
 SF_F16 = 1
@@ -111,6 +113,9 @@ def lib() -> ctypes.CDLL:
     L.sf_attn_fwd.argtypes = [P, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     L.sf_attn_fwd.restype = ctypes.c_int
+    L.sf_attn_fwd_noalloc.argtypes = [P, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p]
+    L.sf_attn_fwd_noalloc.restype = ctypes.c_int
     L.sf_gemm.argtypes = [ctypes.POINTER(GemmDesc), ctypes.c_void_p]
     L.sf_gemm.restype = ctypes.c_int
     L.sf_gemm_workspace_bytes.argtypes = [ctypes.POINTER(GemmDesc)]

@@ -35,6 +35,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "sf_device.h"
 #include "sf_hip.h"
 
@@ -1100,6 +1102,54 @@ int validate(const sf_attn_desc* d) {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the split-K partials live in a fixed device array
+// instead of a caller workspace.  Every auto-chosen split count keeps the
+// partials under ~5.4 MB (B*H*chunks*splits is about one workgroup per CU,
+// 256 x 80 rows x 66 floats), so only a forced num_splits can exceed it.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[SF_ATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};   // device address of `scratch`, per device
+
+// The device address of this device's copy of `scratch`, looked up once per
+// device (with that device current) on its first use.  Host code never
+// passes the array's name itself to a kernel: on the host that name is a
+// stand-in, not a device address.
+int scratch_address(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return SF_EDEVICE;
+    if (dev < 0 || dev >= kMaxDevices) return SF_ENOTSUP;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SF_EDEVICE;
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return SF_OK;
+}
+
+}  // namespace
+
+extern "C" int sf_attn_fwd_noalloc(const sf_attn_desc* d, const void* q, const void* k, const void* v,
+                                   void* out, void* stream) {
+    const int st = validate(d);
+    if (st != SF_OK) return st;
+    const size_t need = sf_attn_workspace_bytes(d);
+    if (need > (size_t)SF_ATTN_NOALLOC_SCRATCH_BYTES) return SF_ESCRATCH;
+    void* ws = nullptr;
+    if (need > 0) {
+        const int sst = scratch_address(&ws);
+        if (sst != SF_OK) return sst;
+    }
+    return sf_attn_fwd(d, q, k, v, out, ws, need, stream);
+}
+
 extern "C" void sf_attn_desc_init_bhsd(sf_attn_desc* d, int32_t B, int32_t H, int32_t Sq,
                                        int32_t Sk, int32_t D, int32_t in_dtype,
                                        int32_t out_dtype) {
@@ -1217,6 +1267,7 @@ extern "C" const char* sf_strerror(int status) {
         case SF_EWORKSPACE: return "workspace missing or too small";
         case SF_ELAUNCH: return "kernel launch failed";
         case SF_EDEVICE: return "HIP runtime error";
+        case SF_ESCRATCH: return "request exceeds the fixed device scratch of the allocation-free entry point";
         default: return "unknown status";
     }
 }

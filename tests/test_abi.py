@@ -45,7 +45,8 @@ def test_library_exports_symbol(name):
 
 
 def test_strerror_texts():
-    for st in (abi.SF_OK, abi.SF_EINVAL, abi.SF_ENOTSUP, abi.SF_EWORKSPACE, abi.SF_ELAUNCH, abi.SF_EDEVICE):
+    for st in (abi.SF_OK, abi.SF_EINVAL, abi.SF_ENOTSUP, abi.SF_EWORKSPACE, abi.SF_ELAUNCH, abi.SF_EDEVICE,
+               abi.SF_ESCRATCH):
         assert len(abi.strerror(st)) > 3
     assert abi.strerror(12345) == "unknown status"
 
@@ -153,3 +154,28 @@ def test_backend_library_loads_and_exports_the_operator():
     syms = subprocess.run(["nm", "-DC", path], capture_output=True, text=True).stdout
     assert "sf_amd::RocmBackend::attention(" in syms
     assert "sf_amd::RocmBackend::reserve_attention_workspace(" in syms
+
+
+def test_noalloc_rejects_before_touching_the_device():
+    """sf_attn_fwd_noalloc validates and sizes its partials on the host: a bad
+    descriptor and partials beyond the fixed scratch return without a HIP call."""
+    d = abi.attn_desc_bhsd(1, 32, 67, 4374)
+    d.D = 128
+    assert abi.lib().sf_attn_fwd_noalloc(ctypes.byref(d), 16, 16, 16, 16, None) == abi.SF_ENOTSUP
+    d = abi.attn_desc_bhsd(4, 32, 67, 4374)
+    d.num_splits = 32
+    assert abi.lib().sf_attn_workspace_bytes(ctypes.byref(d)) > abi.SF_ATTN_NOALLOC_SCRATCH_BYTES
+    assert abi.lib().sf_attn_fwd_noalloc(ctypes.byref(d), 16, 16, 16, 16, None) == abi.SF_ESCRATCH
+
+
+def test_auto_split_partials_fit_the_noalloc_scratch():
+    """Every automatically chosen split count keeps its partials inside the
+    allocation-free entry point's scratch."""
+    worst = 0
+    for B in (1, 2, 3, 4, 5, 8, 16):
+        for H in (1, 8, 32):
+            for Sq in (1, 16, 67, 80, 81, 160, 200, 1000):
+                for Sk in (129, 1024, 4374, 65536, 1 << 20):
+                    d = abi.attn_desc_bhsd(B, H, Sq, Sk)
+                    worst = max(worst, abi.lib().sf_attn_workspace_bytes(ctypes.byref(d)))
+    assert 0 < worst <= abi.SF_ATTN_NOALLOC_SCRATCH_BYTES
