@@ -63,6 +63,11 @@ int sf_add_pos_bf16(const void* tok, const float* pos, void* out, int32_t B, int
  * flow_matching.cpp:77-78). */
 int sf_euler_update(float* x, const float* v, int32_t B, int32_t T, int32_t A, int32_t S,
                     float dt, void* stream);
+/* *out = max(*out, max |p[i]|) over n bf16 values (p 16-byte aligned; *out
+ * fp32, >= 0, initialised by the caller, e.g. sf_fill_f32 with 0): NaN in p
+ * gives NaN.  The runtime checks each layer's cached V against the fp16
+ * range of the fast P.V form with it. */
+int sf_absmax_bf16(const void* p, int64_t n, float* out, void* stream);
 
 /* ---- model runtime (libsf_rdt.so) ---------------------------------------- */
 
@@ -150,6 +155,14 @@ int sf_rdt_sample(sf_rdt* m, float* x, int32_t use_graph, void* stream);
 int sf_rdt_infer(sf_rdt* m, uint64_t frame_id, const void* lang_tokens, const int32_t* lang_len,
                  const void* img_tokens, const void* state, uint64_t noise_seed,
                  float* action_out, int32_t* encoded, void* stream);
+
+/* P.V form block `layer`'s cross-attention runs with the current condition:
+ * 0 the fp16 form (every cached V element below 65504 in magnitude), 1 the
+ * exact bf16 form (a larger, infinite or NaN element), -1 on error.  The
+ * runtime measures each layer's max |V| when a condition is set and chooses
+ * the form before the next step or graph capture (one wait for the
+ * condition's encode per new condition); asking here does the same. */
+int32_t sf_rdt_pv_exact(sf_rdt* m, int32_t layer);
 
 /* Cross-attention K or V cache of block `layer` ([B, H, S, 64] bf16). */
 void* sf_rdt_cache_ptr(sf_rdt* m, int32_t layer, int32_t which_v);

@@ -8,12 +8,25 @@ Parameters are a dict name -> float32 array, named as in the reference
 checkpoint (tests/alignment/test_rdt1b_alignment.py:213-257,
 docs/RDT1B_ARCHITECTURE.md key list).
 
-`rb` (round to bf16): when True, values are rounded to bf16 at exactly the
-points where the GPU pipeline stores bf16 (GEMM inputs, per-head q/k/v,
-attention outputs, the cross-attention K/V cache); the residual stream and
-GEMM outputs that feed it stay fp32.  With rb=False everything is fp32 (the
-pure restatement).  The reference's own bf16 build rounds at all of these
-points and also rounds the residual (norm.cuh:146).
+`rb` (round to storage precision) names the storage points where values
+are rounded, to model a pipeline that stores them in 16-bit types:
+  True   every point below rounded to bf16 (GEMM inputs, per-head q/k/v,
+         attention outputs, the cross-attention K/V cache, condition tokens,
+         embeddings);
+  False  none: the pure fp32 restatement;
+  a set  of point names rounded to bf16;
+  a dict point name -> "bf16" or "f16", e.g. storage_points(ffn16=True) for
+         the MI355X runtime at batch <= 2, which stores the FFN inputs (the
+         norm3 output and the GELU hidden) in fp16.
+The residual stream and GEMM outputs that feed it stay fp32 throughout.  The
+reference's own bf16 build rounds at all of these points and also rounds the
+residual (norm.cuh:146).
+
+Points: "cond" condition tokens + position embedding, "kv" cross K/V cache,
+"n1" norm1 / norm_final outputs, "qkv" per-head q/k/v (self and cross),
+"a" attention outputs, "n2" / "n3" norm2 / norm3 outputs, "h" FFN and final
+hidden, "emb" timestep-embedding inputs, "adapt" adaptor inputs / hidden,
+"state" the state token.
 """
 from __future__ import annotations
 
@@ -45,8 +58,34 @@ class RdtConfig:
         return self.horizon + 3
 
 
-def _r(x, rb):
-    return O.bf16_round(x) if rb else np.ascontiguousarray(x, np.float32)
+ALL_POINTS = frozenset({"cond", "kv", "n1", "qkv", "a", "n2", "n3", "h", "emb", "adapt", "state"})
+
+
+def storage_points(ffn16):
+    """How the MI355X runtime stores each point: bf16 everywhere, except
+    (ffn16: batch * 67 <= 160 rows) the FFN inputs n3 and h in fp16."""
+    pts = {p: "bf16" for p in ALL_POINTS}
+    if ffn16:
+        pts["n3"] = pts["h"] = "f16"
+    return pts
+
+
+def _f16_round(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def _r(x, rb, point):
+    if rb is True:
+        return O.bf16_round(x)
+    if isinstance(rb, dict):
+        mode = rb.get(point)
+        if mode == "bf16":
+            return O.bf16_round(x)
+        if mode == "f16":
+            return _f16_round(x)
+    elif rb and point in rb:
+        return O.bf16_round(x)
+    return np.ascontiguousarray(x, np.float32)
 
 
 def heads_of(x, H):
@@ -62,7 +101,7 @@ def cross_kv(p, i, cond, cfg, rb=True):
     kv = O.linear(cond, p[pre + "kv.weight"], p[pre + "kv.bias"]).reshape(B, Sc, 2 * D)
     K, V = O.split_kv(kv, cfg.heads, 64)
     K = O.rms_norm(K, p[pre + "k_norm.weight"], cfg.eps)
-    return _r(K, rb), _r(V, rb)
+    return _r(K, rb, "kv"), _r(V, rb, "kv")
 
 
 def rdt_block(p, i, x, ck, cv, cond_len, cfg, rb=True):
@@ -72,23 +111,23 @@ def rdt_block(p, i, x, ck, cv, cond_len, cfg, rb=True):
     H = cfg.heads
     pre = f"blocks.{i}."
     # self-attention branch (dit_block.cu:198-238)
-    n1 = _r(O.rms_norm(x, p[pre + "norm1.weight"], cfg.eps), rb)
+    n1 = _r(O.rms_norm(x, p[pre + "norm1.weight"], cfg.eps), rb, "n1")
     qkv = O.linear(n1, p[pre + "attn.qkv.weight"], p[pre + "attn.qkv.bias"])
     Q, K, V = O.split_qkv(qkv.reshape(B, S, 3 * D), H, 64)
-    Q = _r(O.rms_norm(Q, p[pre + "attn.q_norm.weight"], cfg.eps), rb)
-    K = _r(O.rms_norm(K, p[pre + "attn.k_norm.weight"], cfg.eps), rb)
-    V = _r(V, rb)
-    a = _r(O.head_to_seq(O.attention_f32(Q, K, V)), rb)
+    Q = _r(O.rms_norm(Q, p[pre + "attn.q_norm.weight"], cfg.eps), rb, "qkv")
+    K = _r(O.rms_norm(K, p[pre + "attn.k_norm.weight"], cfg.eps), rb, "qkv")
+    V = _r(V, rb, "qkv")
+    a = _r(O.head_to_seq(O.attention_f32(Q, K, V)), rb, "a")
     x = x + O.linear(a, p[pre + "attn.proj.weight"], p[pre + "attn.proj.bias"])
     # cross-attention branch (dit_block.cu:274-326), norm2 from fused_add_rms_norm
-    n2 = _r(O.rms_norm(x, p[pre + "norm2.weight"], cfg.eps), rb)
+    n2 = _r(O.rms_norm(x, p[pre + "norm2.weight"], cfg.eps), rb, "n2")
     cq = O.linear(n2, p[pre + "cross_attn.q.weight"], p[pre + "cross_attn.q.bias"])
-    cq = _r(O.rms_norm(heads_of(cq.reshape(B, S, D), H), p[pre + "cross_attn.q_norm.weight"], cfg.eps), rb)
-    ca = _r(O.head_to_seq(O.attention_f32(cq, ck, cv, valid_len=cond_len)), rb)
+    cq = _r(O.rms_norm(heads_of(cq.reshape(B, S, D), H), p[pre + "cross_attn.q_norm.weight"], cfg.eps), rb, "qkv")
+    ca = _r(O.head_to_seq(O.attention_f32(cq, ck, cv, valid_len=cond_len)), rb, "a")
     x = x + O.linear(ca, p[pre + "cross_attn.proj.weight"], p[pre + "cross_attn.proj.bias"])
     # FFN branch (Mlp::forward, dit_block.cu:143-163: fc1 + GELU, fc2)
-    n3 = _r(O.rms_norm(x, p[pre + "norm3.weight"], cfg.eps), rb)
-    h = _r(O.linear(n3, p[pre + "ffn.fc1.weight"], p[pre + "ffn.fc1.bias"], act=1), rb)
+    n3 = _r(O.rms_norm(x, p[pre + "norm3.weight"], cfg.eps), rb, "n3")
+    h = _r(O.linear(n3, p[pre + "ffn.fc1.weight"], p[pre + "ffn.fc1.bias"], act=1), rb, "h")
     return x + O.linear(h, p[pre + "ffn.fc2.weight"], p[pre + "ffn.fc2.bias"])
 
 
@@ -97,16 +136,16 @@ def timestep_embed(p, name, step, cfg, rb=True):
     Linear + SiLU -> Linear.  Returns [1, D] fp32."""
     table = O.sincos_table(cfg.num_train_timesteps, cfg.freq_dim)
     step = max(0, min(int(step), cfg.num_train_timesteps - 1))
-    e = _r(table[step:step + 1], rb)
-    hdn = _r(O.linear(e, p[name + ".mlp.0.weight"], p[name + ".mlp.0.bias"], act=2), rb)
+    e = _r(table[step:step + 1], rb, "emb")
+    hdn = _r(O.linear(e, p[name + ".mlp.0.weight"], p[name + ".mlp.0.bias"], act=2), rb, "emb")
     return O.linear(hdn, p[name + ".mlp.2.weight"], p[name + ".mlp.2.bias"])
 
 
 def mlp_adaptor(p, name, x, depth, rb=True):
     """MlpAdaptor::forward, rdt1b.cpp:56-85: (Linear + GELU) x (depth-1), Linear."""
-    h = _r(x, rb)
+    h = _r(x, rb, "adapt")
     for j in range(depth - 1):
-        h = _r(O.linear(h, p[f"{name}.{2 * j}.weight"], p[f"{name}.{2 * j}.bias"], act=1), rb)
+        h = _r(O.linear(h, p[f"{name}.{2 * j}.weight"], p[f"{name}.{2 * j}.bias"], act=1), rb, "adapt")
     return O.linear(h, p[f"{name}.{2 * (depth - 1)}.weight"], p[f"{name}.{2 * (depth - 1)}.bias"])
 
 
@@ -123,8 +162,8 @@ def condition_tokens(p, lang_c, img_c, cfg, rb=True):
     """lang_c + lang_cond_pos_embed[:L], img_c + img_cond_pos_embed
     (rdt1b.cpp:342-349), rounded where the GPU stores them."""
     L = lang_c.shape[1]
-    lang = _r(lang_c + p["lang_cond_pos_embed"][:, :L], rb)
-    img = _r(img_c + p["img_cond_pos_embed"], rb)
+    lang = _r(lang_c + p["lang_cond_pos_embed"][:, :L], rb, "cond")
+    img = _r(img_c + p["img_cond_pos_embed"], rb, "cond")
     return lang, img
 
 
@@ -150,15 +189,16 @@ def denoise_step(p, x_t, t, state_tok, caches, lang_len, cfg, rb=True):
     x = np.empty((B, T + 3, D), np.float32)
     x[:, 0] = t_emb[0]
     x[:, 1] = f_emb[0]
-    x[:, 2] = _r(state_tok, rb)
+    x[:, 2] = _r(state_tok, rb, "state")
     x[:, 3:] = action_traj
     x = x + p["x_pos_embed"]                                            # :340
     for i in range(cfg.layers):                                         # :353-355
         ck, cv = caches[i]
         x = rdt_block(p, i, x, ck, cv, lang_len if i % 2 == 0 else None, cfg, rb)
     # FinalLayer::forward (dit_block.cu:407-412), last T tokens (rdt1b.cpp:362)
-    nf = _r(O.rms_norm(x, p["final_layer.norm_final.weight"], cfg.eps), rb)
-    hf = _r(O.linear(nf, p["final_layer.ffn_final.fc1.weight"], p["final_layer.ffn_final.fc1.bias"], act=1), rb)
+    nf = _r(O.rms_norm(x, p["final_layer.norm_final.weight"], cfg.eps), rb, "n1")
+    hf = _r(O.linear(nf, p["final_layer.ffn_final.fc1.weight"], p["final_layer.ffn_final.fc1.bias"], act=1), rb,
+            "h")
     out = O.linear(hf, p["final_layer.ffn_final.fc2.weight"], p["final_layer.ffn_final.fc2.bias"])
     return out[:, 3:]
 

@@ -63,8 +63,14 @@ namespace sfk {
 
 constexpr int kGemmThreads = 512;   // 8 waves
 
+// Activation (A operand) element kinds.  bf16: as loaded.  fp32: a bf16
+// (hi, lo) pair, two MFMAs per weight fragment.  fp16: fp16 MFMAs, with the
+// bf16 weight fragment converted to fp16 in registers (exact for bf16
+// magnitudes in [2^-14, 65504], to within 2^-25 below; int8 codes exact).
+enum ActKind { kActBF16 = 0, kActF32 = 1, kActF16 = 2 };
+
 struct GemmArgs {
-    const uint16_t* a;     // [M][lda] bf16
+    const void* a;         // [M][lda] bf16, fp32 or fp16 (ActKind)
     const void* w;         // [N][ldw] bf16 or int8
     const float* w_scale;  // [N] (int8 weights)
     const float* bias;     // [N] or null
@@ -73,6 +79,7 @@ struct GemmArgs {
     int M, N, K;
     int act;               // 0 none, 1 GELU(tanh), 2 SiLU
     int c_f32;
+    int c_f16;             // fp16 C (else bf16 when !c_f32)
     int accumulate;        // c (f32) += result
     // per-head epilogue
     int heads;             // 1: columns are sections of H*64 -> [B,H,S,D]
@@ -96,6 +103,26 @@ __device__ __forceinline__ float apply_act(int act, float v) {
     return act == 1 ? gelu_tanh(v) : (act == 2 ? silu(v) : v);
 }
 
+// Eight bf16 weights -> fp16x8 (round to nearest; exact in fp16's normal range).
+__device__ __forceinline__ f16x8 bf16x8_to_f16x8(u32x4 w) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_f16x2_rn(__uint_as_float(w[e] << 16), __uint_as_float(w[e] & 0xffff0000u));
+    return u32x4_as_f16x8(o);
+}
+
+// Eight int8 codes -> fp16x8 (exact).
+__device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 raw) {
+    u32x4 o;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t src = p < 2 ? raw.x : raw.y;
+        const int sh = (p & 1) * 16;
+        o[p] = pack_f16x2_rn((float)(int)(int8_t)(src >> sh), (float)(int)(int8_t)(src >> (sh + 8)));
+    }
+    return u32x4_as_f16x8(o);
+}
+
 // Eight int8 codes -> bf16x8 (exact: |code| <= 128 needs 8 significant bits).
 __device__ __forceinline__ bf16x8 i8x8_to_bf16x8(uint2 raw) {
     uint32_t w[4];
@@ -110,11 +137,25 @@ __device__ __forceinline__ bf16x8 i8x8_to_bf16x8(uint2 raw) {
     return u32x4_as_bf16x8(u32x4{w[0], w[1], w[2], w[3]});
 }
 
+// An fp32 activation x as a bf16 pair: hi = bf16(x) (nearest), lo =
+// bf16(x - hi); hi + lo carries ~16 significant bits of x, and
+// W.hi + W.lo on two bf16 MFMAs is the product with that activation.
+__device__ __forceinline__ void split_bf16x4(u32x4 f, uint2& hi, uint2& lo) {
+    const float x0 = __uint_as_float(f[0]), x1 = __uint_as_float(f[1]);
+    const float x2 = __uint_as_float(f[2]), x3 = __uint_as_float(f[3]);
+    hi.x = pack_bf16x2(x0, x1);
+    hi.y = pack_bf16x2(x2, x3);
+    lo.x = pack_bf16x2(x0 - bf16_bits_to_f32(hi.x & 0xffffu), x1 - bf16_bits_to_f32(hi.x >> 16));
+    lo.y = pack_bf16x2(x2 - bf16_bits_to_f32(hi.y & 0xffffu), x3 - bf16_bits_to_f32(hi.y >> 16));
+}
+
 // NR weight rows per workgroup: 16 (plain epilogue, K split 8 ways) or 64
 // (one attention head, K split 2 ways, per-head epilogue).  MB activation
-// blocks of 16 rows.  W8: int8 weights.
-template <int NR, int MB, bool W8>
+// blocks of 16 rows.  W8: int8 weights.  AK: activation kind (ActKind).
+template <int NR, int MB, bool W8, int AK>
 __global__ __launch_bounds__(kGemmThreads) void gemm_smallm_kernel(const GemmArgs g) {
+    constexpr bool A32 = AK == kActF32;
+    constexpr bool A16 = AK == kActF16;
     constexpr int KS = 8 / (NR / 16);         // waves sharing one n-block
     constexpr int MR = 16 * MB;
     __shared__ __attribute__((aligned(16))) float red[KS * NR * MR];
@@ -139,8 +180,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_smallm_kernel(const GemmArg
     const int wbytes = W8 ? 1 : 2;
     const __amdgpu_buffer_rsrc_t wrs =
         make_rsrc(g.w, (uint32_t)min((int64_t)g.N * g.ldw * wbytes, (int64_t)0x7fffffff));
-    const __amdgpu_buffer_rsrc_t ars = make_rsrc(g.a + (int64_t)m0 * g.lda,
-                                                 (uint32_t)((int64_t)max(0, min(MR, g.M - m0)) * g.lda * 2));
+    constexpr int AB = A32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(static_cast<const char*>(g.a) + (int64_t)m0 * g.lda * AB,
+                                                 (uint32_t)((int64_t)max(0, min(MR, g.M - m0)) * g.lda * AB));
     // Rows past N (and activation rows past M) read as zeros.
     const uint32_t wrow_off = wrow < g.N ? (uint32_t)((int64_t)wrow * g.ldw * wbytes) : 0x80000000u;
 
@@ -148,10 +190,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_smallm_kernel(const GemmArg
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    constexpr int U = 8;   // chunks in flight per wave
+    constexpr int U = A32 ? 4 : 8;   // chunks in flight per wave
     for (int c0 = c_beg; c0 < c_end; c0 += U) {
         bf16x8 wv[U];
+        f16x8 wh[A16 ? U : 1];
         bf16x8 av[U][MB];
+        bf16x8 al[A32 ? U : 1][MB];
 #pragma unroll
         for (int j = 0; j < U; ++j) {
             const int c = c0 + j;
@@ -161,21 +205,39 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_smallm_kernel(const GemmArg
                 const uint32_t off = live ? wrow_off + (uint32_t)k : 0x80000000u;
                 const uint2 raw = __builtin_bit_cast(
                     uint2, __builtin_amdgcn_raw_buffer_load_b64(wrs, off, 0, 0));
-                wv[j] = i8x8_to_bf16x8(raw);
+                if constexpr (A16) wh[j] = i8x8_to_f16x8(raw);
+                else wv[j] = i8x8_to_bf16x8(raw);
             } else {
                 const uint32_t off = live ? wrow_off + (uint32_t)k * 2 : 0x80000000u;
-                wv[j] = __builtin_bit_cast(bf16x8, buffer_load16(wrs, off));
+                const u32x4 raw = buffer_load16(wrs, off);
+                if constexpr (A16) wh[j] = bf16x8_to_f16x8(raw);
+                else wv[j] = __builtin_bit_cast(bf16x8, raw);
             }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
-                const uint32_t off = live ? (uint32_t)(((16 * mb + r) * g.lda + k) * 2) : 0x80000000u;
-                av[j][mb] = __builtin_bit_cast(bf16x8, buffer_load16(ars, off));
+                const uint32_t off = live ? (uint32_t)(((16 * mb + r) * g.lda + k) * AB) : 0x80000000u;
+                if constexpr (A32) {
+                    uint2 h0, l0, h1, l1;
+                    split_bf16x4(buffer_load16(ars, off), h0, l0);
+                    split_bf16x4(buffer_load16(ars, live ? off + 16 : 0x80000000u), h1, l1);
+                    av[j][mb] = u32x4_as_bf16x8(u32x4{h0.x, h0.y, h1.x, h1.y});
+                    al[j][mb] = u32x4_as_bf16x8(u32x4{l0.x, l0.y, l1.x, l1.y});
+                } else {
+                    av[j][mb] = __builtin_bit_cast(bf16x8, buffer_load16(ars, off));
+                }
             }
         }
 #pragma unroll
         for (int j = 0; j < U; ++j) {
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16x16x32(wv[j], av[j][mb], acc[mb]);
+            for (int mb = 0; mb < MB; ++mb) {
+                if constexpr (A16) {
+                    acc[mb] = mfma16x16x32_f16(wh[j], __builtin_bit_cast(f16x8, av[j][mb]), acc[mb]);
+                } else {
+                    acc[mb] = mfma16x16x32(wv[j], av[j][mb], acc[mb]);
+                    if constexpr (A32) acc[mb] = mfma16x16x32(wv[j], al[j][mb], acc[mb]);
+                }
+            }
         }
     }
 
@@ -206,6 +268,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_smallm_kernel(const GemmArg
             if (g.c_f32) {
                 float* cp = reinterpret_cast<float*>(g.c) + off;
                 *cp = g.accumulate ? *cp + v : v;
+            } else if (g.c_f16) {
+                reinterpret_cast<_Float16*>(g.c)[off] = (_Float16)v;
             } else {
                 reinterpret_cast<uint16_t*>(g.c)[off] = (uint16_t)f32_to_bf16_bits(v);
             }
@@ -251,7 +315,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_smallm_kernel(const GemmArg
 constexpr int kSkMaxSplits = 16;
 
 struct SkArgs {
-    const uint16_t* a;     // [M][lda] bf16
+    const void* a;         // [M][lda] bf16, fp32 or fp16 (ActKind)
     const void* w;         // [N][ldw] bf16 or int8
     float* part;           // [splits][M][N] fp32
     int64_t lda, ldw;
@@ -292,17 +356,24 @@ __device__ __forceinline__ void lds_barrier() {
 // (g4 = lane/16, r = lane%16) of wave w supplies weight rows
 // 16(NB w + nb) + r and activation row 16mb + r, k = 32t + 8g4 .. +7 of MFMA
 // step t; accumulator [nb][mb] holds C^T[16(NB w + nb) + 4g4 + i][16mb + r].
-template <int MB, int KT, int NW, bool W8, int NB>
+// AK (ActKind): fp32 activations are staged in LDS as two bf16 planes (hi,
+// lo) and contracted with two MFMAs per weight fragment; fp16 activations
+// run fp16 MFMAs on weight fragments converted in registers.
+template <int MB, int KT, int NW, bool W8, int NB, int AK>
 __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
+    constexpr bool A32 = AK == kActF32;
+    constexpr bool A16 = AK == kActF16;
     constexpr int kSkThreads = 64 * NW;
     constexpr int kSkRows = 16 * NW * NB;     // weight rows (output columns) per workgroup
     constexpr int MR = 16 * MB;
     constexpr int PITCH = 2 * KT + 16;       // bytes per LDS activation row (+16: bank shift)
-    constexpr int CH = KT / 8;               // 16-byte chunks per activation row
+    constexpr int AB = A32 ? 4 : 2;          // bytes per activation element in memory
+    constexpr int CH = KT * AB / 16;         // 16-byte chunks per activation row
     constexpr int NCH = MR * CH;
     constexpr int PER = (NCH + kSkThreads - 1) / kSkThreads;
     constexpr int STEPS = KT / 32;
-    __shared__ __attribute__((aligned(16))) char lds[MR * PITCH];
+    constexpr int PLANES = A32 ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) char lds[PLANES * MR * PITCH];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -317,14 +388,14 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
     // activation slice first (needed first); rows past M read as zeros
     const int mrows = min(MR, g.M - m0);
     const __amdgpu_buffer_rsrc_t ars =
-        make_rsrc(g.a + (int64_t)m0 * g.lda, (uint32_t)((int64_t)mrows * g.lda * 2));
+        make_rsrc(static_cast<const char*>(g.a) + (int64_t)m0 * g.lda * AB, (uint32_t)((int64_t)mrows * g.lda * AB));
     u32x4 av[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int c = tid + kSkThreads * i;
         const int row = c / CH;
-        const int k = k0 + 8 * (c % CH);
-        const uint32_t off = (c < NCH && k < g.K) ? (uint32_t)((row * g.lda + k) * 2) : 0x80000000u;
+        const int k = k0 + (16 / AB) * (c % CH);
+        const uint32_t off = (c < NCH && k < g.K) ? (uint32_t)((row * g.lda + k) * AB) : 0x80000000u;
         av[i] = buffer_load16(ars, off);
     }
     // every weight fragment of this wave in flight at once; rows past N read 0
@@ -353,8 +424,17 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int c = tid + kSkThreads * i;
-        if (c < NCH)
-            *reinterpret_cast<u32x4*>(lds + (c / CH) * PITCH + (c % CH) * 16) = av[i];
+        if (c < NCH) {
+            if constexpr (A32) {
+                uint2 hi, lo;
+                split_bf16x4(av[i], hi, lo);
+                char* dst = lds + (c / CH) * PITCH + (c % CH) * 8;
+                *reinterpret_cast<uint2*>(dst) = hi;
+                *reinterpret_cast<uint2*>(dst + MR * PITCH) = lo;
+            } else {
+                *reinterpret_cast<u32x4*>(lds + (c / CH) * PITCH + (c % CH) * 16) = av[i];
+            }
+        }
     }
     lds_barrier();
 
@@ -367,17 +447,34 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
     for (int t = 0; t < STEPS; ++t) {
         if (t < nsteps) {
             bf16x8 wf[NB];
+            f16x8 wh[A16 ? NB : 1];
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                if constexpr (W8) wf[nb] = i8x8_to_bf16x8(wq[nb][t]);
-                else wf[nb] = __builtin_bit_cast(bf16x8, wv[nb][t]);
+                if constexpr (A16) {
+                    if constexpr (W8) wh[nb] = i8x8_to_f16x8(wq[nb][t]);
+                    else wh[nb] = bf16x8_to_f16x8(wv[nb][t]);
+                } else {
+                    if constexpr (W8) wf[nb] = i8x8_to_bf16x8(wq[nb][t]);
+                    else wf[nb] = __builtin_bit_cast(bf16x8, wv[nb][t]);
+                }
             }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
-                const bf16x8 af = *reinterpret_cast<const bf16x8*>(
-                    lds + (16 * mb + r) * PITCH + (32 * t + 8 * g4) * 2);
+                const char* ap = lds + (16 * mb + r) * PITCH + (32 * t + 8 * g4) * 2;
+                if constexpr (A16) {
+                    const f16x8 ah = *reinterpret_cast<const f16x8*>(ap);
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb) acc[nb][mb] = mfma16x16x32_f16(wh[nb], ah, acc[nb][mb]);
+                    continue;
+                }
+                const bf16x8 af = *reinterpret_cast<const bf16x8*>(ap);
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) acc[nb][mb] = mfma16x16x32(wf[nb], af, acc[nb][mb]);
+                if constexpr (A32) {
+                    const bf16x8 al = *reinterpret_cast<const bf16x8*>(ap + MR * PITCH);
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb) acc[nb][mb] = mfma16x16x32(wf[nb], al, acc[nb][mb]);
+                }
             }
         }
     }
@@ -407,7 +504,7 @@ struct EpiArgs {
     // plain
     void* c;
     int64_t ldc;
-    int c_f32, accumulate;
+    int c_f32, c_f16, accumulate;
     // per-head
     int H, S;
     float eps;
@@ -418,7 +515,7 @@ struct EpiArgs {
     const float* norm_gamma;
     void* norm_out;
     int64_t norm_ldo;
-    int norm_f32;
+    int norm_f32, norm_f16;
 };
 
 // Sum of the K-slice partials for C[m][n..n+3], slices in ascending order,
@@ -465,6 +562,10 @@ __device__ __forceinline__ uint2 pack_bf16x4(f32x4 v) {
     return uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }
 
+__device__ __forceinline__ uint2 pack_16x4(f32x4 v, bool f16) {
+    return f16 ? uint2{pack_f16x2_rn(v[0], v[1]), pack_f16x2_rn(v[2], v[3])} : pack_bf16x4(v);
+}
+
 // Output tile of a reduce workgroup when N % 64 == 0: 16 rows x the 64
 // columns of one weight tile of the split-K kernel, tile index fastest.  That
 // kernel writes every K slice of weight tile j from XCD j % 8 (workgroup id
@@ -497,7 +598,7 @@ __global__ __launch_bounds__(256) void reduce_plain_kernel(const EpiArgs e) {
         if (e.accumulate) v += *cp;
         *cp = v;
     } else {
-        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.c) + off) = pack_bf16x4(v);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.c) + off) = pack_16x4(v, e.c_f16);
     }
 }
 
@@ -581,7 +682,7 @@ __global__ __launch_bounds__(kAddNormThreads) void reduce_addnorm_kernel(const E
             if (e.norm_f32)
                 *reinterpret_cast<f32x4*>(static_cast<float*>(e.norm_out) + off) = o;
             else
-                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.norm_out) + off) = pack_bf16x4(o);
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.norm_out) + off) = pack_16x4(o, e.norm_f16);
         }
     }
 }
@@ -614,9 +715,11 @@ struct SkPlan {
 // one block) only when 256 would need more than 16 slices or more
 // workgroups than fit on the chip at once for one 80-row tile.  The slicing depends on (N, K) only, never on M, so each
 // row's sums are added in the same order whatever the batch: a row's result
-// does not depend on how many rows share the call.
+// does not depend on how many rows share the call.  fp32 activations (a32)
+// take two bf16 LDS planes: 84 KB for a 256-wide slice (one workgroup per
+// CU), too much for a 512-wide one, so those shapes run single-pass.
 constexpr int kSkResident = 256 * 3;
-inline SkPlan plan_splitk(int M, int N, int K) {
+inline SkPlan plan_splitk(int M, int N, int K, bool a32) {
     SkPlan p;
     if (M <= 0 || M > 160 || N <= 0 || (N & 15) || K <= 0 || (K & 31)) return p;
     p.mb = M <= 80 ? (M + 15) / 16 : 5;
@@ -633,35 +736,41 @@ inline SkPlan plan_splitk(int M, int N, int K) {
         p.splits = (K + 511) / 512;
     }
     if (p.splits > kSkMaxSplits) return SkPlan{};
+    if (a32 && p.kt != 256) return SkPlan{};
     p.split = true;
     p.ws_bytes = (size_t)p.splits * M * N * 4;
     return p;
 }
 
-template <int KT, int NW, bool W8, int NB>
+template <int KT, int NW, bool W8, int NB, int AK>
 void launch_splitk_mb(const SkArgs& a, const SkPlan& p, hipStream_t s) {
     const dim3 grid(p.ntiles, p.splits, p.mtiles), block(64 * NW);
     switch (p.mb) {
-        case 1: hipLaunchKernelGGL((gemm_splitk_kernel<1, KT, NW, W8, NB>), grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL((gemm_splitk_kernel<2, KT, NW, W8, NB>), grid, block, 0, s, a); break;
-        case 3: hipLaunchKernelGGL((gemm_splitk_kernel<3, KT, NW, W8, NB>), grid, block, 0, s, a); break;
-        case 4: hipLaunchKernelGGL((gemm_splitk_kernel<4, KT, NW, W8, NB>), grid, block, 0, s, a); break;
-        default: hipLaunchKernelGGL((gemm_splitk_kernel<5, KT, NW, W8, NB>), grid, block, 0, s, a); break;
+        case 1: hipLaunchKernelGGL((gemm_splitk_kernel<1, KT, NW, W8, NB, AK>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((gemm_splitk_kernel<2, KT, NW, W8, NB, AK>), grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL((gemm_splitk_kernel<3, KT, NW, W8, NB, AK>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((gemm_splitk_kernel<4, KT, NW, W8, NB, AK>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((gemm_splitk_kernel<5, KT, NW, W8, NB, AK>), grid, block, 0, s, a); break;
     }
 }
 
 template <bool W8>
-void launch_splitk_w(const SkArgs& a, const SkPlan& p, hipStream_t s) {
-    if (p.kt == 256) {
-        launch_splitk_mb<256, 2, W8, 2>(a, p, s);
+void launch_splitk_w(const SkArgs& a, const SkPlan& p, int ak, hipStream_t s) {
+    if (ak == kActF32) {
+        launch_splitk_mb<256, 2, W8, 2, kActF32>(a, p, s);   // the plan keeps fp32 at 256-wide slices
+    } else if (ak == kActF16) {
+        if (p.kt == 256) launch_splitk_mb<256, 2, W8, 2, kActF16>(a, p, s);
+        else launch_splitk_mb<512, 4, W8, 1, kActF16>(a, p, s);
+    } else if (p.kt == 256) {
+        launch_splitk_mb<256, 2, W8, 2, kActBF16>(a, p, s);
     } else {
-        launch_splitk_mb<512, 4, W8, 1>(a, p, s);
+        launch_splitk_mb<512, 4, W8, 1, kActBF16>(a, p, s);
     }
 }
 
-inline void launch_splitk(const SkArgs& a, const SkPlan& p, bool w8, hipStream_t s) {
-    if (w8) launch_splitk_w<true>(a, p, s);
-    else launch_splitk_w<false>(a, p, s);
+inline void launch_splitk(const SkArgs& a, const SkPlan& p, bool w8, int ak, hipStream_t s) {
+    if (w8) launch_splitk_w<true>(a, p, ak, s);
+    else launch_splitk_w<false>(a, p, ak, s);
 }
 
 template <int NS>
@@ -678,16 +787,55 @@ void launch_reduce(const sf_gemm_desc* d, const EpiArgs& e, hipStream_t s) {
         hipLaunchKernelGGL(reduce_plain_kernel<NS>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, e);
 }
 
-template <int NR, bool W8>
+template <int NR, bool W8, int AK>
 hipError_t launch_smallm(const GemmArgs& g, int mb, dim3 grid, hipStream_t s) {
     switch (mb) {
-        case 1: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 1, W8>), grid, dim3(kGemmThreads), 0, s, g); break;
-        case 2: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 2, W8>), grid, dim3(kGemmThreads), 0, s, g); break;
-        case 3: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 3, W8>), grid, dim3(kGemmThreads), 0, s, g); break;
-        case 4: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 4, W8>), grid, dim3(kGemmThreads), 0, s, g); break;
-        default: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 5, W8>), grid, dim3(kGemmThreads), 0, s, g); break;
+        case 1: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 1, W8, AK>), grid, dim3(kGemmThreads), 0, s, g); break;
+        case 2: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 2, W8, AK>), grid, dim3(kGemmThreads), 0, s, g); break;
+        case 3: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 3, W8, AK>), grid, dim3(kGemmThreads), 0, s, g); break;
+        case 4: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 4, W8, AK>), grid, dim3(kGemmThreads), 0, s, g); break;
+        default: hipLaunchKernelGGL((gemm_smallm_kernel<NR, 5, W8, AK>), grid, dim3(kGemmThreads), 0, s, g); break;
     }
     return hipGetLastError();
+}
+
+template <int NR, bool W8>
+hipError_t launch_smallm_ak(const GemmArgs& g, int ak, int mb, dim3 grid, hipStream_t s) {
+    if (ak == kActF32) return launch_smallm<NR, W8, kActF32>(g, mb, grid, s);
+    if (ak == kActF16) return launch_smallm<NR, W8, kActF16>(g, mb, grid, s);
+    return launch_smallm<NR, W8, kActBF16>(g, mb, grid, s);
+}
+
+template <int NR>
+hipError_t launch_smallm_any(const GemmArgs& g, bool w8, int ak, int mb, dim3 grid, hipStream_t s) {
+    return w8 ? launch_smallm_ak<NR, true>(g, ak, mb, grid, s) : launch_smallm_ak<NR, false>(g, ak, mb, grid, s);
+}
+
+// fp32 or fp16 activation rows -> bf16 (nearest) [rows][K] for the library path.
+__global__ __launch_bounds__(256) void round_rows_bf16_kernel(const void* __restrict__ a, int a_f16, int64_t lda,
+                                                               uint16_t* __restrict__ out, int rows, int K) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;   // 8 values per thread
+    const int k8 = K / 8;
+    if (idx >= (int64_t)rows * k8) return;
+    const int64_t m = idx / k8;
+    const int k = 8 * (int)(idx % k8);
+    float x[8];
+    if (a_f16) {
+        const f16x8 h = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a) + m * lda + k);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = (float)h[j];
+    } else {
+        const float* ap = static_cast<const float*>(a) + m * lda + k;
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(ap);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(ap + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[j] = x0[j];
+            x[4 + j] = x1[j];
+        }
+    }
+    *reinterpret_cast<u32x4*>(out + m * K + k) =
+        u32x4{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7])};
 }
 
 }  // namespace sfk
@@ -706,16 +854,20 @@ size_t up256(size_t n) { return (n + 255) & ~(size_t)255; }
 struct LibPlan {
     bool ok = false;
     int chunk = 0;
-    size_t c_bytes = 0, w_bytes = 0, total = 0;
+    size_t c_bytes = 0, w_bytes = 0, a_bytes = 0, total = 0;
 };
 
-LibPlan plan_library(int M, int N, int K, bool w8) {
+// Workspace of the library path: the fp32 product of one chunk of rows, the
+// bf16 copy of int8 weights, bf16 rows of an fp32 activation chunk, and
+// hipBLASLt's own scratch.
+LibPlan plan_library(int M, int N, int K, bool w8, bool a_conv) {
     LibPlan p;
     if (M < kLibMinRows || N <= 0 || (N & 15) || K <= 0 || (K & 31)) return p;
     p.chunk = std::min(M, kLibChunkRows);
     p.c_bytes = up256((size_t)p.chunk * N * 4);
     p.w_bytes = w8 ? up256((size_t)N * K * 2) : 0;
-    p.total = p.c_bytes + p.w_bytes + kLibLtBytes;
+    p.a_bytes = a_conv ? up256((size_t)p.chunk * K * 2) : 0;
+    p.total = p.c_bytes + p.w_bytes + p.a_bytes + kLibLtBytes;
     p.ok = true;
     return p;
 }
@@ -816,9 +968,14 @@ int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, hipblasLtHandle_
         constexpr int kCand = 16;
         hipblasLtMatmulHeuristicResult_t res[kCand];
         int nres = 0;
-        ok = ok && hipblasLtMatmulAlgoGetHeuristic(*h, sh.desc, sh.a, sh.b, sh.d, sh.d, pref, tune ? kCand : 1, res,
-                                                   &nres) == HIPBLAS_STATUS_SUCCESS;
-        ok = ok && nres > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= kLibLtBytes;
+        ok = ok && hipblasLtMatmulAlgoGetHeuristic(*h, sh.desc, sh.a, sh.b, sh.d, sh.d, pref, kCand, res, &nres) ==
+                       HIPBLAS_STATUS_SUCCESS;
+        // keep the candidates that ran the heuristic and fit the workspace
+        int nuse = 0;
+        for (int i = 0; ok && i < nres; ++i)
+            if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kLibLtBytes) res[nuse++] = res[i];
+        nres = nuse;
+        ok = ok && nres > 0;
         if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
         int pick = 0;
         if (ok && tune && nres > 1) {
@@ -842,17 +999,22 @@ namespace {
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
+int act_kind(const sf_gemm_desc* d) {
+    return d->a_dtype == SF_F32 ? sfk::kActF32 : (d->a_dtype == SF_F16 ? sfk::kActF16 : sfk::kActBF16);
+}
+
 // Shape / pointer checks shared by both paths; fills the epilogue fields.
 int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
     if (d->K == 0 || (d->K & 31)) return SF_ENOTSUP;
-    if (d->a_dtype != SF_BF16) return SF_ENOTSUP;
+    if (d->a_dtype != SF_BF16 && d->a_dtype != SF_F32 && d->a_dtype != SF_F16) return SF_ENOTSUP;
     if (d->w_dtype != SF_BF16 && d->w_dtype != SF_I8) return SF_ENOTSUP;
     if (d->act < 0 || d->act > 2) return SF_EINVAL;
     if (!d->A || !d->W) return SF_EINVAL;
     if (!al16(d->A) || !al16(d->W) || (d->lda & 7) || d->lda < d->K) return SF_EINVAL;
     if ((d->ldw & 7) || d->ldw < d->K) return SF_EINVAL;
     if (d->w_dtype == SF_I8 && !d->w_scale) return SF_EINVAL;
-    if ((int64_t)std::max(1, std::min(80, d->M)) * d->lda * 2 > 0x7fffffffLL) return SF_ENOTSUP;
+    const int64_t abytes = d->a_dtype == SF_F32 ? 4 : 2;
+    if ((int64_t)std::max(1, std::min(80, d->M)) * d->lda * abytes > 0x7fffffffLL) return SF_ENOTSUP;
     if ((int64_t)std::min(64, d->N) * d->ldw * 2 > 0x7fffffffLL) return SF_ENOTSUP;
     e.M = d->M;
     e.N = d->N;
@@ -878,20 +1040,22 @@ int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
         e.S = d->S;
     } else if (d->epilogue == SF_EPI_PLAIN || d->epilogue == SF_EPI_ADD_NORM) {
         if (!d->C || d->ldc < d->N) return SF_EINVAL;
-        if (d->c_dtype != SF_BF16 && d->c_dtype != SF_F32) return SF_ENOTSUP;
+        if (d->c_dtype != SF_BF16 && d->c_dtype != SF_F32 && d->c_dtype != SF_F16) return SF_ENOTSUP;
         if ((d->accumulate || d->epilogue == SF_EPI_ADD_NORM) && d->c_dtype != SF_F32) return SF_EINVAL;
         e.c = d->C;
         e.ldc = d->ldc;
         e.c_f32 = d->c_dtype == SF_F32;
+        e.c_f16 = d->c_dtype == SF_F16;
         e.accumulate = d->accumulate != 0 || d->epilogue == SF_EPI_ADD_NORM;
         if (d->epilogue == SF_EPI_ADD_NORM) {
             if (!d->norm_gamma || !d->norm_out || d->norm_ldo < d->N) return SF_EINVAL;
-            if (d->norm_dtype != SF_BF16 && d->norm_dtype != SF_F32) return SF_ENOTSUP;
+            if (d->norm_dtype != SF_BF16 && d->norm_dtype != SF_F32 && d->norm_dtype != SF_F16) return SF_ENOTSUP;
             if (d->N > 4096) return SF_ENOTSUP;
             e.norm_gamma = d->norm_gamma;
             e.norm_out = d->norm_out;
             e.norm_ldo = d->norm_ldo;
             e.norm_f32 = d->norm_dtype == SF_F32;
+            e.norm_f16 = d->norm_dtype == SF_F16;
         }
     } else {
         return SF_EINVAL;
@@ -921,7 +1085,7 @@ int gemm_single_pass(const sf_gemm_desc* d, const sfk::EpiArgs& e, hipStream_t s
     const int64_t wbytes = d->w_dtype == SF_I8 ? 1 : 2;
     if ((int64_t)d->N * d->ldw * wbytes > 0x7fffffffLL) return SF_ENOTSUP;
     sfk::GemmArgs g{};
-    g.a = static_cast<const uint16_t*>(d->A);
+    g.a = d->A;
     g.w = d->W;
     g.w_scale = d->w_scale;
     g.bias = d->bias;
@@ -946,17 +1110,17 @@ int gemm_single_pass(const sf_gemm_desc* d, const sfk::EpiArgs& e, hipStream_t s
         g.c = d->C;
         g.ldc = d->ldc;
         g.c_f32 = e.c_f32;
+        g.c_f16 = e.c_f16;
         g.accumulate = e.accumulate;
     }
     const int mtiles = (d->M + 79) / 80;
     const int mb = d->M >= 80 ? 5 : (d->M + 15) / 16;
+    const int ak = act_kind(d);
     hipError_t err;
     if (g.heads) {
-        const dim3 grid(d->N / 64, mtiles);
-        err = w8 ? sfk::launch_smallm<64, true>(g, mb, grid, s) : sfk::launch_smallm<64, false>(g, mb, grid, s);
+        err = sfk::launch_smallm_any<64>(g, w8, ak, mb, dim3(d->N / 64, mtiles), s);
     } else {
-        const dim3 grid((d->N + 15) / 16, mtiles);
-        err = w8 ? sfk::launch_smallm<16, true>(g, mb, grid, s) : sfk::launch_smallm<16, false>(g, mb, grid, s);
+        err = sfk::launch_smallm_any<16>(g, w8, ak, mb, dim3((d->N + 15) / 16, mtiles), s);
     }
     if (err != hipSuccess) return SF_ELAUNCH;
     if (d->epilogue == SF_EPI_ADD_NORM)
@@ -966,26 +1130,38 @@ int gemm_single_pass(const sf_gemm_desc* d, const sfk::EpiArgs& e, hipStream_t s
 }
 }  // namespace
 
+// Leading dimensions hipBLASLt sees on the library path: int8 weights are
+// widened into a [N][K] copy, fp32 activations rounded into [chunk][K].
+int64_t lib_ldw(const sf_gemm_desc* d) { return d->w_dtype == SF_I8 ? d->K : d->ldw; }
+int64_t lib_lda(const sf_gemm_desc* d) { return d->a_dtype != SF_BF16 ? d->K : d->lda; }
+
+// Whether hipBLASLt has an algorithm for every chunk shape of this call (a
+// shape without one runs the single-pass kernel instead).
+bool lib_available(const sf_gemm_desc* d, const LibPlan& lp, bool tune) {
+    hipblasLtHandle_t h;
+    const LtShape* sh = nullptr;
+    for (int rows : {lp.chunk, d->M % lp.chunk}) {
+        if (rows <= 0) continue;
+        if (lt_lookup(d->N, d->K, rows, lib_lda(d), lib_ldw(d), &h, &sh, tune) != SF_OK) return false;
+    }
+    return true;
+}
+
 extern "C" size_t sf_gemm_workspace_bytes(const sf_gemm_desc* d) {
     if (!d) return 0;
-    const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K);
+    const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K, d->a_dtype == SF_F32);
     if (p.split) return p.ws_bytes;
-    const LibPlan lp = plan_library(d->M, d->N, d->K, d->w_dtype == SF_I8);
+    const LibPlan lp = plan_library(d->M, d->N, d->K, d->w_dtype == SF_I8, d->a_dtype != SF_BF16);
     return lp.ok ? lp.total : 0;
 }
 
 extern "C" int sf_gemm_prepare(const sf_gemm_desc* d) {
     if (!d) return SF_EINVAL;
-    const LibPlan lp = plan_library(d->M, d->N, d->K, d->w_dtype == SF_I8);
+    const LibPlan lp = plan_library(d->M, d->N, d->K, d->w_dtype == SF_I8, d->a_dtype != SF_BF16);
     if (!lp.ok) return SF_OK;   // split-K and single-pass paths need no setup
-    const int64_t ldw = d->w_dtype == SF_I8 ? d->K : d->ldw;
-    hipblasLtHandle_t h;
-    const LtShape* sh = nullptr;
-    for (int rows : {lp.chunk, d->M % lp.chunk}) {
-        if (rows <= 0) continue;
-        const int st = lt_lookup(d->N, d->K, rows, d->lda, ldw, &h, &sh, true);
-        if (st != SF_OK) return st;
-    }
+    // a shape hipBLASLt has no algorithm for is served by the single-pass
+    // kernel: not an error
+    (void)lib_available(d, lp, true);
     return SF_OK;
 }
 
@@ -996,16 +1172,20 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     sfk::EpiArgs e{};
     SF_CHECK_OK(validate(d, e));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K);
+    const bool a32 = d->a_dtype == SF_F32;
+    const bool a_conv = d->a_dtype != SF_BF16;   // library path: activations rounded to bf16 first
+    if (a32 && ((d->lda & 3) || !al16(d->A))) return SF_EINVAL;
+    const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K, a32);
     if (d->workspace && !p.split && splittable(d)) {
         const bool w8 = d->w_dtype == SF_I8;
-        const LibPlan lp = plan_library(d->M, d->N, d->K, w8);
-        if (lp.ok) {
+        const LibPlan lp = plan_library(d->M, d->N, d->K, w8, a_conv);
+        if (lp.ok && lib_available(d, lp, false)) {
             if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < lp.total) return SF_EWORKSPACE;
             if (!al16(d->workspace)) return SF_EINVAL;
             char* ws = static_cast<char*>(d->workspace);
             float* cbuf = reinterpret_cast<float*>(ws);
-            void* ltws = ws + lp.c_bytes + lp.w_bytes;
+            uint16_t* abuf = reinterpret_cast<uint16_t*>(ws + lp.c_bytes + lp.w_bytes);
+            void* ltws = ws + lp.c_bytes + lp.w_bytes + lp.a_bytes;
             const void* W = d->W;
             int64_t ldw = d->ldw;
             if (w8) {
@@ -1022,8 +1202,18 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
                 const int rows = std::min(lp.chunk, d->M - m0);
                 hipblasLtHandle_t h;
                 const LtShape* sh = nullptr;
-                SF_CHECK_OK(lt_lookup(d->N, d->K, rows, d->lda, ldw, &h, &sh));
-                const uint16_t* Ac = static_cast<const uint16_t*>(d->A) + (int64_t)m0 * d->lda;
+                SF_CHECK_OK(lt_lookup(d->N, d->K, rows, lib_lda(d), ldw, &h, &sh));
+                const uint16_t* Ac;
+                if (a_conv) {
+                    const int64_t n8 = (int64_t)rows * (d->K / 8);
+                    const char* Ab = static_cast<const char*>(d->A) + (int64_t)m0 * d->lda * (a32 ? 4 : 2);
+                    hipLaunchKernelGGL(sfk::round_rows_bf16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256),
+                                       0, s, static_cast<const void*>(Ab), a32 ? 0 : 1, d->lda, abuf, rows, d->K);
+                    if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
+                    Ac = abuf;
+                } else {
+                    Ac = static_cast<const uint16_t*>(d->A) + (int64_t)m0 * d->lda;
+                }
                 if (hipblasLtMatmul(h, sh->desc, &one, W, sh->a, Ac, sh->b, &zero, cbuf, sh->d, cbuf, sh->d,
                                     &sh->algo, ltws, kLibLtBytes, s) != HIPBLAS_STATUS_SUCCESS)
                     return SF_ELAUNCH;
@@ -1042,13 +1232,13 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < p.ws_bytes) return SF_EWORKSPACE;
     if (!al16(d->workspace)) return SF_EINVAL;
     sfk::SkArgs a{};
-    a.a = static_cast<const uint16_t*>(d->A);
+    a.a = d->A;
     a.w = d->W;
     a.part = static_cast<float*>(d->workspace);
     a.lda = d->lda;
     a.ldw = d->ldw;
     a.M = d->M; a.N = d->N; a.K = d->K;
-    sfk::launch_splitk(a, p, d->w_dtype == SF_I8, s);
+    sfk::launch_splitk(a, p, d->w_dtype == SF_I8, act_kind(d), s);
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     e.part = a.part;
     e.splits = p.splits;

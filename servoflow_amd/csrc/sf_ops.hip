@@ -31,17 +31,21 @@ __device__ __forceinline__ float load_elem(const void* p, int bf16, int64_t i) {
                 : reinterpret_cast<const float*>(p)[i];
 }
 
-__device__ __forceinline__ void store_elem(void* p, int bf16, int64_t i, float v) {
-    if (bf16) reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_bf16_bits(v);
+// kind: 0 fp32, 1 bf16, 2 fp16
+__device__ __forceinline__ void store_elem(void* p, int kind, int64_t i, float v) {
+    if (kind == 1) reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)f32_to_bf16_bits(v);
+    else if (kind == 2) reinterpret_cast<_Float16*>(p)[i] = (_Float16)v;
     else reinterpret_cast<float*>(p)[i] = v;
 }
+
+int out_kind(int32_t dtype) { return dtype == SF_BF16 ? 1 : (dtype == SF_F16 ? 2 : 0); }
 
 // Each thread owns up to kPer columns of its row in registers.
 constexpr int kPer = 16;   // 256 threads x 16 = 4096 columns max per row
 
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
     const void* x, int x_bf16, int64_t ldx, const void* delta, int delta_bf16, float* residual,
-    const float* gamma, void* out, int out_bf16, int64_t ldo, int cols, float eps) {
+    const float* gamma, void* out, int okind, int64_t ldo, int cols, float eps) {
     __shared__ float red[4];
     const int64_t row = blockIdx.x;
     float v[kPer];
@@ -66,7 +70,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int c = threadIdx.x + kNormThreads * j;
-        if (c < cols) store_elem(out, out_bf16, row * ldo + c, v[j] * inv_rms * gamma[c]);
+        if (c < cols) store_elem(out, okind, row * ldo + c, v[j] * inv_rms * gamma[c]);
     }
 }
 
@@ -88,11 +92,11 @@ extern "C" int sf_rmsnorm(const void* x, int32_t x_dtype, int64_t ldx, const flo
     if ((long)rows * cols == 0) return SF_OK;
     if (!x || !gamma || !out || ldx < cols || ldo < cols) return SF_EINVAL;
     if (x_dtype != SF_F32 && x_dtype != SF_BF16) return SF_ENOTSUP;
-    if (out_dtype != SF_F32 && out_dtype != SF_BF16) return SF_ENOTSUP;
+    if (out_dtype != SF_F32 && out_dtype != SF_BF16 && out_dtype != SF_F16) return SF_ENOTSUP;
     if (cols > sfk::kNormThreads * sfk::kPer) return SF_ENOTSUP;
     hipLaunchKernelGGL(sfk::rmsnorm_kernel, dim3(rows), dim3(sfk::kNormThreads), 0,
                        static_cast<hipStream_t>(stream), x, x_dtype == SF_BF16, ldx, nullptr, 0,
-                       nullptr, gamma, out, out_dtype == SF_BF16, ldo, cols, eps);
+                       nullptr, gamma, out, sfk::out_kind(out_dtype), ldo, cols, eps);
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
 }
 
@@ -103,11 +107,11 @@ extern "C" int sf_add_rmsnorm(const void* delta, int32_t delta_dtype, float* res
     if ((long)rows * cols == 0) return SF_OK;
     if (!delta || !residual || !gamma || !out) return SF_EINVAL;
     if (delta_dtype != SF_F32 && delta_dtype != SF_BF16) return SF_ENOTSUP;
-    if (out_dtype != SF_F32 && out_dtype != SF_BF16) return SF_ENOTSUP;
+    if (out_dtype != SF_F32 && out_dtype != SF_BF16 && out_dtype != SF_F16) return SF_ENOTSUP;
     if (cols > sfk::kNormThreads * sfk::kPer) return SF_ENOTSUP;
     hipLaunchKernelGGL(sfk::rmsnorm_kernel, dim3(rows), dim3(sfk::kNormThreads), 0,
                        static_cast<hipStream_t>(stream), nullptr, 0, (int64_t)cols, delta,
-                       delta_dtype == SF_BF16, residual, gamma, out, out_dtype == SF_BF16,
+                       delta_dtype == SF_BF16, residual, gamma, out, sfk::out_kind(out_dtype),
                        (int64_t)cols, cols, eps);
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
 }

@@ -7,6 +7,8 @@
 //   euler_update         slice last T rows + copy + scale(dt) + add
 //                        (rdt1b.cpp:362-368, flow_matching.cpp:77-78)
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <math.h>
 #include <stdint.h>
 
@@ -122,6 +124,34 @@ inline unsigned blocks_for(int64_t n, int per = 256) {
     return (unsigned)(b > 0x7fffffff ? 0x7fffffff : b);
 }
 
+// Largest |x| over n bf16 values, merged into *out (fp32 bits, so the
+// integer maximum of non-negative values is their float maximum; NaN bit
+// patterns order above inf, so a NaN anywhere gives a NaN result).  Eight
+// values (16 bytes) per thread and step; the workgroup's maximum goes out
+// as one atomic (all workgroups target the same word, so there are few).
+__global__ __launch_bounds__(256) void absmax_bf16_kernel(const uint16_t* __restrict__ p, int64_t n,
+                                                          unsigned int* out) {
+    uint32_t m = 0;
+    const int64_t n8 = n / 8;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += stride) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(p + 8 * i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = max(m, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
+    }
+    for (int64_t i = 8 * n8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        m = max(m, (uint32_t)(p[i] & 0x7fffu));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+    __shared__ uint32_t wm[4];
+    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = max(max(wm[0], wm[1]), max(wm[2], wm[3]));
+        if (m) atomicMax(out, m << 16);
+    }
+}
+
 }  // namespace sfk
 
 using sfk::blocks_for;
@@ -195,5 +225,16 @@ extern "C" int sf_euler_update(float* x, const float* v, int32_t B, int32_t T, i
     if (!n) return SF_OK;
     hipLaunchKernelGGL(sfk::euler_update_kernel, dim3(blocks_for(n)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, v, B, T, A, S, dt);
+    return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+}
+
+extern "C" int sf_absmax_bf16(const void* p, int64_t n, float* out, void* stream) {
+    if (!p || !out || n < 0) return SF_EINVAL;
+    if (reinterpret_cast<uintptr_t>(p) & 15) return SF_EINVAL;
+    if (!n) return SF_OK;
+    const int64_t want = (n / 8 + 255) / 256;
+    const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 256));
+    hipLaunchKernelGGL(sfk::absmax_bf16_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(p), n, reinterpret_cast<unsigned int*>(out));
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
 }

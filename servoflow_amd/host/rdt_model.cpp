@@ -90,10 +90,17 @@ struct sf_rdt {
 
     // activations (batch B, sequence S = horizon + 3)
     float* x = nullptr;            // [B*S, D] fp32 residual stream
-    uint16_t* n = nullptr;         // [B*S, D] bf16 normed activations
+    uint16_t* n = nullptr;         // [B*S, D] bf16 norm1 / norm2 / final-norm output
     uint16_t *q = nullptr, *k = nullptr, *v = nullptr;   // [B, H, S, 64]
-    uint16_t* a = nullptr;         // [B*S, D] attention output
-    uint16_t* h = nullptr;         // [B*S, D] FFN hidden
+    uint16_t* a = nullptr;         // [B*S, D] bf16 attention output
+    // The FFN's inputs (norm3 output, GELU hidden) in ffn_dtype: fp16 while
+    // B*S rows fit the split-K regime (3 more significant bits than bf16 at
+    // the same bytes; the fc1 / fc2 weight fragments are converted to fp16
+    // in registers), bf16 above it.  Of the block's bf16 storage points these
+    // two move the block output furthest from fp32 arithmetic.
+    int32_t ffn_dtype = SF_BF16;
+    void* n3 = nullptr;            // [B*S, D] norm3 output
+    void* h = nullptr;             // [B*S, F] FFN hidden
     uint16_t* act_in = nullptr;    // [B*T, 2A]
     uint16_t *sa0 = nullptr, *sa1 = nullptr;   // [B*T, D]
     float* act_out = nullptr;      // [B*T, D]
@@ -117,6 +124,18 @@ struct sf_rdt {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     hipStream_t graph_stream = nullptr;
+
+    // P.V form of each block's cross-attention.  The fast fp16 form holds a
+    // cached V element only below 65504 in magnitude; sf_rdt_set_condition
+    // measures each layer's max |V| on the device, and before the next step
+    // (or graph capture) the host reads it once and runs a layer whose V
+    // would overflow (or holds NaN/inf) in the exact bf16 form.
+    float* v_absmax = nullptr;        // [layers] device
+    float* v_absmax_host = nullptr;   // [layers] pinned host copy
+    hipEvent_t cond_event = nullptr;  // recorded after the copy
+    uint64_t cond_gen = 0;            // conditions set so far
+    uint64_t forms_gen = 0;           // condition the forms were chosen for
+    std::vector<uint8_t> exact_pv;    // [layers]
 
     // sf_rdt_infer's condition cache: the frame id the cached condition was
     // encoded for, valid until another condition or new weights replace it
@@ -236,7 +255,7 @@ void build_param_table(sf_rdt* m) {
 const float* pf(sf_rdt* m, int idx) { return static_cast<const float*>(m->params[idx].data); }
 
 int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, int act, void* C,
-           int64_t ldc, int c_dtype, bool accumulate, hipStream_t s) {
+           int64_t ldc, int c_dtype, bool accumulate, hipStream_t s, int a_dtype = SF_BF16) {
     const Param& W = m->params[w_idx];
     sf_gemm_desc d{};
     d.M = M;
@@ -244,7 +263,7 @@ int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, i
     d.K = (int32_t)W.shape[1];
     d.A = A;
     d.lda = lda;
-    d.a_dtype = SF_BF16;
+    d.a_dtype = a_dtype;
     d.W = W.data;
     d.ldw = W.shape[1];
     d.w_dtype = W.dtype;
@@ -261,9 +280,10 @@ int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, i
     return sf_gemm(&d, s);
 }
 
-// x += A W^T + b (fp32 residual m->x), then m->n = rmsnorm(x) * gamma (bf16).
-int linear_add_norm(sf_rdt* m, const void* A, int M, int w_idx, int b_idx, int gamma_idx,
-                    hipStream_t s) {
+// x += A W^T + b (fp32 residual m->x, A in a_dtype), then
+// out = rmsnorm(x) * gamma in out_dtype.
+int linear_add_norm(sf_rdt* m, const void* A, int a_dtype, int M, int w_idx, int b_idx, int gamma_idx,
+                    void* out, int out_dtype, hipStream_t s) {
     const Param& W = m->params[w_idx];
     const int D = m->cfg.hidden;
     sf_gemm_desc d{};
@@ -272,7 +292,7 @@ int linear_add_norm(sf_rdt* m, const void* A, int M, int w_idx, int b_idx, int g
     d.K = (int32_t)W.shape[1];
     d.A = A;
     d.lda = W.shape[1];
-    d.a_dtype = SF_BF16;
+    d.a_dtype = a_dtype;
     d.W = W.data;
     d.ldw = W.shape[1];
     d.w_dtype = W.dtype;
@@ -284,9 +304,9 @@ int linear_add_norm(sf_rdt* m, const void* A, int M, int w_idx, int b_idx, int g
     d.c_dtype = SF_F32;
     d.eps = m->cfg.eps;
     d.norm_gamma = pf(m, gamma_idx);
-    d.norm_out = m->n;
+    d.norm_out = out;
     d.norm_ldo = D;
-    d.norm_dtype = SF_BF16;
+    d.norm_dtype = out_dtype;
     d.workspace = m->gemm_ws;
     d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
     return sf_gemm(&d, s);
@@ -294,7 +314,8 @@ int linear_add_norm(sf_rdt* m, const void* A, int M, int w_idx, int b_idx, int g
 
 // Per-head projection: sections of H*64 columns -> [B, H, S, 64] bf16.
 int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
-                 uint16_t* const* outs, const int* gamma_idx, int nsec, hipStream_t s) {
+                 uint16_t* const* outs, const int* gamma_idx, int nsec, hipStream_t s,
+                 int a_dtype = SF_BF16) {
     const Param& W = m->params[w_idx];
     const int H = m->cfg.heads;
     sf_gemm_desc d{};
@@ -303,7 +324,7 @@ int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
     d.K = (int32_t)W.shape[1];
     d.A = A;
     d.lda = W.shape[1];
-    d.a_dtype = SF_BF16;
+    d.a_dtype = a_dtype;
     d.W = W.data;
     d.ldw = W.shape[1];
     d.w_dtype = W.dtype;
@@ -326,12 +347,13 @@ int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
 }
 
 int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v, int Sk,
-              const int32_t* valid_len, uint16_t* out, hipStream_t s) {
+              const int32_t* valid_len, void* out, bool exact_pv, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const int S = c.horizon + 3;
     sf_attn_desc d;
     sf_attn_desc_init_bhsd(&d, c.batch, c.heads, S, Sk, 64, SF_BF16, SF_BF16);
     d.kv_valid_len = valid_len;
+    d.exact_pv = exact_pv ? 1 : 0;
     // output straight into [B, S, H*64] (head_to_seq fused away)
     d.o_stride[0] = (int64_t)S * c.hidden;
     d.o_stride[1] = 64;
@@ -351,15 +373,19 @@ size_t gemm_ws_for(const sf_rdt* m, bool prepare, int* status) {
     for (const Param& p : m->params) {
         if (p.shape.size() != 2 || p.dtype == SF_F32) continue;
         for (int M : rows) {
-            sf_gemm_desc d{};
-            d.M = M;
-            d.N = (int32_t)p.shape[0];
-            d.K = (int32_t)p.shape[1];
-            d.lda = d.K;
-            d.ldw = d.K;
-            d.w_dtype = p.dtype;
-            best = std::max(best, sf_gemm_workspace_bytes(&d));
-            if (prepare && status && *status == SF_OK) *status = sf_gemm_prepare(&d);
+            for (int ad : {SF_BF16, SF_F16}) {
+                if (ad == SF_F16 && ad != m->ffn_dtype) continue;
+                sf_gemm_desc d{};
+                d.M = M;
+                d.N = (int32_t)p.shape[0];
+                d.K = (int32_t)p.shape[1];
+                d.lda = d.K;
+                d.a_dtype = ad;
+                d.ldw = d.K;
+                d.w_dtype = p.dtype;
+                best = std::max(best, sf_gemm_workspace_bytes(&d));
+                if (prepare && status && *status == SF_OK) *status = sf_gemm_prepare(&d);
+            }
         }
     }
     return best;
@@ -396,12 +422,13 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const LayerIdx& L = m->layers[i];
     const int D = c.hidden, S = c.horizon + 3, M = c.batch * S;
+    const int fd = m->ffn_dtype;
     // self-attention branch
     uint16_t* qkv[3] = {m->q, m->k, m->v};
     const int qk_g[3] = {L.q_norm, L.k_norm, -1};
     SF_TRY(linear_heads(m, m->n, M, S, L.qkv_w, L.qkv_b, qkv, qk_g, 3, s));
-    SF_TRY(attention(m, m->q, m->k, m->v, S, nullptr, m->a, s));
-    SF_TRY(linear_add_norm(m, m->a, M, L.proj_w, L.proj_b, L.norm2, s));
+    SF_TRY(attention(m, m->q, m->k, m->v, S, nullptr, m->a, false, s));
+    SF_TRY(linear_add_norm(m, m->a, SF_BF16, M, L.proj_w, L.proj_b, L.norm2, m->n, SF_BF16, s));
     // cross-attention branch: even blocks attend to language, odd to image
     // (dit_block.cu:369)
     uint16_t* cq[1] = {m->q};
@@ -409,12 +436,13 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s));
     const bool lang = (i % 2) == 0;
     SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? c.lang_max : c.img_len,
-                     lang ? m->lang_len : nullptr, m->a, s));
-    SF_TRY(linear_add_norm(m, m->a, M, L.cproj_w, L.cproj_b, L.norm3, s));
-    // FFN branch (Mlp::forward, dit_block.cu:143-163)
+                     lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s));
+    SF_TRY(linear_add_norm(m, m->a, SF_BF16, M, L.cproj_w, L.cproj_b, L.norm3, m->n3, fd, s));
+    // FFN branch (Mlp::forward, dit_block.cu:143-163); fc2's add + norm
+    // writes the next block's norm1 (bf16, the QKV input)
     const int F = (int)ffn_dim(c);
-    SF_TRY(linear(m, m->n, D, M, L.fc1_w, L.fc1_b, SF_ACT_GELU_TANH, m->h, F, SF_BF16, false, s));
-    return linear_add_norm(m, m->h, M, L.fc2_w, L.fc2_b, next_norm(m, i), s);
+    SF_TRY(linear(m, m->n3, D, M, L.fc1_w, L.fc1_b, SF_ACT_GELU_TANH, m->h, F, fd, false, s, fd));
+    return linear_add_norm(m, m->h, fd, M, L.fc2_w, L.fc2_b, next_norm(m, i), m->n, SF_BF16, s);
 }
 
 // m->n = first norm applied to the residual m->x before block `first`.
@@ -446,8 +474,9 @@ int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s) {
     SF_TRY(entry_norm(m, 0, s));
     for (int i = 0; i < c.layers; ++i) SF_TRY(block_forward(m, i, s));
     // FinalLayer (dit_block.cu:407-412); m->n = norm_final(x) from the last block
-    SF_TRY(linear(m, m->n, D, M, m->f1w, m->f1b, SF_ACT_GELU_TANH, m->h, D, SF_BF16, false, s));
-    return linear(m, m->h, D, M, m->f2w, m->f2b, SF_ACT_NONE, m->vel_rows, A, SF_F32, false, s);
+    SF_TRY(linear(m, m->n, D, M, m->f1w, m->f1b, SF_ACT_GELU_TANH, m->h, D, m->ffn_dtype, false, s));
+    return linear(m, m->h, D, M, m->f2w, m->f2b, SF_ACT_NONE, m->vel_rows, A, SF_F32, false, s,
+                  m->ffn_dtype);
 }
 
 std::vector<float> schedule(int num_steps) {
@@ -478,6 +507,23 @@ void release_graph(sf_rdt* m) {
     m->graph_exec = nullptr;
     m->graph = nullptr;
     m->graph_stream = nullptr;
+}
+
+// Chooses each layer's P.V form for the condition set last (waits for its
+// max |V| once per condition; never under capture).  A change of forms
+// invalidates the captured loop.
+int resolve_pv_forms(sf_rdt* m) {
+    if (m->forms_gen == m->cond_gen) return SF_OK;
+    SF_HIP(hipEventSynchronize(m->cond_event));
+    bool changed = false;
+    for (int i = 0; i < m->cfg.layers; ++i) {
+        const uint8_t exact = m->v_absmax_host[i] < 65504.f ? 0 : 1;   // NaN compares false
+        changed |= exact != m->exact_pv[i];
+        m->exact_pv[i] = exact;
+    }
+    if (changed) release_graph(m);
+    m->forms_gen = m->cond_gen;
+    return SF_OK;
 }
 
 hipStream_t pick_stream(sf_rdt* m, void* stream) {
@@ -524,6 +570,8 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
         return SF_ENOTSUP;   // GEMM K dims are multiples of 32
     sf_rdt* m = new sf_rdt();
     m->cfg = c;
+    // fp16 FFN inputs while the block GEMMs run split-K (M <= 160 rows)
+    m->ffn_dtype = c.batch * (c.horizon + 3) <= 160 ? SF_F16 : SF_BF16;
     build_param_table(m);
 
     const int64_t B = c.batch, D = c.hidden, T = c.horizon, S = T + 3, A = c.action_dim;
@@ -549,6 +597,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
         {(void**)&m->k, (size_t)(B * H * S * 64 * 2)},
         {(void**)&m->v, (size_t)(B * H * S * 64 * 2)},
         {(void**)&m->a, (size_t)(B * S * D * 2)},
+        {(void**)&m->n3, (size_t)(B * S * D * 2)},
         {(void**)&m->h, (size_t)(B * S * ffn_dim(c) * 2)},
         {(void**)&m->act_in, (size_t)(B * T * 2 * A * 2)},
         {(void**)&m->sa0, (size_t)(B * T * D * 2)},
@@ -563,6 +612,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
         {(void**)&m->x_state, (size_t)(B * T * A * 4)},
         {(void**)&m->x_infer, (size_t)(B * T * A * 4)},
         {(void**)&m->lang_len, (size_t)(B * 4)},
+        {(void**)&m->v_absmax, (size_t)std::max(c.layers, 1) * 4},
         {(void**)&m->lang_c, (size_t)(B * c.lang_max * D * 2)},
         {(void**)&m->img_c, (size_t)(B * c.img_len * D * 2)},
         {(void**)&m->ad_h, (size_t)(adapt_rows * D * 2)},
@@ -592,9 +642,15 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
         if (p.dtype == SF_I8) p.scale = reinterpret_cast<float*>(m->arena + p.scale_offset);
     }
     for (size_t i = 0; i < bufs.size(); ++i) *bufs[i].ptr = m->arena + boff[i];
+    m->exact_pv.assign(c.layers, 0);
     if (hipStreamCreate(&m->own_stream) != hipSuccess) {
         (void)hipFree(m->arena);
         delete m;
+        return SF_EDEVICE;
+    }
+    if (hipEventCreateWithFlags(&m->cond_event, hipEventDisableTiming) != hipSuccess ||
+        hipHostMalloc((void**)&m->v_absmax_host, (size_t)std::max(c.layers, 1) * 4) != hipSuccess) {
+        sf_rdt_destroy(m);
         return SF_EDEVICE;
     }
     // sincos table, built in float as TimestepEmbedding::build_sincos_table
@@ -634,6 +690,8 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
 extern "C" void sf_rdt_destroy(sf_rdt* m) {
     if (!m) return;
     release_graph(m);
+    if (m->cond_event) (void)hipEventDestroy(m->cond_event);
+    if (m->v_absmax_host) (void)hipHostFree(m->v_absmax_host);
     if (m->own_stream) (void)hipStreamDestroy(m->own_stream);
     if (m->arena) (void)hipFree(m->arena);
     delete m;
@@ -718,6 +776,17 @@ extern "C" int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t
         SF_TRY(linear_heads(m, lang ? m->lang_c : m->img_c, B * Sc, Sc, m->layers[i].ckv_w,
                             m->layers[i].ckv_b, kv, g, 2, s));
     }
+    // each layer's max |V| for the choice of P.V form (resolve_pv_forms)
+    if (c.layers > 0) {
+        SF_TRY(sf_fill_f32(m->v_absmax, c.layers, 0.f, s));
+        for (int i = 0; i < c.layers; ++i) {
+            const int64_t Sc = (i % 2 == 0) ? c.lang_max : c.img_len;
+            SF_TRY(sf_absmax_bf16(m->cv[i], (int64_t)B * c.heads * Sc * 64, m->v_absmax + i, s));
+        }
+        SF_HIP(hipMemcpyAsync(m->v_absmax_host, m->v_absmax, (size_t)c.layers * 4, hipMemcpyDeviceToHost, s));
+        SF_HIP(hipEventRecord(m->cond_event, s));
+        ++m->cond_gen;
+    }
     // the control-frequency token is constant: embed it once (rdt1b.cpp:316)
     return timestep_embed(m, m->fe, c.ctrl_freq, m->f_emb, s);
 }
@@ -757,6 +826,7 @@ extern "C" int sf_rdt_run_blocks(sf_rdt* m, float* x, int32_t first, int32_t cou
     if (!m || !x || first < 0 || count < 0 || first + count > m->cfg.layers) return SF_EINVAL;
     const sf_rdt_config& c = m->cfg;
     hipStream_t s = pick_stream(m, stream);
+    SF_TRY(resolve_pv_forms(m));
     const size_t nbytes = (size_t)c.batch * (c.horizon + 3) * c.hidden * 4;
     SF_HIP(hipMemcpyAsync(m->x, x, nbytes, hipMemcpyDeviceToDevice, s));
     SF_TRY(entry_norm(m, first, s));
@@ -770,6 +840,7 @@ extern "C" int sf_rdt_denoise_step(sf_rdt* m, const float* x_t, float t, float* 
     if (!m || !x_t || !velocity) return SF_EINVAL;
     const sf_rdt_config& c = m->cfg;
     hipStream_t s = pick_stream(m, stream);
+    SF_TRY(resolve_pv_forms(m));
     SF_TRY(step_forward(m, x_t, t, s));
     // last T token rows of each batch element (rdt1b.cpp:362-368)
     SF_HIP(hipMemcpy2DAsync(velocity, (size_t)c.horizon * c.action_dim * 4,
@@ -782,6 +853,7 @@ extern "C" int sf_rdt_sample(sf_rdt* m, float* x, int32_t use_graph, void* strea
     if (!m || !x) return SF_EINVAL;
     const sf_rdt_config& c = m->cfg;
     hipStream_t s = pick_stream(m, stream);
+    SF_TRY(resolve_pv_forms(m));
     const size_t nbytes = (size_t)c.batch * c.horizon * c.action_dim * 4;
     // the initial noise is copied in outside the graph (flow_matching.cpp:49-51)
     SF_HIP(hipMemcpyAsync(m->x_state, x, nbytes, hipMemcpyDeviceToDevice, s));
@@ -839,4 +911,10 @@ extern "C" int sf_rdt_infer(sf_rdt* m, uint64_t frame_id, const void* lang_token
     SF_HIP(hipMemcpyAsync(action_out, m->x_infer, (size_t)n * 4, hipMemcpyDeviceToHost, s));
     SF_HIP(hipStreamSynchronize(s));
     return SF_OK;
+}
+
+extern "C" int32_t sf_rdt_pv_exact(sf_rdt* m, int32_t layer) {
+    if (!m || layer < 0 || layer >= m->cfg.layers) return -1;
+    if (resolve_pv_forms(m) != SF_OK) return -1;
+    return m->exact_pv[layer];
 }

@@ -9,7 +9,7 @@ import torch
 
 from . import abi
 
-_DT = {torch.bfloat16: abi.SF_BF16, torch.float32: abi.SF_F32, torch.int8: abi.SF_I8}
+_DT = {torch.bfloat16: abi.SF_BF16, torch.float32: abi.SF_F32, torch.float16: abi.SF_F16, torch.int8: abi.SF_I8}
 
 
 def _stream(t):

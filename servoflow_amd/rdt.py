@@ -63,6 +63,8 @@ def lib():
     L.sf_rdt_find_param.restype = i32
     L.sf_rdt_cache_ptr.argtypes = [vp, i32, i32]
     L.sf_rdt_cache_ptr.restype = vp
+    L.sf_rdt_pv_exact.argtypes = [vp, i32]
+    L.sf_rdt_pv_exact.restype = i32
     L.sf_rdt_set_condition.argtypes = [vp, vp, vp, vp, vp, vp]
     L.sf_rdt_encode_condition.argtypes = [vp, vp, vp, vp, vp, vp]
     L.sf_rdt_denoise_step.argtypes = [vp, vp, ctypes.c_float, vp, vp]
@@ -101,15 +103,19 @@ def inspect_safetensors(path):
 _hip = None
 
 
-def _memcpy_d2h(dst_np, src_ptr):
+def _hipmemcpy(dst, src, nbytes, kind):
     global _hip
     if _hip is None:
         _hip = ctypes.CDLL("libamdhip64.so")
         _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
     torch.cuda.synchronize()
-    st = _hip.hipMemcpy(dst_np.ctypes.data, src_ptr, dst_np.nbytes, 2)   # DeviceToHost
+    st = _hip.hipMemcpy(dst, src, nbytes, kind)
     if st != 0:
         raise RuntimeError(f"hipMemcpy failed ({st})")
+
+
+def _memcpy_d2h(dst_np, src_ptr):
+    _hipmemcpy(dst_np.ctypes.data, src_ptr, dst_np.nbytes, 2)   # DeviceToHost
     return dst_np
 
 
@@ -180,6 +186,23 @@ class RdtModel:
         if st != abi.SF_OK:
             raise abi.SfError(st, "sf_rdt_load_safetensors: " + lib().sf_rdt_last_error(self.h).decode())
         return n.value
+
+    def param_write(self, idx, values, offset=0):
+        """Writes `values` (numpy, the parameter's element type) into parameter
+        idx starting at element `offset` (host -> device copy)."""
+        _, dt, shape = self.params()[idx]
+        esize = {abi.SF_F32: 4, abi.SF_BF16: 2, abi.SF_I8: 1}[dt]
+        v = np.ascontiguousarray(values)
+        assert v.itemsize == esize and offset + v.size <= int(np.prod(shape))
+        _hipmemcpy(lib().sf_rdt_param_data(self.h, idx) + offset * esize, v.ctypes.data, v.nbytes, 1)
+
+    def pv_exact(self, layer):
+        """sf_rdt_pv_exact: 1 when block `layer`'s cross-attention runs the
+        exact bf16 P.V form for the current condition, 0 for the fp16 form."""
+        r = lib().sf_rdt_pv_exact(self.h, layer)
+        if r < 0:
+            raise abi.SfError(abi.SF_EINVAL, "sf_rdt_pv_exact")
+        return r
 
     def state_dict(self):
         return {nm: self.param_numpy(i, dt, sh) for i, (nm, dt, sh) in enumerate(self.params())}

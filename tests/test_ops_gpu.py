@@ -294,3 +294,124 @@ def test_gemm_library_heads_and_add_norm():
     x_ref = x + O.linear(a2, w2, b2)
     close(host(xd), x_ref, "residual (library)", rel=1e-5)
     close(host(n), O.rms_norm(x_ref, g2), "norm (library)", rel=1e-4)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(67, 2048, 2048), (1, 2048, 256), (80, 6144, 2048), (160, 96, 2080),
+                                    (67, 2048, 8192), (134, 2048, 2048)])
+@pytest.mark.parametrize("ws", PATHS)
+def test_gemm_fp32_activations(M, N, Kd, ws):
+    """fp32 activations (a_dtype SF_F32), carried as bf16 (hi, lo) pairs with
+    two MFMAs per product on the split-K and single-pass paths (K = 8192
+    takes the single-pass kernel even with a workspace: two planes of a
+    512-wide slice exceed the LDS): against the fp32 oracle on the
+    unrounded activations, mean-rel <= 2e-5 (hi + lo keeps ~16 significant
+    bits), several times closer than a bf16-rounded activation gets."""
+    a = O.randn(101 + M, (M, Kd))
+    w = rounded(102 + N, (N, Kd), 0.02)
+    b = O.randn(103, (N,), 0.02)
+    got = host(K.gemm(dev(a, torch.float32), dev(w), dev(b, torch.float32), abi.SF_ACT_GELU_TANH,
+                      out_dtype=torch.float32, workspace=ws))
+    ref = O.linear(a, w, b, act=abi.SF_ACT_GELU_TANH)
+    close(got, ref, f"fp32-activation gemm {M}x{N}x{Kd} ws={ws}", rel=2e-5)
+    rounded_err = mean_rel(O.linear(O.bf16_round(a), w, b, act=abi.SF_ACT_GELU_TANH), ref)
+    assert mean_rel(got, ref) * 8 < rounded_err
+
+
+@pytest.mark.parametrize("w8", [False, True])
+def test_gemm_fp32_activations_library_path(w8):
+    """M > 160: fp32 activations are rounded to bf16 (nearest) for the
+    library product, so the result is the bf16-activation GEMM's."""
+    M, N, Kd = 1072, 2048, 2048
+    a = O.randn(111, (M, Kd))
+    b = O.randn(113, (N,), 0.02)
+    if w8:
+        q, s = O.quantize_int8_rows(O.randn(112, (N, Kd), 0.02))
+        w, wdev, sdev = O.dequant_int8(q, s), dev(q, torch.int8), dev(s, torch.float32)
+    else:
+        w = rounded(112, (N, Kd), 0.02)
+        wdev, sdev = dev(w), None
+    got = host(K.gemm(dev(a, torch.float32), wdev, dev(b, torch.float32), out_dtype=torch.float32, w_scale=sdev))
+    close(got, O.linear(O.bf16_round(a), w, b), f"fp32-activation library gemm w8={w8}")
+
+
+def test_gemm_fp32_activations_add_norm_and_heads():
+    """The epilogues with fp32 activations on the split-K path: residual add
+    + RMSNorm (proj / cross-proj / fc2) and the per-head scatter with q_norm
+    (cross-q)."""
+    M, H, S = 67, 32, 67
+    a = O.randn(121, (M, 2048))
+    w = rounded(122, (2048, 2048), 0.02)
+    b, g = O.randn(123, (2048,), 0.02), 1.0 + O.randn(124, (2048,), 0.1)
+    x = O.randn(125, (M, 2048))
+    xd = dev(x, torch.float32)
+    n = K.gemm_add_norm(dev(a, torch.float32), dev(w), dev(b, torch.float32), xd, dev(g, torch.float32),
+                        norm_dtype=torch.float32)
+    x_ref = x + O.linear(a, w, b)
+    close(host(xd), x_ref, "residual, fp32 activations", rel=1e-5)
+    close(host(n), O.rms_norm(x_ref, g), "norm, fp32 activations", rel=1e-5)
+    gq = 1.0 + O.randn(126, (64,), 0.1)
+    out = torch.empty(1, H, S, 64, device=DEV, dtype=torch.bfloat16)
+    K.gemm_heads(dev(a, torch.float32), dev(w), dev(b, torch.float32), S, H, [out], (dev(gq, torch.float32),))
+    ref = O.rms_norm(O.seq_to_head(O.linear(a, w, b).reshape(1, S, 2048), H, 64), gq)
+    gh = host(out)
+    assert np.all(np.abs(gh - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6)   # one bf16 ulp
+    assert mean_rel(gh, ref) < 3e-3
+
+
+def f16r(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(67, 2048, 2048), (1, 2048, 256), (80, 6144, 2048), (160, 96, 2080),
+                                    (67, 2048, 8192)])
+@pytest.mark.parametrize("ws", PATHS)
+@pytest.mark.parametrize("w8", [False, True])
+def test_gemm_fp16_activations(M, N, Kd, ws, w8):
+    """fp16 activations (a_dtype SF_F16, the runtime's FFN inputs at batch
+    <= 2): fp16 MFMAs with the bf16 weight fragments (or int8 codes)
+    converted to fp16 in registers -- exact for bf16 weights in fp16's
+    normal range (smaller ones to within 2^-25), so against the oracle on
+    the same fp16-rounded activations only the summation order differs."""
+    a = f16r(O.randn(131 + M, (M, Kd)))
+    b = O.randn(133, (N,), 0.02)
+    if w8:
+        q, s = O.quantize_int8_rows(O.randn(132, (N, Kd), 0.02))
+        w, wdev, sdev = O.dequant_int8(q, s), dev(q, torch.int8), dev(s, torch.float32)
+    else:
+        w = rounded(132 + N, (N, Kd), 0.02)
+        wdev, sdev = dev(w), None
+    got = host(K.gemm(dev(a, torch.float16), wdev, dev(b, torch.float32), abi.SF_ACT_GELU_TANH,
+                      out_dtype=torch.float32, w_scale=sdev, workspace=ws))
+    close(got, O.linear(a, w, b, act=abi.SF_ACT_GELU_TANH), f"fp16-activation gemm {M}x{N}x{Kd} w8={w8}",
+          rel=1e-5)
+
+
+@pytest.mark.parametrize("ws", PATHS)
+def test_gemm_fp16_outputs(ws):
+    """fp16 C (the FFN hidden) and fp16 norm output (norm3): the fp32
+    result rounded to nearest."""
+    M, N, Kd = 67, 2048, 2048
+    a, w = rounded(141, (M, Kd)), rounded(142, (N, Kd), 0.02)
+    b, g = O.randn(143, (N,), 0.02), 1.0 + O.randn(144, (N,), 0.1)
+    c16 = host(K.gemm(dev(a), dev(w), dev(b, torch.float32), abi.SF_ACT_GELU_TANH, out_dtype=torch.float16,
+                      workspace=ws))
+    c32 = host(K.gemm(dev(a), dev(w), dev(b, torch.float32), abi.SF_ACT_GELU_TANH, out_dtype=torch.float32,
+                      workspace=ws))
+    assert np.all(np.abs(c16 - f16r(c32)) <= np.abs(c32) * 2.0 ** -10 + 2.0 ** -24)
+    x = O.randn(145, (M, N))
+    x1, x2 = dev(x, torch.float32), dev(x, torch.float32)
+    n16 = host(K.gemm_add_norm(dev(a), dev(w), dev(b, torch.float32), x1, dev(g, torch.float32),
+                               norm_dtype=torch.float16, workspace=ws))
+    n32 = host(K.gemm_add_norm(dev(a), dev(w), dev(b, torch.float32), x2, dev(g, torch.float32),
+                               norm_dtype=torch.float32, workspace=ws))
+    assert np.array_equal(host(x1), host(x2))
+    assert np.all(np.abs(n16 - f16r(n32)) <= np.abs(n32) * 2.0 ** -10 + 2.0 ** -24)
+
+
+def test_gemm_fp16_activations_library_path():
+    """M > 160: fp16 activations are rounded to bf16 for the library product."""
+    M, N, Kd = 1072, 2048, 2048
+    a = f16r(O.randn(151, (M, Kd)))
+    w, b = rounded(152, (N, Kd), 0.02), O.randn(153, (N,), 0.02)
+    got = host(K.gemm(dev(a, torch.float16), dev(w), dev(b, torch.float32), out_dtype=torch.float32))
+    close(got, O.linear(O.bf16_round(a), w, b), "fp16-activation library gemm")
