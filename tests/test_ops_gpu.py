@@ -354,7 +354,11 @@ def test_gemm_fp32_activations_add_norm_and_heads():
     K.gemm_heads(dev(a, torch.float32), dev(w), dev(b, torch.float32), S, H, [out], (dev(gq, torch.float32),))
     ref = O.rms_norm(O.seq_to_head(O.linear(a, w, b).reshape(1, S, 2048), H, 64), gq)
     gh = host(out)
-    assert np.all(np.abs(gh - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6)   # one bf16 ulp
+    # one bf16 ulp of the output plus the (hi, lo) split's product error: the
+    # activations carry ~16 significant bits, an absolute error of ~2^-16 of
+    # the unit-RMS normed row (measured worst case 5e-6 at a 1.4e-5 output);
+    # bf16 activations meet the bare one-ulp bound (same epilogue).
+    assert np.all(np.abs(gh - ref) <= np.abs(ref) * 2.0 ** -7 + 2.0 ** -15)
     assert mean_rel(gh, ref) < 3e-3
 
 
