@@ -43,12 +43,12 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 # HBM bytes per roofline op measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (x2.0 / x1.0, scales read off a 256 MiB copy kernel) on `bench.py
-# --profile-roofline`: ring kernel 17835.5 KiB fetched (36.53 MB read) +
-# 3870.0 KiB written, merge 1972.5 KiB fetched + 268.0 KiB written
+# --profile-roofline`: ring kernel 18639.0 KiB fetched (38.17 MB read) +
+# 3874.5 KiB written, merge 2179.5 KiB fetched + 268.0 KiB written
 # (profiles/cross_attention_image_roofline.md).  Re-measured whenever the
 # attention kernels change.
-TRAFFIC_B1_IMAGE_BYTES = 44804096
-TRAFFIC_B8_IMAGE_BYTES = 291476480   # same profile, batch-8 op (no key split)
+TRAFFIC_B1_IMAGE_BYTES = 46878208
+TRAFFIC_B8_IMAGE_BYTES = 291466240   # same profile, batch-8 op (no key split)
 
 
 def attn_bytes(B, H, Sq, Sk_valid_total, D=64, eb=2):
@@ -249,7 +249,10 @@ def make_model(B, int8=False, seed=1234):
     img = torch.randn(B, cfg.img_len, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
     state = torch.randn(B, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
     rng = np.random.default_rng(seed + B)
-    ll = torch.from_numpy(rng.integers(32, 1025, size=B).astype(np.int32)).to(dev)
+    lens = rng.integers(32, 1025, size=B).astype(np.int32)
+    ll = torch.from_numpy(lens).to(dev)
+    if B == 1:   # the caller's language tensor holds L = lens[0] rows (the reference's [1, L, 4096])
+        m.set_lang_rows(int(lens[0]))
     m.set_condition(lang, ll, img, state)          # warm-up (first launch of each kernel)
     torch.cuda.synchronize()
     start, stop = _events()
@@ -304,7 +307,10 @@ def bench_infer(m, steps):
     lt = torch.randn(B, cfg.lang_max, cfg.lang_token_dim, device=dev, generator=g).to(torch.bfloat16)
     it = torch.randn(B, cfg.img_len, cfg.img_token_dim, device=dev, generator=g).to(torch.bfloat16)
     st = torch.randn(B, cfg.state_dim, device=dev, generator=g).to(torch.bfloat16)
-    ll = torch.from_numpy(np.random.default_rng(5).integers(32, 1025, size=B).astype(np.int32)).to(dev)
+    lens = np.random.default_rng(5).integers(32, 1025, size=B).astype(np.int32)
+    ll = torch.from_numpy(lens).to(dev)
+    if B == 1:
+        m.set_lang_rows(int(lens[0]))
     m.infer(1, lt, ll, it, st, noise_seed=3)          # capture / warm-up
     m.infer(2, lt, ll, it, st, noise_seed=3)
     torch.cuda.synchronize()
@@ -591,8 +597,9 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "config 4: RDT-1B denoise loop, 5 Euler steps, batch 1, 28 layers, "
-                               "hidden 2048, 32 heads, 67 tokens, lang 1024 keys (valid length "
-                               "U{32..1024}) / image 4374 keys cached once, one hipGraph replay "
+                               "hidden 2048, 32 heads, 67 tokens, language condition of L ~ "
+                               "U{32..1024} token rows (padded to 1024, only the L rows encoded "
+                               "and read) / image 4374 keys cached once, one hipGraph replay "
                                "per step, random-init weights; the once-per-inference condition "
                                "encode is not in value (extra.encode_condition_b1_ms; a whole "
                                "control step with a new camera frame, encode + loop + host copy: "

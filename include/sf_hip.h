@@ -169,7 +169,9 @@ int sf_attn_fwd_noalloc(const sf_attn_desc* desc, const void* q, const void* k,
  *   epilogue SF_EPI_HEADS: the N columns are 1..3 sections of H*64 (Q|K|V or
  *        K|V, the order of split_qkv / split_kv, split_ops.cuh:62-84,
  *        210-226); section j goes to head_out[j][b][h][s][d] (bf16, element
- *        strides head_stride[j] = {b, h, s}) with row m = b*S + s, after an
+ *        strides head_stride[j] = {b, h, s}) with row m = b*S + s (M need
+ *        not be a multiple of S: the last batch element may be partial,
+ *        e.g. the first L < S rows of one element), after an
  *        RMSNorm over the 64 head dims with head_gamma[j] when that pointer
  *        is non-NULL (q_norm / k_norm, dit_block.cu:219-220, 307-308);
  *   epilogue SF_EPI_ADD_NORM: C (fp32 residual) += result, then

@@ -125,6 +125,18 @@ int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t* lang_len,
  * state bf16 [B, state_dim]; runs the adaptors then sf_rdt_set_condition. */
 int sf_rdt_encode_condition(sf_rdt* m, const void* lang_tokens, const int32_t* lang_len,
                             const void* img_tokens, const void* state, void* stream);
+/* The language condition's token count L, 1..lang_max (default lang_max):
+ * the length of the reference's language_tokens tensor [B, L, 4096]
+ * (rdt1b.cpp:174-186), whose encode touches L rows, where the padded layout
+ * here holds lang_max.  From the next condition set (sf_rdt_set_condition,
+ * sf_rdt_encode_condition, or sf_rdt_infer, which re-encodes after a
+ * change), the cross-attention reads at most L keys (lang_len[b] still
+ * masks below that), and at batch 1 the language adaptor and every
+ * language K/V projection run over the first L token rows only (batch > 1
+ * keeps the padded rows: rows of one batch element are not contiguous with
+ * the next one's).  Host only; prepares the new GEMM shapes (call outside
+ * graph capture). */
+int sf_rdt_set_lang_rows(sf_rdt* m, int32_t rows);
 
 /* RDTBlock::forward (src/models/rdt1b/dit_block.cu:349-387) for blocks
  * [first, first + count) on the residual stream x fp32 [B, horizon+3, D]

@@ -35,7 +35,6 @@
 #include <math.h>
 #include <stdint.h>
 
-#include <algorithm>
 #include <mutex>
 
 #include "sf_device.h"
@@ -64,8 +63,6 @@ struct AttnArgs {
     int B, H, Sq, Sk;
     int nsplit;
     int nqc;          // query chunks
-    int ngroups;      // B * H * nqc
-    int xcd_grid;     // split call on 1-D grids grouped by XCD (ring + merge)
     int out_kind;     // OutKind
     int causal;
     float scale_log2;   // scale * log2(e)
@@ -349,28 +346,10 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     const int g = lane >> 4;
     const int r = lane & 15;
     const int nsplit = a.nsplit;
-    int split, qc, h, b;
-    if (a.xcd_grid) {
-        // 1-D grid: workgroup L serves query chunk gi of XCD lane L mod 8, so
-        // the splits of one (b, h, chunk) have ids congruent mod 8 and run
-        // on one XCD (the dispatcher hands workgroups to the 8 XCDs
-        // round-robin): Q is fetched into one L2 and the merge kernel, laid
-        // out the same way, reads the partials back from it.  Ids past the
-        // last chunk exit.
-        const int L = blockIdx.x, slot = L >> 3;
-        const int gi = (slot / nsplit) * 8 + (L & 7);
-        if (gi >= a.ngroups) return;
-        split = slot - (slot / nsplit) * nsplit;
-        qc = gi % a.nqc;
-        const int bh = gi / a.nqc;
-        h = bh % a.H;
-        b = bh / a.H;
-    } else {
-        split = blockIdx.x % nsplit;
-        qc = blockIdx.x / nsplit;
-        h = blockIdx.y;
-        b = blockIdx.z;
-    }
+    const int split = blockIdx.x % nsplit;
+    const int qc = blockIdx.x / nsplit;
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
     const int q0 = qc * QR;
 
     int valid = a.Sk;
@@ -717,24 +696,9 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 // out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     const int lane = threadIdx.x & 63;
-    int q, h, b;
-    if (a.xcd_grid) {
-        // the ring kernel's XCD grouping: the 20 four-row workgroups of query
-        // chunk gi at ids congruent to gi mod 8, on the XCD whose L2 holds
-        // the chunk's partials
-        constexpr int kRB = 16 * kQB / 4;
-        const int L = blockIdx.x, slot = L >> 3;
-        const int gi = (slot / kRB) * 8 + (L & 7);
-        if (gi >= a.ngroups) return;
-        const int qc = gi % a.nqc, bh = gi / a.nqc;
-        h = bh % a.H;
-        b = bh / a.H;
-        q = qc * 16 * kQB + (slot % kRB) * 4 + (threadIdx.x >> 6);
-    } else {
-        q = blockIdx.x * 4 + (threadIdx.x >> 6);
-        h = blockIdx.y;
-        b = blockIdx.z;
-    }
+    const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
     if (q >= a.Sq) return;
     const int ns = a.nsplit;   // <= kMaxSplits = 64
     const size_t row0 = ((size_t)b * a.H + h) * ns * (size_t)a.Sq + q;   // split 0's row
@@ -1254,12 +1218,6 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         a.part_ml = a.part_o + (size_t)d->B * d->H * ns * d->Sq * sfk::kD;
     }
     if ((long)ns * nqc > 0x7fffffffL) return SF_ENOTSUP;
-    const long ng = (long)d->B * d->H * nqc;
-    a.ngroups = (int)std::min(ng, 0x7fffffffL);
-    // split bf16 / fp16 calls run on XCD-grouped 1-D grids (ring and merge)
-    a.xcd_grid = ns > 1 && d->in_dtype != SF_F32 && d->Sk > sfk::kShortMaxKeys &&
-                 8 * ((ng + 7) / 8) * std::max(ns, 16 * sfk::kQB / 4) <= 0x7fffffffL;
-    const unsigned xg_groups = (unsigned)(8 * ((ng + 7) / 8));
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f16 = d->in_dtype == SF_F16;
@@ -1283,7 +1241,7 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         }
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
     } else {
-        const dim3 grid = a.xcd_grid ? dim3(xg_groups * (unsigned)ns) : dim3(ns * nqc, d->H, d->B);
+        const dim3 grid(ns * nqc, d->H, d->B);
         if (d->exact_pv) {
             if (f16) hipLaunchKernelGGL((sfk::attn_ring_kernel<true, true>), grid, dim3(256), 0, s, a);
             else hipLaunchKernelGGL((sfk::attn_ring_kernel<true, false>), grid, dim3(256), 0, s, a);
@@ -1294,9 +1252,8 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     }
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     if (ns > 1) {
-        const dim3 mgrid = a.xcd_grid ? dim3(xg_groups * (unsigned)(16 * sfk::kQB / 4))
-                                      : dim3((d->Sq + 3) / 4, d->H, d->B);
-        hipLaunchKernelGGL(sfk::attn_merge_kernel, mgrid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(sfk::attn_merge_kernel, dim3((d->Sq + 3) / 4, d->H, d->B), dim3(256), 0,
+                           s, a);
         if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     }
     return SF_OK;

@@ -141,6 +141,14 @@ struct sf_rdt {
     // encoded for, valid until another condition or new weights replace it
     float* x_infer = nullptr;      // [B*T*A] initial noise, then the action chunk
     bool infer_cond_valid = false;
+
+    // Language token rows per batch element (the reference's L, the length
+    // of its language_tokens tensor): lang_rows is the caller's setting,
+    // cond_lang_rows the value the cached condition was encoded with (the
+    // cross-attention reads at most that many keys).  At batch 1 the
+    // language adaptor and K/V projections run over those rows only.
+    int32_t lang_rows = 0;
+    int32_t cond_lang_rows = 0;
     uint64_t infer_cond_frame = 0;
 
     std::string last_error;
@@ -346,12 +354,27 @@ int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
     return sf_gemm(&d, s);
 }
 
+// Sc: the rows per head of the K/V buffer (its capacity), Sk <= Sc the keys
+// read.
 int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v, int Sk,
-              const int32_t* valid_len, void* out, bool exact_pv, hipStream_t s) {
+              const int32_t* valid_len, void* out, bool exact_pv, hipStream_t s, int Sc = 0) {
     const sf_rdt_config& c = m->cfg;
     const int S = c.horizon + 3;
     sf_attn_desc d;
     sf_attn_desc_init_bhsd(&d, c.batch, c.heads, S, Sk, 64, SF_BF16, SF_BF16);
+    if (Sc > Sk) {
+        d.k_stride[0] = d.v_stride[0] = (int64_t)c.heads * Sc * 64;
+        d.k_stride[1] = d.v_stride[1] = (int64_t)Sc * 64;
+        // the split count of the full buffer: its key splits are shares of
+        // the valid keys, which already lie below Sk (fewer, longer splits
+        // for the shorter key range measured slower: 8.9 vs 7.9 us per
+        // call at batch 1)
+        if (Sk > 128) {
+            sf_attn_desc full = d;
+            full.Sk = Sc;
+            d.num_splits = sf_attn_num_splits(&full);
+        }
+    }
     d.kv_valid_len = valid_len;
     d.exact_pv = exact_pv ? 1 : 0;
     // output straight into [B, S, H*64] (head_to_seq fused away)
@@ -367,8 +390,9 @@ int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v
 // path's algorithms now, outside any graph capture.
 size_t gemm_ws_for(const sf_rdt* m, bool prepare, int* status) {
     const sf_rdt_config& c = m->cfg;
-    const int rows[6] = {c.batch * (c.horizon + 3), c.batch * c.horizon, c.batch, 1,
-                         c.batch * c.lang_max, c.batch * c.img_len};
+    const int rows[7] = {c.batch * (c.horizon + 3), c.batch * c.horizon, c.batch, 1,
+                         c.batch * c.lang_max, c.batch * c.img_len,
+                         std::min(160, c.lang_max)};   // largest split-K M (language rows at batch 1)
     size_t best = 0;
     for (const Param& p : m->params) {
         if (p.shape.size() != 2 || p.dtype == SF_F32) continue;
@@ -435,8 +459,9 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     const int cq_g[1] = {L.cq_norm};
     SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s));
     const bool lang = (i % 2) == 0;
-    SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? c.lang_max : c.img_len,
-                     lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s));
+    SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? m->cond_lang_rows : c.img_len,
+                     lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,
+                     lang ? c.lang_max : c.img_len));
     SF_TRY(linear_add_norm(m, m->a, SF_BF16, M, L.cproj_w, L.cproj_b, L.norm3, m->n3, fd, s));
     // FFN branch (Mlp::forward, dit_block.cu:143-163); fc2's add + norm
     // writes the next block's norm1 (bf16, the QKV input)
@@ -643,6 +668,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     }
     for (size_t i = 0; i < bufs.size(); ++i) *bufs[i].ptr = m->arena + boff[i];
     m->exact_pv.assign(c.layers, 0);
+    m->lang_rows = m->cond_lang_rows = c.lang_max;
     if (hipStreamCreate(&m->own_stream) != hipSuccess) {
         (void)hipFree(m->arena);
         delete m;
@@ -671,6 +697,15 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
             };
             tab[(size_t)step * c.freq_dim + i] = bf(cv_);
             tab[(size_t)step * c.freq_dim + half + i] = bf(sv);
+        }
+    }
+    // language K/V caches zeroed once: at batch 1 a condition projects only
+    // its L rows, and the V range check reads whole caches
+    for (int i = 0; i < c.layers; i += 2) {
+        const size_t cb = (size_t)(B * H * c.lang_max * 64 * 2);
+        if (hipMemset(m->ck[i], 0, cb) != hipSuccess || hipMemset(m->cv[i], 0, cb) != hipSuccess) {
+            sf_rdt_destroy(m);
+            return SF_EDEVICE;
         }
     }
     if (hipMemcpy(m->sincos, tab.data(), tab.size() * 2, hipMemcpyHostToDevice) != hipSuccess) {
@@ -764,16 +799,22 @@ extern "C" int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t
         SF_HIP(hipMemcpyAsync(m->lang_len, lang_len, B * 4, hipMemcpyDeviceToDevice, s));
     if (state_tok != m->state_tok)
         SF_HIP(hipMemcpyAsync(m->state_tok, state_tok, (size_t)B * D * 2, hipMemcpyDeviceToDevice, s));
+    // language rows: the caller's L at batch 1 (the reference's language
+    // tensor is [B, L, D]); all lang_max rows of the padded layout otherwise
+    if (m->cond_lang_rows != m->lang_rows) release_graph(m);   // its attention reads cond_lang_rows keys
+    m->cond_lang_rows = m->lang_rows;
+    const int Lr = B == 1 ? m->lang_rows : c.lang_max;
     // lang_c + lang_cond_pos_embed[:L], img_c + img_cond_pos_embed (rdt1b.cpp:342-349)
-    SF_TRY(sf_add_pos_bf16(lang_c, pf(m, m->lpos), m->lang_c, B, c.lang_max, D, s));
+    SF_TRY(sf_add_pos_bf16(lang_c, pf(m, m->lpos), m->lang_c, B, Lr, D, s));
     SF_TRY(sf_add_pos_bf16(img_c, pf(m, m->ipos), m->img_c, B, c.img_len, D, s));
     // every block's K/V projection with k_norm, once per inference
     for (int i = 0; i < c.layers; ++i) {
         const bool lang = (i % 2) == 0;
         const int Sc = lang ? c.lang_max : c.img_len;
+        const int rows = lang && B == 1 ? Lr : B * Sc;   // batch 1: the L language rows only
         uint16_t* kv[2] = {m->ck[i], m->cv[i]};
         const int g[2] = {m->layers[i].ck_norm, -1};
-        SF_TRY(linear_heads(m, lang ? m->lang_c : m->img_c, B * Sc, Sc, m->layers[i].ckv_w,
+        SF_TRY(linear_heads(m, lang ? m->lang_c : m->img_c, rows, Sc, m->layers[i].ckv_w,
                             m->layers[i].ckv_b, kv, g, 2, s));
     }
     // each layer's max |V| for the choice of P.V form (resolve_pv_forms)
@@ -791,17 +832,45 @@ extern "C" int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t
     return timestep_embed(m, m->fe, c.ctrl_freq, m->f_emb, s);
 }
 
+extern "C" int sf_rdt_set_lang_rows(sf_rdt* m, int32_t rows) {
+    if (!m || rows < 1 || rows > m->cfg.lang_max) return SF_EINVAL;
+    if (rows == m->lang_rows) return SF_OK;
+    m->lang_rows = rows;
+    m->infer_cond_valid = false;   // sf_rdt_infer re-encodes with the new rows
+    if (m->cfg.batch != 1) return SF_OK;
+    // the language GEMMs at M = rows: library-path algorithms chosen now,
+    // outside any capture (adaptor 4096 -> D -> D, K/V projection D -> 2D)
+    const sf_rdt_config& c = m->cfg;
+    const int D = c.hidden;
+    const int shapes[3][2] = {{D, c.lang_token_dim}, {D, D}, {2 * D, D}};
+    const int widx[3] = {m->la[0], m->la[2], c.layers > 0 ? m->layers[0].ckv_w : m->la[2]};
+    for (int j = 0; j < 3; ++j) {
+        sf_gemm_desc d{};
+        d.M = rows;
+        d.N = shapes[j][0];
+        d.K = shapes[j][1];
+        d.lda = d.K;
+        d.a_dtype = SF_BF16;
+        d.ldw = d.K;
+        d.w_dtype = m->params[widx[j]].dtype;
+        SF_TRY(sf_gemm_prepare(&d));
+    }
+    return SF_OK;
+}
+
 extern "C" int sf_rdt_encode_condition(sf_rdt* m, const void* lang_tokens, const int32_t* lang_len,
                                        const void* img_tokens, const void* state, void* stream) {
     if (!m || !lang_tokens || !lang_len || !img_tokens || !state) return SF_EINVAL;
     const sf_rdt_config& c = m->cfg;
     hipStream_t s = pick_stream(m, stream);
     const int D = c.hidden, B = c.batch;
-    // lang_adaptor: mlp2x_gelu 4096 -> D -> D (rdt1b.cpp:118-120, 185)
-    SF_TRY(linear(m, lang_tokens, c.lang_token_dim, B * c.lang_max, m->la[0], m->la[1],
-                  SF_ACT_GELU_TANH, m->ad_h, D, SF_BF16, false, s));
-    SF_TRY(linear(m, m->ad_h, D, B * c.lang_max, m->la[2], m->la[3], SF_ACT_NONE, m->lang_c, D,
-                  SF_BF16, false, s));
+    // lang_adaptor: mlp2x_gelu 4096 -> D -> D (rdt1b.cpp:118-120, 185), over
+    // the L token rows at batch 1
+    const int lrows = B == 1 ? m->lang_rows : B * c.lang_max;
+    SF_TRY(linear(m, lang_tokens, c.lang_token_dim, lrows, m->la[0], m->la[1], SF_ACT_GELU_TANH, m->ad_h,
+                  D, SF_BF16, false, s));
+    SF_TRY(linear(m, m->ad_h, D, lrows, m->la[2], m->la[3], SF_ACT_NONE, m->lang_c, D, SF_BF16, false,
+                  s));
     // img_adaptor: mlp2x_gelu 1152 -> D -> D (:121-123, 199)
     SF_TRY(linear(m, img_tokens, c.img_token_dim, B * c.img_len, m->ia[0], m->ia[1],
                   SF_ACT_GELU_TANH, m->ad_h, D, SF_BF16, false, s));

@@ -66,6 +66,7 @@ def lib():
     L.sf_rdt_pv_exact.argtypes = [vp, i32]
     L.sf_rdt_pv_exact.restype = i32
     L.sf_rdt_set_condition.argtypes = [vp, vp, vp, vp, vp, vp]
+    L.sf_rdt_set_lang_rows.argtypes = [vp, i32]
     L.sf_rdt_encode_condition.argtypes = [vp, vp, vp, vp, vp, vp]
     L.sf_rdt_denoise_step.argtypes = [vp, vp, ctypes.c_float, vp, vp]
     L.sf_rdt_sample.argtypes = [vp, vp, i32, vp]
@@ -195,6 +196,13 @@ class RdtModel:
         v = np.ascontiguousarray(values)
         assert v.itemsize == esize and offset + v.size <= int(np.prod(shape))
         _hipmemcpy(lib().sf_rdt_param_data(self.h, idx) + offset * esize, v.ctypes.data, v.nbytes, 1)
+
+    def set_lang_rows(self, rows):
+        """The language condition's token count L (sf_rdt_set_lang_rows): the
+        cross-attention reads at most L keys, and at batch 1 the language
+        adaptor and K/V projections run over L rows, from the next condition
+        set."""
+        abi.check(lib().sf_rdt_set_lang_rows(self.h, int(rows)), "sf_rdt_set_lang_rows")
 
     def pv_exact(self, layer):
         """sf_rdt_pv_exact: 1 when block `layer`'s cross-attention runs the

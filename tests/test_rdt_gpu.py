@@ -264,6 +264,63 @@ def test_encode_condition_runs_adaptors():
     assert_within_floor(v, ref, floor, "encode_condition + step")
 
 
+def test_lang_rows_reads_only_the_first_rows():
+    """sf_rdt_set_lang_rows(L) at batch 1 (the reference's language tensor
+    is [B, L, 4096], rdt1b.cpp:174-186): the language K/V projection covers
+    the first L condition rows only and the cross-attention reads at most L
+    keys.  NaN rows past L are therefore never read -- the V range check of
+    the language layer still sees finite (zeroed) cache rows and keeps the
+    fp16 P.V form -- and the step equals a model given the same rows with
+    lang_len = L (lang_len past L is clamped to L keys)."""
+    c = small_cfg(batch=1, lang_max=192)
+    L = 100
+    lang, _, img, state = make_condition(c, lang_len=[L])
+    x_t = torch.from_numpy(O.randn(98, (1, c.horizon, c.action_dim))).to(DEV)
+    m_full = build(c)
+    set_cond(m_full, lang, np.array([L], np.int32), img, state)
+    ref = m_full.denoise_step(x_t, 0.6).cpu().numpy()
+    m = build(c)
+    m.set_lang_rows(L)
+    bad = lang.copy()
+    bad[:, L:] = np.nan
+    set_cond(m, bad, np.array([c.lang_max], np.int32), img, state)
+    got = m.denoise_step(x_t, 0.6).cpu().numpy()
+    assert np.isfinite(got).all()
+    assert m.pv_exact(0) == 0 and m.pv_exact(1) == 0
+    assert mean_rel(got, ref) < 2e-3
+    with pytest.raises(abi.SfError):
+        m.set_lang_rows(0)
+    with pytest.raises(abi.SfError):
+        m.set_lang_rows(c.lang_max + 1)
+
+
+def test_lang_rows_infer_reencodes_and_recaptures():
+    """A new row count makes sf_rdt_infer encode again for the same frame
+    id, and the captured loop is rebuilt for the new key count: the result
+    equals a fresh model fed the padded tokens masked to L (the adaptor runs
+    over the L rows only, so NaN token rows past L never reach it), and going
+    back to all rows reproduces the first result bit for bit."""
+    c = small_cfg(batch=1, lang_max=192)
+    lt = O.bf16_round(O.randn(61, (1, c.lang_max, c.lang_token_dim)))
+    it = bf(O.bf16_round(O.randn(62, (1, c.img_len, c.img_token_dim))))
+    st = bf(O.bf16_round(O.randn(63, (1, c.state_dim))))
+    ll_all = torch.tensor([c.lang_max], dtype=torch.int32, device=DEV)
+    m = build(c)
+    a_full, e0 = m.infer(1, bf(lt), ll_all, it, st, noise_seed=5)
+    assert e0
+    m.set_lang_rows(120)
+    lt_nan = lt.copy()
+    lt_nan[:, 120:] = np.nan
+    a_120, e1 = m.infer(1, bf(lt_nan), ll_all, it, st, noise_seed=5)
+    assert e1 and np.isfinite(a_120).all() and not np.array_equal(a_120, a_full)
+    m2 = build(c)
+    a_ref, _ = m2.infer(1, bf(lt), torch.tensor([120], dtype=torch.int32, device=DEV), it, st, noise_seed=5)
+    assert mean_rel(a_120, a_ref) < 2e-3
+    m.set_lang_rows(c.lang_max)
+    a_back, e2 = m.infer(1, bf(lt), ll_all, it, st, noise_seed=5)
+    assert e2 and np.array_equal(a_back, a_full)
+
+
 def test_infer_frame_cache_noise_and_host_output():
     """sf_rdt_infer (InferenceEngine::infer, inference_engine.cpp:99-175):
     the condition is encoded on the first call and whenever the frame id
