@@ -688,15 +688,26 @@ __global__ __launch_bounds__(kAddNormThreads) void reduce_addnorm_kernel(const E
 }
 
 // int8 weight codes -> bf16 (exact), row-major [N][K] out of [N][ldw].
+// CH codes per thread (16: one 16-byte load and two 16-byte stores, needs
+// 16-byte aligned rows; 8 otherwise); 32-bit index arithmetic (callers keep
+// N * K / CH below 2^31).
+template <int CH>
 __global__ __launch_bounds__(256) void widen_int8_kernel(const int8_t* __restrict__ q, int64_t ldw,
                                                          uint16_t* __restrict__ out, int N, int K) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;   // 8 codes per thread
-    const int k8 = K / 8;
-    if (idx >= (int64_t)N * k8) return;
-    const int64_t n = idx / k8;
-    const int k = 8 * (int)(idx % k8);
-    const uint2 raw = *reinterpret_cast<const uint2*>(q + n * ldw + k);
-    *reinterpret_cast<bf16x8*>(out + n * K + k) = i8x8_to_bf16x8(raw);
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t kc = (uint32_t)K / CH;
+    if (idx >= (uint32_t)N * kc) return;
+    const uint32_t n = idx / kc;
+    const uint32_t k = CH * (idx - n * kc);
+    const int8_t* src = q + (int64_t)n * ldw + k;
+    uint16_t* dst = out + (int64_t)n * K + k;
+    if constexpr (CH == 16) {
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(src);
+        *reinterpret_cast<bf16x8*>(dst) = i8x8_to_bf16x8(uint2{raw[0], raw[1]});
+        *reinterpret_cast<bf16x8*>(dst + 8) = i8x8_to_bf16x8(uint2{raw[2], raw[3]});
+    } else {
+        *reinterpret_cast<bf16x8*>(dst) = i8x8_to_bf16x8(*reinterpret_cast<const uint2*>(src));
+    }
 }
 
 struct SkPlan {
@@ -1190,9 +1201,16 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
             int64_t ldw = d->ldw;
             if (w8) {
                 uint16_t* wb = reinterpret_cast<uint16_t*>(ws + lp.c_bytes);
-                const int64_t n8 = (int64_t)d->N * (d->K / 8);
-                hipLaunchKernelGGL(sfk::widen_int8_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s,
-                                   static_cast<const int8_t*>(d->W), d->ldw, wb, d->N, d->K);
+                const bool c16 = (d->ldw & 15) == 0 && (d->K & 15) == 0;
+                const int64_t nch = (int64_t)d->N * (d->K / (c16 ? 16 : 8));
+                if (nch >= 0x7fffffffLL) return SF_ENOTSUP;
+                const dim3 grid((unsigned)((nch + 255) / 256));
+                if (c16)
+                    hipLaunchKernelGGL(sfk::widen_int8_kernel<16>, grid, dim3(256), 0, s,
+                                       static_cast<const int8_t*>(d->W), d->ldw, wb, d->N, d->K);
+                else
+                    hipLaunchKernelGGL(sfk::widen_int8_kernel<8>, grid, dim3(256), 0, s,
+                                       static_cast<const int8_t*>(d->W), d->ldw, wb, d->N, d->K);
                 if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
                 W = wb;
                 ldw = d->K;
