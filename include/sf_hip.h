@@ -191,6 +191,16 @@ int sf_attn_fwd_noalloc(const sf_attn_desc* desc, const void* q, const void* k,
  * CUs.  M > 160: the library path -- hipBLASLt writes the fp32 product in
  * chunks of <= 8192 rows into the workspace (plus a bf16 copy of int8
  * weights and hipBLASLt's own scratch) and the epilogue kernels read it.
+ * Two library-path cases store a bf16 product instead, with the bias (and
+ * the int8 row scale) applied by hipBLASLt, as the reference's cuBLASLt
+ * BIAS / GELU_BIAS epilogues return C in bf16 (cuda_backend.cu:414-447):
+ *   - SF_EPI_PLAIN into a bf16 C without accumulate, act NONE or GELU_TANH:
+ *     hipBLASLt writes C itself (GELU_BIAS for the GELU), one rounding as
+ *     in the other paths, no epilogue kernel;
+ *   - SF_EPI_HEADS / SF_EPI_ADD_NORM with round_product != 0: the per-head
+ *     RMSNorm or the residual add + RMSNorm read bf16(A.W^T + bias) -- the
+ *     reference's own storage point (the projection's bf16 output feeds
+ *     split_qkv / fused_add_rms_norm) -- instead of the fp32 product.
  * With workspace == NULL a single-pass kernel runs instead and nothing
  * beyond A, W and the outputs is touched.  A non-NULL workspace that is too
  * small is SF_EWORKSPACE.  Calls that may run concurrently need separate
@@ -226,6 +236,7 @@ typedef struct sf_gemm_desc {
     int32_t norm_dtype;
     void* workspace;         /* split-K partial sums, or NULL */
     int64_t workspace_bytes;
+    int32_t round_product;   /* M > 160, SF_EPI_HEADS / SF_EPI_ADD_NORM: bf16 product (see above) */
 } sf_gemm_desc;
 
 /* Bytes of workspace the split-K path needs for this shape (0: the shape

@@ -18,15 +18,19 @@ are rounded, to model a pipeline that stores them in 16-bit types:
   a dict point name -> "bf16" or "f16", e.g. storage_points(ffn16=True) for
          the MI355X runtime at batch <= 2, which stores the FFN inputs (the
          norm3 output and the GELU hidden) in fp16.
-The residual stream and GEMM outputs that feed it stay fp32 throughout.  The
-reference's own bf16 build rounds at all of these points and also rounds the
-residual (norm.cuh:146).
+The residual stream stays fp32 throughout; the block's projection outputs
+stay fp32 except at the "gemm" point.  The reference's own bf16 build rounds
+at all of these points and also rounds the residual (norm.cuh:146).
 
 Points: "cond" condition tokens + position embedding, "kv" cross K/V cache,
 "n1" norm1 / norm_final outputs, "qkv" per-head q/k/v (self and cross),
 "a" attention outputs, "n2" / "n3" norm2 / norm3 outputs, "h" FFN and final
 hidden, "emb" timestep-embedding inputs, "adapt" adaptor inputs / hidden,
-"state" the state token.
+"state" the state token, "gemm" the block projections' outputs before the
+per-head norm or the residual add (qkv, cross q, attention / cross proj,
+fc2; the bf16 outputs of the reference's cuBLASLt epilogues,
+cuda_backend.cu:414-447), which the MI355X runtime stores in bf16 above 160
+rows (storage_points(gemm16=True)).
 """
 from __future__ import annotations
 
@@ -61,12 +65,16 @@ class RdtConfig:
 ALL_POINTS = frozenset({"cond", "kv", "n1", "qkv", "a", "n2", "n3", "h", "emb", "adapt", "state"})
 
 
-def storage_points(ffn16):
+def storage_points(ffn16, gemm16=False):
     """How the MI355X runtime stores each point: bf16 everywhere, except
-    (ffn16: batch * 67 <= 160 rows) the FFN inputs n3 and h in fp16."""
+    (ffn16: batch * 67 <= 160 rows) the FFN inputs n3 and h in fp16; the
+    block projections' outputs ("gemm") in bf16 only with gemm16 (batch *
+    67 > 160 rows), fp32 otherwise."""
     pts = {p: "bf16" for p in ALL_POINTS}
     if ffn16:
         pts["n3"] = pts["h"] = "f16"
+    if gemm16:
+        pts["gemm"] = "bf16"
     return pts
 
 
@@ -112,23 +120,23 @@ def rdt_block(p, i, x, ck, cv, cond_len, cfg, rb=True):
     pre = f"blocks.{i}."
     # self-attention branch (dit_block.cu:198-238)
     n1 = _r(O.rms_norm(x, p[pre + "norm1.weight"], cfg.eps), rb, "n1")
-    qkv = O.linear(n1, p[pre + "attn.qkv.weight"], p[pre + "attn.qkv.bias"])
+    qkv = _r(O.linear(n1, p[pre + "attn.qkv.weight"], p[pre + "attn.qkv.bias"]), rb, "gemm")
     Q, K, V = O.split_qkv(qkv.reshape(B, S, 3 * D), H, 64)
     Q = _r(O.rms_norm(Q, p[pre + "attn.q_norm.weight"], cfg.eps), rb, "qkv")
     K = _r(O.rms_norm(K, p[pre + "attn.k_norm.weight"], cfg.eps), rb, "qkv")
     V = _r(V, rb, "qkv")
     a = _r(O.head_to_seq(O.attention_f32(Q, K, V)), rb, "a")
-    x = x + O.linear(a, p[pre + "attn.proj.weight"], p[pre + "attn.proj.bias"])
+    x = x + _r(O.linear(a, p[pre + "attn.proj.weight"], p[pre + "attn.proj.bias"]), rb, "gemm")
     # cross-attention branch (dit_block.cu:274-326), norm2 from fused_add_rms_norm
     n2 = _r(O.rms_norm(x, p[pre + "norm2.weight"], cfg.eps), rb, "n2")
-    cq = O.linear(n2, p[pre + "cross_attn.q.weight"], p[pre + "cross_attn.q.bias"])
+    cq = _r(O.linear(n2, p[pre + "cross_attn.q.weight"], p[pre + "cross_attn.q.bias"]), rb, "gemm")
     cq = _r(O.rms_norm(heads_of(cq.reshape(B, S, D), H), p[pre + "cross_attn.q_norm.weight"], cfg.eps), rb, "qkv")
     ca = _r(O.head_to_seq(O.attention_f32(cq, ck, cv, valid_len=cond_len)), rb, "a")
-    x = x + O.linear(ca, p[pre + "cross_attn.proj.weight"], p[pre + "cross_attn.proj.bias"])
+    x = x + _r(O.linear(ca, p[pre + "cross_attn.proj.weight"], p[pre + "cross_attn.proj.bias"]), rb, "gemm")
     # FFN branch (Mlp::forward, dit_block.cu:143-163: fc1 + GELU, fc2)
     n3 = _r(O.rms_norm(x, p[pre + "norm3.weight"], cfg.eps), rb, "n3")
     h = _r(O.linear(n3, p[pre + "ffn.fc1.weight"], p[pre + "ffn.fc1.bias"], act=1), rb, "h")
-    return x + O.linear(h, p[pre + "ffn.fc2.weight"], p[pre + "ffn.fc2.bias"])
+    return x + _r(O.linear(h, p[pre + "ffn.fc2.weight"], p[pre + "ffn.fc2.bias"]), rb, "gemm")
 
 
 def timestep_embed(p, name, step, cfg, rb=True):

@@ -81,6 +81,7 @@ class GemmDesc(ctypes.Structure):
         ("norm_gamma", ctypes.c_void_p), ("norm_out", ctypes.c_void_p),
         ("norm_ldo", ctypes.c_int64), ("norm_dtype", ctypes.c_int32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+        ("round_product", ctypes.c_int32),
     ]
 
 

@@ -495,6 +495,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
 
 struct EpiArgs {
     const float* part;     // [splits][M][N]
+    const uint16_t* part16;  // or the library path's bf16 product [M][N], bias and scale already in
     int splits;
     int M, N;
     int64_t m_off;         // row of the outputs that partial row 0 belongs to
@@ -531,6 +532,16 @@ struct Quad {
 
 template <int NS>
 __device__ __forceinline__ void load_quad(const EpiArgs& e, int m, int n, Quad<NS>& q) {
+    if (e.part16) {   // one "slice": the rounded product, bias and scale applied
+        const uint2 h = *reinterpret_cast<const uint2*>(e.part16 + (int64_t)m * e.N + n);
+        q.part[0] = f32x4{bf16_bits_to_f32(h.x & 0xffffu), bf16_bits_to_f32(h.x >> 16),
+                          bf16_bits_to_f32(h.y & 0xffffu), bf16_bits_to_f32(h.y >> 16)};
+#pragma unroll
+        for (int s = 1; s < NS; ++s) q.part[s] = q.part[0];
+        q.bias = f32x4{0.f, 0.f, 0.f, 0.f};
+        q.scale = f32x4{1.f, 1.f, 1.f, 1.f};
+        return;
+    }
     const float* p = e.part + (int64_t)m * e.N + n;
     const int64_t stride = (int64_t)e.M * e.N;
 #pragma unroll
@@ -883,18 +894,45 @@ LibPlan plan_library(int M, int N, int K, bool w8, bool a_conv) {
     return p;
 }
 
+// What hipBLASLt stores for one call: the fp32 product (all flags off), or
+// a bf16 D with the bias epilogue (BIAS, or GELU_BIAS with gelu) and, for
+// int8 weights, the per-row scale as a device alpha vector (one alpha per
+// row of D, i.e. per output column n).  ldd: D's leading dimension.
+struct LtKind {
+    bool out16 = false, bias = false, gelu = false, alpha = false;
+    int64_t ldd = 0;
+    int bits() const { return (out16 ? 1 : 0) | (bias ? 2 : 0) | (gelu ? 4 : 0) | (alpha ? 8 : 0); }
+};
+
 // One hipBLASLt handle per device and one (descriptor, layouts, algorithm)
-// per GEMM shape, created on first use and kept for the process.
+// per GEMM shape and kind, created on first use and kept for the process.
 struct LtShape {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
     hipblasLtMatmulAlgo_t algo{};
+    LtKind kind;
     bool ok = false;
 };
 
 std::mutex g_lt_mu;
 std::map<int, hipblasLtHandle_t> g_lt_handles;
-std::map<std::tuple<int, int, int, int, int64_t, int64_t>, LtShape> g_lt_shapes;
+std::map<std::tuple<int, int, int, int, int64_t, int64_t, int64_t, int>, LtShape> g_lt_shapes;
+
+// D = op(W) . A_act for one call; the bias pointer is a descriptor
+// attribute, so setting it and enqueueing the product hold the lock (the
+// descriptor is shared by every caller of the shape).
+hipblasStatus_t lt_matmul(hipblasLtHandle_t h, const LtShape& sh, const hipblasLtMatmulAlgo_t& algo,
+                          const float* bias, const float* alpha_vec, const void* W, const void* A, void* D,
+                          void* ws, hipStream_t s) {
+    std::lock_guard<std::mutex> lock(g_lt_mu);
+    if (sh.kind.bias &&
+        hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof bias) !=
+            HIPBLAS_STATUS_SUCCESS)
+        return HIPBLAS_STATUS_INVALID_VALUE;
+    const float one = 1.f, zero = 0.f;
+    const void* alpha = sh.kind.alpha ? static_cast<const void*>(alpha_vec) : static_cast<const void*>(&one);
+    return hipblasLtMatmul(h, sh.desc, alpha, W, sh.a, A, sh.b, &zero, D, sh.d, D, sh.d, &algo, ws, kLibLtBytes, s);
+}
 
 // Times each candidate algorithm on scratch buffers of the shape (zeros; 2
 // warm-up and 5 timed runs on a private stream) and returns the index of
@@ -902,25 +940,26 @@ std::map<std::tuple<int, int, int, int, int64_t, int64_t>, LtShape> g_lt_shapes;
 // under graph capture.
 int lt_pick_fastest(hipblasLtHandle_t h, const LtShape& sh, const hipblasLtMatmulHeuristicResult_t* res, int nres,
                     int N, int K, int rows, int64_t lda, int64_t ldw) {
-    void *a = nullptr, *w = nullptr, *dbuf = nullptr, *ws = nullptr;
+    void *a = nullptr, *w = nullptr, *dbuf = nullptr, *ws = nullptr, *vec = nullptr;
     hipStream_t st = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     int best = -1;
     float best_ms = 0.f;
-    const size_t abytes = (size_t)rows * lda * 2, wbytes = (size_t)N * ldw * 2, dbytes = (size_t)rows * N * 4;
+    const size_t abytes = (size_t)rows * lda * 2, wbytes = (size_t)N * ldw * 2;
+    const size_t dbytes = (size_t)rows * sh.kind.ldd * (sh.kind.out16 ? 2 : 4);
     if (hipMalloc(&a, abytes) == hipSuccess && hipMalloc(&w, wbytes) == hipSuccess &&
         hipMalloc(&dbuf, dbytes) == hipSuccess && hipMalloc(&ws, kLibLtBytes) == hipSuccess &&
-        hipStreamCreate(&st) == hipSuccess && hipEventCreate(&e0) == hipSuccess &&
-        hipEventCreate(&e1) == hipSuccess && hipMemsetAsync(a, 0, abytes, st) == hipSuccess &&
-        hipMemsetAsync(w, 0, wbytes, st) == hipSuccess) {
-        const float one = 1.f, zero = 0.f;
+        hipMalloc(&vec, (size_t)N * 4) == hipSuccess && hipStreamCreate(&st) == hipSuccess &&
+        hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess &&
+        hipMemsetAsync(a, 0, abytes, st) == hipSuccess && hipMemsetAsync(w, 0, wbytes, st) == hipSuccess &&
+        hipMemsetAsync(vec, 0, (size_t)N * 4, st) == hipSuccess) {
+        const float* fv = static_cast<const float*>(vec);
         for (int i = 0; i < nres; ++i) {
             if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kLibLtBytes) continue;
             bool ok = true;
             for (int r = 0; r < 7 && ok; ++r) {
                 if (r == 2) ok = hipEventRecord(e0, st) == hipSuccess;
-                ok = ok && hipblasLtMatmul(h, sh.desc, &one, w, sh.a, a, sh.b, &zero, dbuf, sh.d, dbuf, sh.d,
-                                           &res[i].algo, ws, kLibLtBytes, st) == HIPBLAS_STATUS_SUCCESS;
+                ok = ok && lt_matmul(h, sh, res[i].algo, fv, fv, w, a, dbuf, ws, st) == HIPBLAS_STATUS_SUCCESS;
             }
             ok = ok && hipEventRecord(e1, st) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
             float ms = 0.f;
@@ -935,70 +974,100 @@ int lt_pick_fastest(hipblasLtHandle_t h, const LtShape& sh, const hipblasLtMatmu
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     if (st) (void)hipStreamDestroy(st);
-    for (void* p : {a, w, dbuf, ws})
+    for (void* p : {a, w, dbuf, ws, vec})
         if (p) (void)hipFree(p);
     (void)hipGetLastError();
     return best;
 }
 
-// D (fp32 [rows][N]) = A_act (bf16 [rows][lda]) . W (bf16 [N][ldw])^T, in
-// hipBLASLt's column-major terms: D (N x rows) = op_T(W: K x N, ld ldw) .
-// (A_act: K x rows, ld lda).  tune: choose among hipBLASLt's first 16
-// candidates by timing them (sf_gemm_prepare); otherwise its first choice.
-// A shape keeps the algorithm it was first created with.
-int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, hipblasLtHandle_t* h, const LtShape** out,
-              bool tune = false) {
+// D ([rows][ldd], fp32 or bf16 per kind) = A_act (bf16 [rows][lda]) . W (bf16
+// [N][ldw])^T (+ bias, GELU, alpha per kind), in hipBLASLt's column-major
+// terms: D (N x rows, ld ldd) = op_T(W: K x N, ld ldw) . (A_act: K x rows,
+// ld lda).  tune: choose among hipBLASLt's first 16 candidates by timing
+// them (sf_gemm_prepare); otherwise its first choice.  A shape keeps the
+// algorithm it was first created with.
+int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, const LtKind& kind, hipblasLtHandle_t* h,
+              const LtShape** out, bool tune = false) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return SF_EDEVICE;
-    std::lock_guard<std::mutex> lock(g_lt_mu);
-    auto hit = g_lt_handles.find(dev);
-    if (hit == g_lt_handles.end()) {
-        hipblasLtHandle_t nh = nullptr;
-        if (hipblasLtCreate(&nh) != HIPBLAS_STATUS_SUCCESS) return SF_EDEVICE;
-        hit = g_lt_handles.emplace(dev, nh).first;
-    }
-    *h = hit->second;
-    const auto key = std::make_tuple(dev, N, K, rows, lda, ldw);
-    auto it = g_lt_shapes.find(key);
-    if (it == g_lt_shapes.end()) {
-        LtShape sh;
-        bool ok = hipblasLtMatmulDescCreate(&sh.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
-        const hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
-        ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof opT) ==
-                       HIPBLAS_STATUS_SUCCESS;
-        ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof opN) ==
-                       HIPBLAS_STATUS_SUCCESS;
-        ok = ok && hipblasLtMatrixLayoutCreate(&sh.a, HIP_R_16BF, K, N, ldw) == HIPBLAS_STATUS_SUCCESS;
-        ok = ok && hipblasLtMatrixLayoutCreate(&sh.b, HIP_R_16BF, K, rows, lda) == HIPBLAS_STATUS_SUCCESS;
-        ok = ok && hipblasLtMatrixLayoutCreate(&sh.d, HIP_R_32F, N, rows, N) == HIPBLAS_STATUS_SUCCESS;
-        hipblasLtMatmulPreference_t pref = nullptr;
-        ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
-        const uint64_t wsmax = kLibLtBytes;
-        ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax,
-                                                         sizeof wsmax) == HIPBLAS_STATUS_SUCCESS;
-        constexpr int kCand = 16;
-        hipblasLtMatmulHeuristicResult_t res[kCand];
-        int nres = 0;
-        ok = ok && hipblasLtMatmulAlgoGetHeuristic(*h, sh.desc, sh.a, sh.b, sh.d, sh.d, pref, kCand, res, &nres) ==
-                       HIPBLAS_STATUS_SUCCESS;
-        // keep the candidates that ran the heuristic and fit the workspace
-        int nuse = 0;
-        for (int i = 0; ok && i < nres; ++i)
-            if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kLibLtBytes) res[nuse++] = res[i];
-        nres = nuse;
-        ok = ok && nres > 0;
-        if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
-        int pick = 0;
-        if (ok && tune && nres > 1) {
-            const int best = lt_pick_fastest(*h, sh, res, nres, N, K, rows, lda, ldw);
-            if (best >= 0) pick = best;
+    LtShape sh;
+    {
+        std::lock_guard<std::mutex> lock(g_lt_mu);
+        auto hit = g_lt_handles.find(dev);
+        if (hit == g_lt_handles.end()) {
+            hipblasLtHandle_t nh = nullptr;
+            if (hipblasLtCreate(&nh) != HIPBLAS_STATUS_SUCCESS) return SF_EDEVICE;
+            hit = g_lt_handles.emplace(dev, nh).first;
         }
-        if (ok) sh.algo = res[pick].algo;
-        sh.ok = ok;
-        it = g_lt_shapes.emplace(key, sh).first;
+        *h = hit->second;
+        auto it = g_lt_shapes.find(std::make_tuple(dev, N, K, rows, lda, ldw, kind.ldd, kind.bits()));
+        if (it != g_lt_shapes.end()) {
+            *out = &it->second;
+            return it->second.ok ? SF_OK : SF_ENOTSUP;
+        }
     }
-    *out = &it->second;
-    return it->second.ok ? SF_OK : SF_ENOTSUP;
+    sh.kind = kind;
+    bool ok = hipblasLtMatmulDescCreate(&sh.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+    const hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
+    ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof opT) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof opN) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    if (kind.bias || kind.gelu) {
+        const hipblasLtEpilogue_t epi = kind.bias ? (kind.gelu ? HIPBLASLT_EPILOGUE_GELU_BIAS : HIPBLASLT_EPILOGUE_BIAS)
+                                                  : HIPBLASLT_EPILOGUE_GELU;
+        ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof epi) ==
+                       HIPBLAS_STATUS_SUCCESS;
+    }
+    if (kind.bias) {
+        const int32_t bt = HIP_R_32F;
+        ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof bt) ==
+                       HIPBLAS_STATUS_SUCCESS;
+    }
+    if (kind.alpha) {
+        const int32_t pm = HIPBLASLT_POINTER_MODE_ALPHA_DEVICE_VECTOR_BETA_HOST;
+        ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_POINTER_MODE, &pm, sizeof pm) ==
+                       HIPBLAS_STATUS_SUCCESS;
+    }
+    ok = ok && hipblasLtMatrixLayoutCreate(&sh.a, HIP_R_16BF, K, N, ldw) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&sh.b, HIP_R_16BF, K, rows, lda) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&sh.d, kind.out16 ? HIP_R_16BF : HIP_R_32F, N, rows, kind.ldd) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+    const uint64_t wsmax = kLibLtBytes;
+    ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax,
+                                                     sizeof wsmax) == HIPBLAS_STATUS_SUCCESS;
+    constexpr int kCand = 16;
+    hipblasLtMatmulHeuristicResult_t res[kCand];
+    int nres = 0;
+    ok = ok && hipblasLtMatmulAlgoGetHeuristic(*h, sh.desc, sh.a, sh.b, sh.d, sh.d, pref, kCand, res, &nres) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    // keep the candidates that ran the heuristic and fit the workspace
+    int nuse = 0;
+    for (int i = 0; ok && i < nres; ++i)
+        if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kLibLtBytes) res[nuse++] = res[i];
+    nres = nuse;
+    ok = ok && nres > 0;
+    if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
+    int pick = 0;
+    if (ok && tune && nres > 1) {
+        const int best = lt_pick_fastest(*h, sh, res, nres, N, K, rows, lda, ldw);
+        if (best >= 0) pick = best;
+    }
+    if (ok) sh.algo = res[pick].algo;
+    sh.ok = ok;
+    std::lock_guard<std::mutex> lock(g_lt_mu);
+    // a shape another thread created meanwhile wins; this one is dropped
+    auto ins = g_lt_shapes.emplace(std::make_tuple(dev, N, K, rows, lda, ldw, kind.ldd, kind.bits()), sh);
+    if (!ins.second) {
+        if (sh.a) (void)hipblasLtMatrixLayoutDestroy(sh.a);
+        if (sh.b) (void)hipblasLtMatrixLayoutDestroy(sh.b);
+        if (sh.d) (void)hipblasLtMatrixLayoutDestroy(sh.d);
+        if (sh.desc) (void)hipblasLtMatmulDescDestroy(sh.desc);
+    }
+    *out = &ins.first->second;
+    return ins.first->second.ok ? SF_OK : SF_ENOTSUP;
 }
 
 }  // namespace
@@ -1146,14 +1215,36 @@ int gemm_single_pass(const sf_gemm_desc* d, const sfk::EpiArgs& e, hipStream_t s
 int64_t lib_ldw(const sf_gemm_desc* d) { return d->w_dtype == SF_I8 ? d->K : d->ldw; }
 int64_t lib_lda(const sf_gemm_desc* d) { return d->a_dtype != SF_BF16 ? d->K : d->lda; }
 
+// What the library path stores for this call.  A plain bf16 C (no
+// accumulate, act NONE or GELU) is written by hipBLASLt itself with the bias
+// (GELU_BIAS) epilogue -- one rounding, as on every path; with
+// round_product the heads / add+norm epilogues read bf16(A.W^T + bias) from
+// the workspace.  int8 row scales go in as hipBLASLt's alpha vector
+// whenever D is bf16 (they must precede the rounding).  Otherwise the fp32
+// product, and the epilogue kernel applies scale, bias and activation.
+LtKind lib_kind(const sf_gemm_desc* d) {
+    LtKind k;
+    k.ldd = d->N;
+    const bool act_ok = d->act == SF_ACT_NONE || d->act == SF_ACT_GELU_TANH;
+    const bool plain16 = d->epilogue == SF_EPI_PLAIN && !d->accumulate && d->c_dtype == SF_BF16;
+    const bool rounded = (d->epilogue == SF_EPI_HEADS || d->epilogue == SF_EPI_ADD_NORM) && d->round_product;
+    if (!act_ok || !(plain16 || rounded)) return k;
+    k.out16 = true;
+    k.bias = d->bias != nullptr;
+    k.gelu = d->act == SF_ACT_GELU_TANH;
+    k.alpha = d->w_dtype == SF_I8;
+    if (plain16) k.ldd = d->ldc;
+    return k;
+}
+
 // Whether hipBLASLt has an algorithm for every chunk shape of this call (a
 // shape without one runs the single-pass kernel instead).
-bool lib_available(const sf_gemm_desc* d, const LibPlan& lp, bool tune) {
+bool lib_available(const sf_gemm_desc* d, const LibPlan& lp, const LtKind& kind, bool tune) {
     hipblasLtHandle_t h;
     const LtShape* sh = nullptr;
     for (int rows : {lp.chunk, d->M % lp.chunk}) {
         if (rows <= 0) continue;
-        if (lt_lookup(d->N, d->K, rows, lib_lda(d), lib_ldw(d), &h, &sh, tune) != SF_OK) return false;
+        if (lt_lookup(d->N, d->K, rows, lib_lda(d), lib_ldw(d), kind, &h, &sh, tune) != SF_OK) return false;
     }
     return true;
 }
@@ -1170,9 +1261,17 @@ extern "C" int sf_gemm_prepare(const sf_gemm_desc* d) {
     if (!d) return SF_EINVAL;
     const LibPlan lp = plan_library(d->M, d->N, d->K, d->w_dtype == SF_I8, d->a_dtype != SF_BF16);
     if (!lp.ok) return SF_OK;   // split-K and single-pass paths need no setup
-    // a shape hipBLASLt has no algorithm for is served by the single-pass
-    // kernel: not an error
-    (void)lib_available(d, lp, true);
+    // the fp32 product and the two bf16 products with bias (plain / GELU) at
+    // D = [rows][N]; a shape hipBLASLt has no algorithm for is served by the
+    // single-pass kernel: not an error
+    LtKind k;
+    k.ldd = d->N;
+    (void)lib_available(d, lp, k, true);
+    k.out16 = k.bias = true;
+    k.alpha = d->w_dtype == SF_I8;
+    (void)lib_available(d, lp, k, true);
+    k.gelu = true;
+    (void)lib_available(d, lp, k, true);
     return SF_OK;
 }
 
@@ -1190,7 +1289,8 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     if (d->workspace && !p.split && splittable(d)) {
         const bool w8 = d->w_dtype == SF_I8;
         const LibPlan lp = plan_library(d->M, d->N, d->K, w8, a_conv);
-        if (lp.ok && lib_available(d, lp, false)) {
+        const LtKind kind = lib_kind(d);
+        if (lp.ok && lib_available(d, lp, kind, false)) {
             if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < lp.total) return SF_EWORKSPACE;
             if (!al16(d->workspace)) return SF_EINVAL;
             char* ws = static_cast<char*>(d->workspace);
@@ -1215,12 +1315,12 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
                 W = wb;
                 ldw = d->K;
             }
-            const float one = 1.f, zero = 0.f;
+            const bool direct = kind.out16 && d->epilogue == SF_EPI_PLAIN;   // hipBLASLt writes C
             for (int m0 = 0; m0 < d->M; m0 += lp.chunk) {
                 const int rows = std::min(lp.chunk, d->M - m0);
                 hipblasLtHandle_t h;
                 const LtShape* sh = nullptr;
-                SF_CHECK_OK(lt_lookup(d->N, d->K, rows, lib_lda(d), ldw, &h, &sh));
+                SF_CHECK_OK(lt_lookup(d->N, d->K, rows, lib_lda(d), ldw, kind, &h, &sh));
                 const uint16_t* Ac;
                 if (a_conv) {
                     const int64_t n8 = (int64_t)rows * (d->K / 8);
@@ -1232,14 +1332,24 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
                 } else {
                     Ac = static_cast<const uint16_t*>(d->A) + (int64_t)m0 * d->lda;
                 }
-                if (hipblasLtMatmul(h, sh->desc, &one, W, sh->a, Ac, sh->b, &zero, cbuf, sh->d, cbuf, sh->d,
-                                    &sh->algo, ltws, kLibLtBytes, s) != HIPBLAS_STATUS_SUCCESS)
+                void* D = direct ? static_cast<void*>(static_cast<uint16_t*>(d->C) + (int64_t)m0 * d->ldc)
+                                 : static_cast<void*>(cbuf);
+                if (lt_matmul(h, *sh, sh->algo, d->bias, d->w_scale, W, Ac, D, ltws, s) != HIPBLAS_STATUS_SUCCESS)
                     return SF_ELAUNCH;
+                if (direct) continue;
                 sfk::EpiArgs ec = e;
-                ec.part = cbuf;
                 ec.splits = 1;
                 ec.M = rows;
                 ec.m_off = m0;
+                if (kind.out16) {   // bias, GELU and the int8 scale are in the bf16 product
+                    ec.part = nullptr;
+                    ec.part16 = reinterpret_cast<const uint16_t*>(cbuf);
+                    ec.bias = nullptr;
+                    ec.w_scale = nullptr;
+                    ec.act = SF_ACT_NONE;
+                } else {
+                    ec.part = cbuf;
+                }
                 sfk::launch_reduce<1>(d, ec, s);
                 if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
             }

@@ -289,7 +289,9 @@ int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, i
 }
 
 // x += A W^T + b (fp32 residual m->x, A in a_dtype), then
-// out = rmsnorm(x) * gamma in out_dtype.
+// out = rmsnorm(x) * gamma in out_dtype.  At more than 160 rows the branch
+// output is stored in bf16 before the add (round_product), as the
+// reference's projection returns it (dit_block.cu:233, 321, 160).
 int linear_add_norm(sf_rdt* m, const void* A, int a_dtype, int M, int w_idx, int b_idx, int gamma_idx,
                     void* out, int out_dtype, hipStream_t s) {
     const Param& W = m->params[w_idx];
@@ -317,13 +319,18 @@ int linear_add_norm(sf_rdt* m, const void* A, int a_dtype, int M, int w_idx, int
     d.norm_dtype = out_dtype;
     d.workspace = m->gemm_ws;
     d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
+    d.round_product = 1;
     return sf_gemm(&d, s);
 }
 
 // Per-head projection: sections of H*64 columns -> [B, H, S, 64] bf16.
+// round_product: above 160 rows the projection is stored in bf16 before the
+// per-head RMSNorm, as the reference's qkv / q projection output is
+// (dit_block.cu:207, 284); the once-per-inference K/V cache projection keeps
+// its fp32 product.
 int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
                  uint16_t* const* outs, const int* gamma_idx, int nsec, hipStream_t s,
-                 int a_dtype = SF_BF16) {
+                 int a_dtype = SF_BF16, bool round_product = false) {
     const Param& W = m->params[w_idx];
     const int H = m->cfg.heads;
     sf_gemm_desc d{};
@@ -351,6 +358,7 @@ int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
     }
     d.workspace = m->gemm_ws;
     d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
+    d.round_product = round_product ? 1 : 0;
     return sf_gemm(&d, s);
 }
 
@@ -450,14 +458,14 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     // self-attention branch
     uint16_t* qkv[3] = {m->q, m->k, m->v};
     const int qk_g[3] = {L.q_norm, L.k_norm, -1};
-    SF_TRY(linear_heads(m, m->n, M, S, L.qkv_w, L.qkv_b, qkv, qk_g, 3, s));
+    SF_TRY(linear_heads(m, m->n, M, S, L.qkv_w, L.qkv_b, qkv, qk_g, 3, s, SF_BF16, true));
     SF_TRY(attention(m, m->q, m->k, m->v, S, nullptr, m->a, false, s));
     SF_TRY(linear_add_norm(m, m->a, SF_BF16, M, L.proj_w, L.proj_b, L.norm2, m->n, SF_BF16, s));
     // cross-attention branch: even blocks attend to language, odd to image
     // (dit_block.cu:369)
     uint16_t* cq[1] = {m->q};
     const int cq_g[1] = {L.cq_norm};
-    SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s));
+    SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s, SF_BF16, true));
     const bool lang = (i % 2) == 0;
     SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? m->cond_lang_rows : c.img_len,
                      lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,

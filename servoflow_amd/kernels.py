@@ -65,9 +65,10 @@ def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat1
 
 
 def gemm_add_norm(a, w, bias, residual, gamma, eps=1e-6, act=abi.SF_ACT_NONE, w_scale=None,
-                  norm_dtype=torch.bfloat16, workspace="auto"):
+                  norm_dtype=torch.bfloat16, workspace="auto", round_product=False):
     """residual (fp32 [M,N]) += act(a w^T + bias); returns
-    rmsnorm(residual) * gamma in norm_dtype."""
+    rmsnorm(residual) * gamma in norm_dtype.  round_product: above 160 rows
+    the branch output is stored in bf16 before the add."""
     M = a.shape[0]
     N = w.shape[0]
     out = torch.empty(M, N, dtype=norm_dtype, device=a.device)
@@ -77,17 +78,21 @@ def gemm_add_norm(a, w, bias, residual, gamma, eps=1e-6, act=abi.SF_ACT_NONE, w_
     d.eps = eps
     d.norm_gamma, d.norm_out = gamma.data_ptr(), out.data_ptr()
     d.norm_ldo, d.norm_dtype = out.stride(0), _DT[norm_dtype]
+    d.round_product = 1 if round_product else 0
     _run(d, a, workspace)
     return out
 
 
 def gemm_heads(a, w, bias, S, H, outs, gammas=(None, None, None), eps=1e-6, w_scale=None,
-               workspace="auto"):
+               workspace="auto", round_product=False):
     """Projection whose N columns are sections of H*64, written per head to
-    outs[j] ([B,H,S,64] bf16 views) with optional per-head RMSNorm."""
+    outs[j] ([B,H,S,64] bf16 views) with optional per-head RMSNorm.
+    round_product: above 160 rows the projection is stored in bf16 before
+    the norm."""
     d = _desc(a, w, bias, abi.SF_ACT_NONE, w_scale)
     d.epilogue = abi.SF_EPI_HEADS
     d.H, d.S, d.eps = H, S, eps
+    d.round_product = 1 if round_product else 0
     for j, o in enumerate(outs):
         d.head_out[j] = o.data_ptr()
         d.head_gamma[j] = _p(gammas[j])

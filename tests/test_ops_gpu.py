@@ -296,6 +296,73 @@ def test_gemm_library_heads_and_add_norm():
     close(host(n), O.rms_norm(x_ref, g2), "norm (library)", rel=1e-4)
 
 
+def _library_weights(seed, N, Kd, w8):
+    if w8:
+        q, s = O.quantize_int8_rows(O.randn(seed, (N, Kd), 0.02))
+        return O.dequant_int8(q, s), dev(q, torch.int8), dev(s, torch.float32)
+    w = rounded(seed, (N, Kd), 0.02)
+    return w, dev(w), None
+
+
+@pytest.mark.parametrize("M,N,Kd,w8,act", [(1072, 2048, 2048, False, abi.SF_ACT_GELU_TANH),
+                                          (1072, 2048, 2048, False, abi.SF_ACT_NONE),
+                                          (2144, 2048, 2048, True, abi.SF_ACT_GELU_TANH),
+                                          (9000, 64, 256, True, abi.SF_ACT_NONE)])
+def test_gemm_library_bf16_out_is_one_rounding(M, N, Kd, w8, act):
+    """M > 160 into a bf16 C: hipBLASLt's bias / GELU_BIAS epilogue (int8
+    row scales as its alpha vector) writes C directly; the result is the
+    fp32 product rounded once to the nearest bf16 (chunks of 8192 rows)."""
+    a = rounded(121 + M, (M, Kd))
+    b = O.randn(123, (N,), 0.02)
+    w, wdev, sdev = _library_weights(122, N, Kd, w8)
+    got = host(K.gemm(dev(a), wdev, dev(b, torch.float32), act, w_scale=sdev))
+    ref = O.linear(a, w, b, act=act)
+    # within half a bf16 ulp of the fp32 result (plus the summation order)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * (2.0 ** -8 + 1e-5) + 1e-6), f"{M}x{N}x{Kd}"
+    # and rounded to nearest: equal to the oracle's rounding but where the
+    # fp32 sums differ across a rounding midpoint
+    same = float(np.mean(got == O.bf16_round(ref)))
+    assert same >= 0.995, f"{M}x{N}x{Kd} w8={w8} act={act}: {same:.4f} equal to round-to-nearest"
+
+
+@pytest.mark.parametrize("w8", [False, True])
+def test_gemm_library_round_product_heads_and_add_norm(w8):
+    """round_product above 160 rows: the per-head RMSNorm and the residual
+    add + RMSNorm read bf16(A.W^T + bias) -- the reference's storage point --
+    instead of the fp32 product (batch-16 QKV and projection shapes)."""
+    B, S, H = 16, 67, 32
+    M = B * S
+    a = rounded(131, (M, 2048))
+    w, wdev, sdev = _library_weights(132, 3 * H * 64, 2048, w8)
+    b = O.randn(133, (3 * H * 64,), 0.02)
+    gq, gk = 1.0 + O.randn(134, (64,), 0.1), 1.0 + O.randn(135, (64,), 0.1)
+    outs = [torch.empty(B, H, S, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3)]
+    K.gemm_heads(dev(a), wdev, dev(b, torch.float32), S, H, outs,
+                 (dev(gq, torch.float32), dev(gk, torch.float32), None), w_scale=sdev, round_product=True)
+    qkv = O.bf16_round(O.linear(a, w, b)).reshape(B, S, 3 * H * 64)
+    Q, Kh, V = O.split_qkv(qkv, H, 64)
+    for got, ref, what in zip(outs, (O.rms_norm(Q, gq), O.rms_norm(Kh, gk), V), "QKV"):
+        g = host(got)
+        # where the two fp32 sums straddle a bf16 midpoint the products
+        # round to neighbours (~3e-4 of them): that input ulp moves a normed
+        # output by up to one more ulp, so two ulps elementwise; everywhere
+        # else the output is the oracle's rounding
+        assert np.all(np.abs(g - ref) <= np.abs(ref) * 2.0 ** -6 + 1e-3), what
+        assert float(np.mean(g == O.bf16_round(ref))) >= 0.995, what
+        assert mean_rel(g, ref) < 2e-3, what
+    # V is the rounded product itself: bit-equal but for summation-order midpoints
+    assert float(np.mean(host(outs[2]) == V)) >= 0.995
+    w2, w2dev, s2dev = _library_weights(136, 2048, 2048, w8)
+    b2, g2 = O.randn(137, (2048,), 0.02), 1.0 + O.randn(138, (2048,), 0.1)
+    x = O.randn(139, (M, 2048))
+    xd = dev(x, torch.float32)
+    n = K.gemm_add_norm(dev(a), w2dev, dev(b2, torch.float32), xd, dev(g2, torch.float32),
+                        w_scale=s2dev, norm_dtype=torch.float32, round_product=True)
+    x_ref = x + O.bf16_round(O.linear(a, w2, b2))
+    close(host(xd), x_ref, "residual (bf16 product)", rel=1e-5)
+    close(host(n), O.rms_norm(x_ref, g2), "norm (bf16 product)", rel=1e-4)
+
+
 @pytest.mark.parametrize("M,N,Kd", [(67, 2048, 2048), (1, 2048, 256), (80, 6144, 2048), (160, 96, 2080),
                                     (67, 2048, 8192), (134, 2048, 2048)])
 @pytest.mark.parametrize("ws", PATHS)

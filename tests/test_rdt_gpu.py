@@ -57,8 +57,10 @@ def bf(x):
 def rb_of(c):
     """The oracle's storage model of the runtime at config c: bf16
     everywhere, except at batch * 67 <= 160 rows the FFN inputs (norm3
-    output, GELU hidden), which the runtime stores in fp16."""
-    return OR.storage_points(c.batch * (c.horizon + 3) <= 160)
+    output, GELU hidden), which the runtime stores in fp16; above 160 rows
+    also the block projections' outputs (the library path's bf16 product)."""
+    rows = c.batch * (c.horizon + 3)
+    return OR.storage_points(rows <= 160, gemm16=rows > 160)
 
 
 def make_condition(c, seed=5, lang_len=None):
