@@ -237,6 +237,9 @@ typedef struct sf_gemm_desc {
     void* workspace;         /* split-K partial sums, or NULL */
     int64_t workspace_bytes;
     int32_t round_product;   /* M > 160, SF_EPI_HEADS / SF_EPI_ADD_NORM: bf16 product (see above) */
+    const void* w_codes16;   /* int8 weights, optional: their codes as bf16 [N][K] (16-byte aligned,
+                                sf_int8_codes_to_bf16); the library path reads this copy instead of
+                                widening the codes itself on every call */
 } sf_gemm_desc;
 
 /* Bytes of workspace the split-K path needs for this shape (0: the shape
@@ -246,11 +249,13 @@ size_t sf_gemm_workspace_bytes(const sf_gemm_desc* desc);
 int sf_gemm(const sf_gemm_desc* desc, void* stream);
 
 /* Setup of the library path (M > 160) for this shape, once per shape and
- * process: the hipBLASLt algorithm is chosen by timing its first 16
- * candidates on scratch buffers of the shape (synchronous: allocates,
- * launches on a private stream, frees).  sf_gemm on a shape never prepared
- * takes hipBLASLt's first candidate without timing.  Call this before
- * capturing a graph that contains the call. */
+ * process: for the fp32 product and the two bf16 products with bias (plain,
+ * GELU) the hipBLASLt algorithm is chosen by timing its first 16
+ * candidates on scratch buffers of the shape, each over weight copies
+ * totalling 320 MB so that the weights stream from HBM as in a model step
+ * (synchronous: allocates, launches on a private stream, frees).  sf_gemm
+ * on a shape never prepared takes hipBLASLt's first candidate without
+ * timing.  Call this before capturing a graph that contains the call. */
 int sf_gemm_prepare(const sf_gemm_desc* desc);
 
 /* ---------------------------------------------------------------------------
@@ -280,6 +285,23 @@ int sf_add_rmsnorm(const void* delta, int32_t delta_dtype, float* residual,
 int sf_dequant_int8(const int8_t* q, const float* scale, int32_t per_channel,
                     void* out, int32_t out_dtype, int64_t N, int64_t K,
                     void* stream);
+
+/* Exact bf16 copies of int8 weight codes (no scale: |code| <= 128 fits
+ * bf16's 8 significant bits), for up to SF_CODES_MAX_JOBS matrices in one
+ * launch: job j widens q [N][ldq] into out [N][K].  The unpack of
+ * dequantize_int8_fp16_kernel (quantization.cu:18-51) without its scale
+ * multiply; the library path of sf_gemm (M > 160) takes such a copy as
+ * w_codes16, so a caller running several int8 projections at a large batch
+ * can widen their weights in one pass instead of one pass per call.  ldq
+ * and K multiples of 16, pointers 16-byte aligned. */
+#define SF_CODES_MAX_JOBS 8
+typedef struct sf_codes_job {
+    const int8_t* q;
+    int64_t ldq;
+    void* out;
+    int32_t N, K;
+} sf_codes_job;
+int sf_int8_codes_to_bf16(const sf_codes_job* jobs, int32_t count, void* stream);
 
 /* Static text for a status code. */
 const char* sf_strerror(int status);

@@ -82,7 +82,18 @@ class GemmDesc(ctypes.Structure):
         ("norm_ldo", ctypes.c_int64), ("norm_dtype", ctypes.c_int32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
         ("round_product", ctypes.c_int32),
+        ("w_codes16", ctypes.c_void_p),
     ]
+
+
+class CodesJob(ctypes.Structure):
+    """Mirror of `sf_codes_job`."""
+
+    _fields_ = [("q", ctypes.c_void_p), ("ldq", ctypes.c_int64), ("out", ctypes.c_void_p),
+                ("N", ctypes.c_int32), ("K", ctypes.c_int32)]
+
+
+SF_CODES_MAX_JOBS = 8
 
 
 class SfError(RuntimeError):
@@ -130,6 +141,8 @@ def lib() -> ctypes.CDLL:
     L.sf_add_rmsnorm.restype = ctypes.c_int
     L.sf_dequant_int8.argtypes = [vp, vp, i32, vp, i32, i64, i64, vp]
     L.sf_dequant_int8.restype = ctypes.c_int
+    L.sf_int8_codes_to_bf16.argtypes = [ctypes.POINTER(CodesJob), i32, vp]
+    L.sf_int8_codes_to_bf16.restype = ctypes.c_int
     L.sf_strerror.argtypes = [ctypes.c_int]
     L.sf_strerror.restype = ctypes.c_char_p
     _lib = L

@@ -26,6 +26,7 @@
 #include <cmath>
 #include <cstdint>
 #include <algorithm>
+#include <array>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -75,6 +76,11 @@ struct LayerIdx {
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// The projection weights a block's forward multiplies by.
+std::array<int, 6> block_weights(const LayerIdx& L) {
+    return {L.qkv_w, L.proj_w, L.cq_w, L.cproj_w, L.fc1_w, L.fc2_w};
+}
+
 }  // namespace
 
 struct sf_rdt {
@@ -120,6 +126,13 @@ struct sf_rdt {
     size_t attn_ws_bytes = 0;
     void* gemm_ws = nullptr;       // split-K partial sums, shared by the stream's GEMMs
     size_t gemm_ws_bytes = 0;
+    // int8 models above 160 rows (the library path): the current block's six
+    // projection weights widened to bf16 codes in one launch at the block's
+    // start (sf_int8_codes_to_bf16), instead of one widening pass per GEMM;
+    // codes16_of[param] points at a weight's copy while its block runs.
+    char* codes16 = nullptr;
+    size_t codes16_bytes = 0;
+    std::vector<const void*> codes16_of;
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -276,6 +289,7 @@ int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, i
     d.ldw = W.shape[1];
     d.w_dtype = W.dtype;
     d.w_scale = W.scale;
+    d.w_codes16 = m->codes16_of[w_idx];
     d.bias = b_idx >= 0 ? pf(m, b_idx) : nullptr;
     d.act = act;
     d.epilogue = SF_EPI_PLAIN;
@@ -307,6 +321,7 @@ int linear_add_norm(sf_rdt* m, const void* A, int a_dtype, int M, int w_idx, int
     d.ldw = W.shape[1];
     d.w_dtype = W.dtype;
     d.w_scale = W.scale;
+    d.w_codes16 = m->codes16_of[w_idx];
     d.bias = pf(m, b_idx);
     d.epilogue = SF_EPI_ADD_NORM;
     d.C = m->x;
@@ -344,6 +359,7 @@ int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
     d.ldw = W.shape[1];
     d.w_dtype = W.dtype;
     d.w_scale = W.scale;
+    d.w_codes16 = m->codes16_of[w_idx];
     d.bias = pf(m, b_idx);
     d.epilogue = SF_EPI_HEADS;
     d.H = H;
@@ -455,6 +471,25 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     const LayerIdx& L = m->layers[i];
     const int D = c.hidden, S = c.horizon + 3, M = c.batch * S;
     const int fd = m->ffn_dtype;
+    if (m->codes16) {   // int8 weights above 160 rows: widen the block's six in one pass
+        sf_codes_job jobs[6];
+        int n = 0;
+        char* dst = m->codes16;
+        for (int w : block_weights(L)) {
+            const Param& P = m->params[w];
+            m->codes16_of[w] = nullptr;
+            if (P.dtype != SF_I8) continue;
+            jobs[n].q = static_cast<const int8_t*>(P.data);
+            jobs[n].ldq = P.shape[1];
+            jobs[n].out = dst;
+            jobs[n].N = (int32_t)P.shape[0];
+            jobs[n].K = (int32_t)P.shape[1];
+            m->codes16_of[w] = dst;
+            dst += align256((size_t)P.shape[0] * P.shape[1] * 2);
+            ++n;
+        }
+        SF_TRY(sf_int8_codes_to_bf16(jobs, n, s));
+    }
     // self-attention branch
     uint16_t* qkv[3] = {m->q, m->k, m->v};
     const int qk_g[3] = {L.q_norm, L.k_norm, -1};
@@ -660,6 +695,16 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     bufs.push_back({&m->attn_ws, std::max<size_t>(m->attn_ws_bytes, 256)});
     m->gemm_ws_bytes = gemm_ws_for(m, false, nullptr);
     bufs.push_back({&m->gemm_ws, std::max<size_t>(m->gemm_ws_bytes, 256)});
+    if (S * B > 160) {
+        for (const LayerIdx& L : m->layers) {
+            size_t bytes = 0;
+            for (int w : block_weights(L))
+                if (m->params[w].dtype == SF_I8)
+                    bytes += align256((size_t)m->params[w].shape[0] * m->params[w].shape[1] * 2);
+            m->codes16_bytes = std::max(m->codes16_bytes, bytes);
+        }
+        if (m->codes16_bytes) bufs.push_back({(void**)&m->codes16, m->codes16_bytes});
+    }
     std::vector<size_t> boff(bufs.size());
     for (size_t i = 0; i < bufs.size(); ++i) {
         boff[i] = off;
@@ -675,6 +720,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
         if (p.dtype == SF_I8) p.scale = reinterpret_cast<float*>(m->arena + p.scale_offset);
     }
     for (size_t i = 0; i < bufs.size(); ++i) *bufs[i].ptr = m->arena + boff[i];
+    m->codes16_of.assign(m->params.size(), nullptr);
     m->exact_pv.assign(c.layers, 0);
     m->lang_rows = m->cond_lang_rows = c.lang_max;
     if (hipStreamCreate(&m->own_stream) != hipSuccess) {

@@ -49,14 +49,17 @@ def workspace_bytes(a, w):
 
 
 def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat16,
-         accumulate=False, w_scale=None, workspace="auto"):
+         accumulate=False, w_scale=None, workspace="auto", w_codes16=None):
     """out[M,N] = act(a[M,K] w[N,K]^T + bias) (bf16 a; bf16 or int8 w with
-    per-row fp32 w_scale).  accumulate adds into an fp32 `out`."""
+    per-row fp32 w_scale).  accumulate adds into an fp32 `out`.  w_codes16:
+    int8 w's codes as bf16 (int8_codes_to_bf16), read by the library path
+    instead of widening them."""
     M, K = a.shape
     N = w.shape[0]
     if out is None:
         out = torch.empty(M, N, dtype=out_dtype, device=a.device)
     d = _desc(a, w, bias, act, w_scale)
+    d.w_codes16 = _p(w_codes16)
     d.epilogue = abi.SF_EPI_PLAIN
     d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), _DT[out.dtype]
     d.accumulate = 1 if accumulate else 0
@@ -98,6 +101,19 @@ def gemm_heads(a, w, bias, S, H, outs, gammas=(None, None, None), eps=1e-6, w_sc
         d.head_gamma[j] = _p(gammas[j])
         d.head_stride[j][:] = (o.stride(0), o.stride(1), o.stride(2))
     _run(d, a, workspace)
+    return outs
+
+
+def int8_codes_to_bf16(qs):
+    """bf16 copies [N][K] of the codes of int8 matrices (row-strided views
+    allowed), all in one launch (at most abi.SF_CODES_MAX_JOBS)."""
+    outs = [torch.empty(q.shape[0], q.shape[1], dtype=torch.bfloat16, device=q.device) for q in qs]
+    jobs = (abi.CodesJob * max(1, len(qs)))()
+    for j, (q, o) in enumerate(zip(qs, outs)):
+        jobs[j].q, jobs[j].ldq, jobs[j].out = q.data_ptr(), q.stride(0), o.data_ptr()
+        jobs[j].N, jobs[j].K = q.shape[0], q.shape[1]
+    st = abi.lib().sf_int8_codes_to_bf16(jobs, len(qs), _stream(qs[0]) if qs else None)
+    abi.check(st, "sf_int8_codes_to_bf16")
     return outs
 
 

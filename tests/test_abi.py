@@ -179,3 +179,21 @@ def test_auto_split_partials_fit_the_noalloc_scratch():
                     d = abi.attn_desc_bhsd(B, H, Sq, Sk)
                     worst = max(worst, abi.lib().sf_attn_workspace_bytes(ctypes.byref(d)))
     assert 0 < worst <= abi.SF_ATTN_NOALLOC_SCRATCH_BYTES
+
+
+def test_int8_codes_to_bf16_rejects_bad_jobs():
+    """Argument checks of the batched code widening, before any launch:
+    too many jobs, K or the row stride not a multiple of 16, misaligned
+    pointers, stride below K."""
+    lib = abi.lib()
+    jobs = (abi.CodesJob * (abi.SF_CODES_MAX_JOBS + 1))()
+    for j in jobs:
+        j.q, j.ldq, j.out, j.N, j.K = 256, 64, 512, 4, 64
+    assert lib.sf_int8_codes_to_bf16(jobs, 0, None) == abi.SF_OK
+    assert lib.sf_int8_codes_to_bf16(jobs, abi.SF_CODES_MAX_JOBS + 1, None) == abi.SF_EINVAL
+    assert lib.sf_int8_codes_to_bf16(jobs, -1, None) == abi.SF_EINVAL
+    for field, bad in (("K", 40), ("ldq", 72), ("ldq", 48), ("q", 264), ("out", 520), ("N", -1)):
+        one = (abi.CodesJob * 1)()
+        one[0].q, one[0].ldq, one[0].out, one[0].N, one[0].K = 256, 64, 512, 4, 64
+        setattr(one[0], field, bad)
+        assert lib.sf_int8_codes_to_bf16(one, 1, None) == abi.SF_EINVAL, (field, bad)

@@ -325,6 +325,59 @@ def test_gemm_library_bf16_out_is_one_rounding(M, N, Kd, w8, act):
     assert same >= 0.995, f"{M}x{N}x{Kd} w8={w8} act={act}: {same:.4f} equal to round-to-nearest"
 
 
+def test_int8_codes_to_bf16_batched_and_exact():
+    """Several int8 matrices (one row-strided) widened in one launch: every
+    code exactly, nothing past each matrix's K columns read into the copy."""
+    shapes = [(6144, 2048), (2048, 2048), (64, 256), (2048, 8192)]
+    qs, views = [], []
+    for j, (N, Kd) in enumerate(shapes):
+        pad = 16 if j == 2 else 0
+        q = np.random.default_rng(40 + j).integers(-128, 128, size=(N, Kd + pad), dtype=np.int8)
+        qs.append(q[:, :Kd])
+        views.append(dev(q, torch.int8)[:, :Kd])
+    outs = K.int8_codes_to_bf16(views)
+    for q, o in zip(qs, outs):
+        assert np.array_equal(host(o), q.astype(np.float32))
+
+
+@pytest.mark.parametrize("epilogue", ["plain", "heads", "add_norm"])
+def test_gemm_library_int8_codes16_equals_internal_widening(epilogue):
+    """w_codes16 (the caller's widened copy) gives bit-identical results to
+    the library path widening the codes itself."""
+    M, N, Kd = 1072, 2048, 2048
+    a = rounded(141, (M, Kd))
+    q, s = O.quantize_int8_rows(O.randn(142, (N, Kd), 0.02))
+    qd, sd = dev(q, torch.int8), dev(s, torch.float32)
+    codes = K.int8_codes_to_bf16([qd])[0]
+    b = dev(O.randn(143, (N,), 0.02), torch.float32)
+    ad = dev(a)     # kept alive: the descriptors below hold raw pointers
+    res = []
+    for c16 in (None, codes):
+        if epilogue == "plain":
+            res.append(host(K.gemm(ad, qd, b, abi.SF_ACT_GELU_TANH, w_scale=sd, w_codes16=c16)))
+        elif epilogue == "heads":
+            outs = [torch.empty(16, 32, 67, 64, device=DEV, dtype=torch.bfloat16)]
+            d = K._desc(ad, qd, b, abi.SF_ACT_NONE, sd)
+            d.w_codes16 = K._p(c16)
+            d.epilogue, d.H, d.S, d.eps, d.round_product = abi.SF_EPI_HEADS, 32, 67, 1e-6, 1
+            d.head_out[0] = outs[0].data_ptr()
+            d.head_stride[0][:] = (outs[0].stride(0), outs[0].stride(1), outs[0].stride(2))
+            K._run(d, ad, "auto")
+            res.append(host(outs[0]))
+        else:
+            xd = dev(O.randn(144, (M, N)), torch.float32)
+            d = K._desc(ad, qd, b, abi.SF_ACT_NONE, sd)
+            d.w_codes16 = K._p(c16)
+            out = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+            g = dev(np.ones(N, np.float32), torch.float32)
+            d.epilogue, d.C, d.ldc, d.c_dtype, d.eps = abi.SF_EPI_ADD_NORM, xd.data_ptr(), N, abi.SF_F32, 1e-6
+            d.norm_gamma, d.norm_out, d.norm_ldo, d.norm_dtype = g.data_ptr(), out.data_ptr(), N, abi.SF_BF16
+            d.round_product = 1
+            K._run(d, ad, "auto")
+            res.append(np.concatenate([host(xd), host(out)]))
+    assert np.array_equal(res[0], res[1]), epilogue
+
+
 @pytest.mark.parametrize("w8", [False, True])
 def test_gemm_library_round_product_heads_and_add_norm(w8):
     """round_product above 160 rows: the per-head RMSNorm and the residual
