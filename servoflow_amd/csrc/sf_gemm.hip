@@ -496,6 +496,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
 struct EpiArgs {
     const float* part;     // [splits][M][N]
     const uint16_t* part16;  // or the library path's bf16 product [M][N], bias and scale already in
+    int heads16;             // heads outputs take 16-byte stores (8-aligned head_out, strides)
     int splits;
     int M, N;
     int64_t m_off;         // row of the outputs that partial row 0 belongs to
@@ -638,6 +639,51 @@ __global__ __launch_bounds__(256) void reduce_heads_kernel(const EpiArgs e) {
     const int64_t s = mg % e.S;
     uint16_t* o = e.head_out[sec] + b * e.head_sb[sec] + h * e.head_sh[sec] + s * e.head_ss[sec] + d;
     *reinterpret_cast<uint2*>(o) = pack_bf16x4(v);
+}
+
+// Per-head epilogue over the library path's bf16 product (bias and scale
+// already in it): 8 lanes per (row, head), 8 columns each, so every lane
+// moves 16 bytes each way; 256 threads = 32 rows x one 64-column head.
+__global__ __launch_bounds__(256) void heads16_kernel(const EpiArgs e) {
+    const int ntl = e.N / 64;
+    const int m = (int)(blockIdx.x / ntl) * 32 + (int)(threadIdx.x >> 3);
+    const int n = 64 * (int)(blockIdx.x % ntl) + 8 * (int)(threadIdx.x & 7);
+    if (m >= e.M) return;   // whole 8-lane groups
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(e.part16 + (int64_t)m * e.N + n);
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[2 * j] = bf16_bits_to_f32(raw[j] & 0xffffu);
+        v[2 * j + 1] = bf16_bits_to_f32(raw[j] >> 16);
+    }
+    const int cols = e.H * 64;
+    const int sec = n / cols;
+    const int h = (n % cols) / 64;
+    const int d = n % 64;
+    const float* gamma = e.head_gamma[sec];
+    if (gamma) {
+        const f32x4 g0 = *reinterpret_cast<const f32x4*>(gamma + d);
+        const f32x4 g1 = *reinterpret_cast<const f32x4*>(gamma + d + 4);
+        // rms_norm_kernel_impl over the 64 head dims (norm.cuh:89-122)
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+        ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0xB1, 0xF, 0xF, true));   // quad_perm 1,0,3,2
+        ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0x4E, 0xF, 0xF, true));   // quad_perm 2,3,0,1
+        ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0x141, 0xF, 0xF, true));  // row_half_mirror
+        const float inv_rms = 1.f / sqrtf(ss / 64.f + e.eps);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = v[j] * inv_rms * g0[j];
+            v[4 + j] = v[4 + j] * inv_rms * g1[j];
+        }
+    }
+    const int64_t mg = e.m_off + m;
+    const int64_t b = mg / e.S;
+    const int64_t s = mg % e.S;
+    uint16_t* o = e.head_out[sec] + b * e.head_sb[sec] + h * e.head_sh[sec] + s * e.head_ss[sec] + d;
+    *reinterpret_cast<u32x4*>(o) =
+        u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
 }
 
 // One workgroup of 512 threads per row: x[m] += result[m];
@@ -827,7 +873,9 @@ template <int NS>
 void launch_reduce(const sf_gemm_desc* d, const EpiArgs& e, hipStream_t s) {
     const int64_t quads = (int64_t)e.M * e.N / 4;
     const unsigned tiles = (unsigned)((int64_t)(e.N / 64) * ((e.M + 15) / 16));
-    if (d->epilogue == SF_EPI_HEADS)
+    if (d->epilogue == SF_EPI_HEADS && e.part16 && e.heads16)
+        hipLaunchKernelGGL(heads16_kernel, dim3((unsigned)((int64_t)(e.N / 64) * ((e.M + 31) / 32))), dim3(256), 0, s, e);
+    else if (d->epilogue == SF_EPI_HEADS)
         hipLaunchKernelGGL(reduce_heads_kernel<NS>, dim3(tiles), dim3(256), 0, s, e);
     else if (d->epilogue == SF_EPI_ADD_NORM)
         hipLaunchKernelGGL(reduce_addnorm_kernel<NS>, dim3(e.M), dim3(kAddNormThreads), 0, s, e);
@@ -1151,10 +1199,14 @@ int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
         if (d->H <= 0 || d->S <= 0) return SF_EINVAL;   // row m -> (m / S, m % S); a partial last element is fine
         const int cols = d->H * 64;
         if (d->N % cols || d->N / cols > 3) return SF_EINVAL;
+        e.heads16 = 1;
         for (int j = 0; j < d->N / cols; ++j) {
             if (!d->head_out[j] || !al8(d->head_out[j])) return SF_EINVAL;
-            for (int q = 0; q < 3; ++q)
+            if (!al16(d->head_out[j])) e.heads16 = 0;
+            for (int q = 0; q < 3; ++q) {
                 if (d->head_stride[j][q] & 3) return SF_EINVAL;
+                if (d->head_stride[j][q] & 7) e.heads16 = 0;
+            }
             e.head_out[j] = static_cast<uint16_t*>(d->head_out[j]);
             e.head_gamma[j] = d->head_gamma[j];
             e.head_sb[j] = d->head_stride[j][0];

@@ -378,6 +378,31 @@ def test_gemm_library_int8_codes16_equals_internal_widening(epilogue):
     assert np.array_equal(res[0], res[1]), epilogue
 
 
+@pytest.mark.parametrize("row_stride", [64, 68])
+def test_gemm_library_round_product_heads_layouts(row_stride):
+    """round_product heads at 300 rows into outputs with a 64-element row
+    (16-byte stores, 8 lanes per head row) and a 68-element row (8-byte
+    stores, the 16-lane kernel): both equal the norm of the rounded product."""
+    B, S, H = 3, 100, 2
+    M = B * S
+    a = rounded(151, (M, 512))
+    w = rounded(152, (2 * H * 64, 512), 0.05)
+    b = O.randn(153, (2 * H * 64,), 0.02)
+    gk = 1.0 + O.randn(154, (64,), 0.1)
+    bufs = [torch.zeros(B, H, S, row_stride, device=DEV, dtype=torch.bfloat16) for _ in range(2)]
+    outs = [t[..., :64] for t in bufs]
+    K.gemm_heads(dev(a), dev(w), dev(b, torch.float32), S, H, outs, (dev(gk, torch.float32), None),
+                 round_product=True)
+    kv = O.bf16_round(O.linear(a, w, b)).reshape(B, S, 2 * H * 64)
+    Kh, V = O.split_kv(kv, H, 64)
+    for got, ref, buf in zip(outs, (O.rms_norm(Kh, gk), V), bufs):
+        g = host(got)
+        assert np.all(np.abs(g - ref) <= np.abs(ref) * 2.0 ** -6 + 1e-3)
+        assert float(np.mean(g == O.bf16_round(ref))) >= 0.995
+        if row_stride > 64:
+            assert not host(buf[..., 64:]).any()        # the padding columns untouched
+
+
 @pytest.mark.parametrize("w8", [False, True])
 def test_gemm_library_round_product_heads_and_add_norm(w8):
     """round_product above 160 rows: the per-head RMSNorm and the residual
