@@ -147,9 +147,10 @@ def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=Fals
 
 def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
     """Graph-timed block projection C[M,N] = A[M,K] W[N,K]^T + bias through
-    sf_gemm with a caller workspace (split-K kernel + reduce for M <= 160,
-    hipBLASLt product + reduce above; the shape is prepared first, as the
-    model runtime does).  The graph's calls cycle through distinct weight
+    sf_gemm with a caller workspace (split-K kernel + reduce for M <= 160;
+    above, hipBLASLt writes the bf16 C with its bias epilogue, int8 codes
+    widened first and their row scales as its alpha vector; the shape is
+    prepared first, as the model runtime does).  The graph's calls cycle through distinct weight
     copies totalling >= COLD_SET_BYTES (at most 64 calls), so weights stream
     from HBM as in the loop, where each is read once per step.  epilogue:
     "plain" (bf16 out) or "addnorm" (fp32 residual += product, then RMSNorm
@@ -484,8 +485,8 @@ def profile_mfma():
     """Runs only what the MFMA-utilisation profile measures, through the same
     graph-timed functions the bench line uses: the batch-1 self-attention op
     (attn_short_kernel, 1x32x67x67x64) and the block projections of
-    GEMM_SHAPES (split-K kernel + reduce at M = 67, hipBLASLt + reduce
-    above)."""
+    GEMM_SHAPES (split-K kernel + reduce at M = 67, hipBLASLt with its bias
+    epilogue above)."""
     r = bench_attention(1, 67, steps=5, warmup=1)
     print(f"profile: self-attention 1x32x67x67x64, graph-timed {r['us']:.2f} us per op", flush=True)
     for name, M, N, K, int8 in GEMM_SHAPES:
@@ -505,6 +506,8 @@ def main():
                     help="run only the roofline op and the copy calibration kernel (for rocprofv3)")
     ap.add_argument("--profile-mfma", action="store_true",
                     help="run only the self-attention op and the projection GEMMs (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-loop", choices=["b16", "b32int8"],
+                    help="build one large-batch model and replay its loop 3 times (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -520,6 +523,13 @@ def main():
         return
     if args.profile_mfma:
         profile_mfma()
+        return
+    if args.profile_loop:
+        B, int8 = (16, False) if args.profile_loop == "b16" else (32, True)
+        m, _ = make_model(B, int8=int8)
+        ms = bench_loop(m, 3, 1)
+        print(f"profile: loop batch {B}{' int8' if int8 else ''}: {ms:.3f} ms", flush=True)
+        m.close()
         return
     extra = {}
     # ---- headline: batch-1 loop (config 4)
