@@ -760,17 +760,29 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
 // key order matches the P^T slots the S^T accumulator provides.
 // ---------------------------------------------------------------------------
 constexpr int kShortMaxKeys = 128;
+// B*H range in which a workgroup takes all of a head's query blocks, one
+// wave each.  Same-box A/B on 1x..x32x67x67: 6.8 vs 7.9 us at B*H = 256,
+// 11.3 vs 11.5 at 512, but 20.9 vs 19.4 at 1024 (one-wave workgroups keep
+// more waves in flight per CU there), so 256 <= B*H < 1024.
+constexpr long kShortGroupMinHeads = 256;
+constexpr long kShortGroupMaxHeads = 1024;
 constexpr int kVPitch = 80;   // LDS row pitch of V (bf16): 160 B keeps the four rows of a read apart
 
-template <int KB, bool kF16>   // 16-key blocks covering Sk (even, <= 8); fp16 (else bf16) Q/K/V
-__global__ __launch_bounds__(64) void attn_short_kernel(const AttnArgs a) {
+// NW query blocks per workgroup, one wave each: 1 spreads a small batch's
+// few heads over the most CUs; 5 (large batches) runs a head's 67 queries on
+// one CU, so its K and V come from L2 once and the other waves hit in L1.
+template <int KB, bool kF16, int NW>   // 16-key blocks covering Sk (even, <= 8); fp16 (else bf16) Q/K/V
+__global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
     using v8 = typename In16<kF16>::v8;
     constexpr int KROWS = 16 * KB;
-    __shared__ __attribute__((aligned(16))) uint16_t vl[KROWS * kVPitch];
-    const int lane = threadIdx.x;
+    __shared__ __attribute__((aligned(16))) uint16_t vls[NW][KROWS * kVPitch];
+    const int lane = threadIdx.x & 63;
+    const int w = NW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
+    uint16_t* vl = vls[w];
     const int g = lane >> 4;
     const int r = lane & 15;
-    const int q0 = 16 * blockIdx.x;
+    const int q0 = 16 * ((int)blockIdx.x * NW + w);
+    if (q0 >= a.Sq) return;   // no barrier below: a wave past the queries just ends
     const int h = blockIdx.y;
     const int b = blockIdx.z;
 
@@ -1068,6 +1080,22 @@ int choose_splits(const sf_attn_desc* d) {
     return (int)ns;
 }
 
+template <int NW>
+void launch_short(bool f16, int kb, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
+    const dim3 block(64 * NW);
+    if (f16) {
+        if (kb <= 2) hipLaunchKernelGGL((sfk::attn_short_kernel<2, true, NW>), grid, block, 0, s, a);
+        else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, true, NW>), grid, block, 0, s, a);
+        else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, true, NW>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((sfk::attn_short_kernel<8, true, NW>), grid, block, 0, s, a);
+    } else {
+        if (kb <= 2) hipLaunchKernelGGL((sfk::attn_short_kernel<2, false, NW>), grid, block, 0, s, a);
+        else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, false, NW>), grid, block, 0, s, a);
+        else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, false, NW>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((sfk::attn_short_kernel<8, false, NW>), grid, block, 0, s, a);
+    }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int validate(const sf_attn_desc* d) {
@@ -1226,19 +1254,16 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         if ((long)ns * qblocks > 0x7fffffffL) return SF_ENOTSUP;
         hipLaunchKernelGGL(sfk::attn_f32_kernel, dim3((unsigned)(ns * qblocks), d->H, d->B), dim3(64), 0, s, a);
     } else if (short_keys) {
-        const dim3 grid((d->Sq + 15) / 16, d->H, d->B);
+        const int qb = (d->Sq + 15) / 16;
         const int kb = ((d->Sk + 31) / 32) * 2;
-        if (f16) {
-            if (kb <= 2) hipLaunchKernelGGL((sfk::attn_short_kernel<2, true>), grid, dim3(64), 0, s, a);
-            else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, true>), grid, dim3(64), 0, s, a);
-            else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, true>), grid, dim3(64), 0, s, a);
-            else hipLaunchKernelGGL((sfk::attn_short_kernel<8, true>), grid, dim3(64), 0, s, a);
-        } else {
-            if (kb <= 2) hipLaunchKernelGGL((sfk::attn_short_kernel<2, false>), grid, dim3(64), 0, s, a);
-            else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, false>), grid, dim3(64), 0, s, a);
-            else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, false>), grid, dim3(64), 0, s, a);
-            else hipLaunchKernelGGL((sfk::attn_short_kernel<8, false>), grid, dim3(64), 0, s, a);
-        }
+        // one wave per query block while B*H*blocks leaves CUs idle; five
+        // per workgroup once B*H alone fills the chip (up to the bound)
+        const long bh = (long)d->B * d->H;
+        const bool grouped = bh >= sfk::kShortGroupMinHeads && bh < sfk::kShortGroupMaxHeads;
+        if (grouped)
+            launch_short<5>(f16, kb, dim3((qb + 4) / 5, d->H, d->B), s, a);
+        else
+            launch_short<1>(f16, kb, dim3(qb, d->H, d->B), s, a);
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
     } else {
         const dim3 grid(ns * nqc, d->H, d->B);

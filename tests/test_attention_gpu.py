@@ -400,3 +400,30 @@ def test_long_keys_and_many_query_chunks(B, H, Sq, Sk):
     q, k, v = rounded(191, (B, H, Sq, 64)), rounded(192, (B, H, Sk, 64)), rounded(193, (B, H, Sk, 64))
     got = run(q, k, v)
     assert_close_bf16(got, O.attention_f32(q, k, v), f"long {B},{H},{Sq},{Sk}")
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,causal,vl,dt", [(8, 32, 67, 67, False, None, torch.bfloat16),
+                                                    (16, 32, 67, 67, False, None, torch.bfloat16),
+                                                    (32, 32, 67, 67, False, None, torch.bfloat16),
+                                                    (8, 32, 81, 100, True, "rand", torch.bfloat16),
+                                                    (4, 64, 67, 67, False, "rand", torch.float16)])
+def test_short_keys_grouped_waves(B, H, Sq, Sk, causal, vl, dt):
+    """Short key sets at 256 <= B*H < 1024 run a head's query blocks as the
+    waves of one workgroup (B*H = 1024 one wave per workgroup again):
+    against the oracle, and bit-identical to the same heads run one batch
+    element at a time (one wave per workgroup)."""
+    q, k, v = rounded(241, (B, H, Sq, 64)), rounded(242, (B, H, Sk, 64)), rounded(243, (B, H, Sk, 64))
+    lens = None if vl is None else np.random.default_rng(244).integers(1, Sk + 1, size=B).astype(np.int32)
+    kw = {"is_causal": causal}
+    dq, dk, dv = (to_dev(x, dt) for x in (q, k, v))
+    full = attention(dq, dk, dv, out_dtype=torch.float32,
+                     valid_len=None if lens is None else to_dev(lens, torch.int32), **kw)
+    torch.cuda.synchronize()
+    got = full.float().cpu().numpy()
+    ref = O.attention_f32(q, k, v, causal=causal, valid_len=lens)
+    assert_close_bf16(got, ref, f"grouped short keys {B},{H},{Sq},{Sk}")
+    for b in range(B):
+        one = attention(dq[b:b + 1], dk[b:b + 1], dv[b:b + 1], out_dtype=torch.float32,
+                        valid_len=None if lens is None else to_dev(lens[b:b + 1], torch.int32), **kw)
+        torch.cuda.synchronize()
+        assert np.array_equal(one.float().cpu().numpy()[0], got[b]), b
