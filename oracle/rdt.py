@@ -30,7 +30,9 @@ hidden, "emb" timestep-embedding inputs, "adapt" adaptor inputs / hidden,
 per-head norm or the residual add (qkv, cross q, attention / cross proj,
 fc2; the bf16 outputs of the reference's cuBLASLt epilogues,
 cuda_backend.cu:414-447), which the MI355X runtime stores in bf16 above 160
-rows (storage_points(gemm16=True)).
+rows (storage_points(gemm16=True)), "kvgemm" the cross K/V projection's
+output before split_kv / k_norm (dit_block.cu:291-308), rounded when the
+projection has more than 160 rows (the runtime's library path).
 """
 from __future__ import annotations
 
@@ -62,7 +64,7 @@ class RdtConfig:
         return self.horizon + 3
 
 
-ALL_POINTS = frozenset({"cond", "kv", "n1", "qkv", "a", "n2", "n3", "h", "emb", "adapt", "state"})
+ALL_POINTS = frozenset({"cond", "kv", "kvgemm", "n1", "qkv", "a", "n2", "n3", "h", "emb", "adapt", "state"})
 
 
 def storage_points(ffn16, gemm16=False):
@@ -107,6 +109,8 @@ def cross_kv(p, i, cond, cfg, rb=True):
     pre = f"blocks.{i}.cross_attn."
     B, Sc, D = cond.shape
     kv = O.linear(cond, p[pre + "kv.weight"], p[pre + "kv.bias"]).reshape(B, Sc, 2 * D)
+    if B * Sc > 160:   # the runtime's library path stores this product in bf16
+        kv = _r(kv, rb, "kvgemm")
     K, V = O.split_kv(kv, cfg.heads, 64)
     K = O.rms_norm(K, p[pre + "k_norm.weight"], cfg.eps)
     return _r(K, rb, "kv"), _r(V, rb, "kv")

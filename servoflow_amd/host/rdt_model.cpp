@@ -340,9 +340,8 @@ int linear_add_norm(sf_rdt* m, const void* A, int a_dtype, int M, int w_idx, int
 
 // Per-head projection: sections of H*64 columns -> [B, H, S, 64] bf16.
 // round_product: above 160 rows the projection is stored in bf16 before the
-// per-head RMSNorm, as the reference's qkv / q projection output is
-// (dit_block.cu:207, 284); the once-per-inference K/V cache projection keeps
-// its fp32 product.
+// per-head RMSNorm, as the reference's qkv / q / kv projection output is
+// (dit_block.cu:207, 284, 291).
 int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
                  uint16_t* const* outs, const int* gamma_idx, int nsec, hipStream_t s,
                  int a_dtype = SF_BF16, bool round_product = false) {
@@ -868,8 +867,11 @@ extern "C" int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t
         const int rows = lang && B == 1 ? Lr : B * Sc;   // batch 1: the L language rows only
         uint16_t* kv[2] = {m->ck[i], m->cv[i]};
         const int g[2] = {m->layers[i].ck_norm, -1};
+        // above 160 rows the projection is stored in bf16 before split_kv /
+        // k_norm, as the reference's kv = gemm_bias_act(...) is
+        // (dit_block.cu:291-308)
         SF_TRY(linear_heads(m, lang ? m->lang_c : m->img_c, rows, Sc, m->layers[i].ckv_w,
-                            m->layers[i].ckv_b, kv, g, 2, s));
+                            m->layers[i].ckv_b, kv, g, 2, s, SF_BF16, true));
     }
     // each layer's max |V| for the choice of P.V form (resolve_pv_forms)
     if (c.layers > 0) {

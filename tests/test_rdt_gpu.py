@@ -142,7 +142,12 @@ def test_kv_cache_matches_oracle():
             got = m.cache_numpy(i, wv)
             ref = caches[i][wv]
             assert mean_rel(got, ref) < 2e-3, (i, wv)
-            assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-3), (i, wv)
+            # above 160 rows both sides round the projection to bf16 before
+            # k_norm; where the fp32 sums straddle a midpoint the rounded
+            # inputs differ by an ulp, which k_norm carries into the output:
+            # two ulps elementwise, and the oracle's value almost everywhere
+            assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -6 + 1e-3), (i, wv)
+            assert float(np.mean(got == ref)) >= 0.99, (i, wv)
 
 
 @pytest.mark.parametrize("int8", [0, 1])
@@ -273,9 +278,12 @@ def test_lang_rows_reads_only_the_first_rows():
     keys.  NaN rows past L are therefore never read -- the V range check of
     the language layer still sees finite (zeroed) cache rows and keeps the
     fp16 P.V form -- and the step equals a model given the same rows with
-    lang_len = L (lang_len past L is clamped to L keys)."""
-    c = small_cfg(batch=1, lang_max=192)
-    L = 100
+    lang_len = L (lang_len past L is clamped to L keys).  160 padded rows
+    and L = 140 keep both models on the same kernels: the split-K GEMM path
+    (row results independent of the row count) and the key-split attention
+    (above 128 keys) with the splits of the 160-row buffer."""
+    c = small_cfg(batch=1, lang_max=160)
+    L = 140
     lang, _, img, state = make_condition(c, lang_len=[L])
     x_t = torch.from_numpy(O.randn(98, (1, c.horizon, c.action_dim))).to(DEV)
     m_full = build(c)
@@ -301,8 +309,10 @@ def test_lang_rows_infer_reencodes_and_recaptures():
     id, and the captured loop is rebuilt for the new key count: the result
     equals a fresh model fed the padded tokens masked to L (the adaptor runs
     over the L rows only, so NaN token rows past L never reach it), and going
-    back to all rows reproduces the first result bit for bit."""
-    c = small_cfg(batch=1, lang_max=192)
+    back to all rows reproduces the first result bit for bit.  160 padded
+    rows and 140 kept keep both models on the same GEMM and attention
+    kernels."""
+    c = small_cfg(batch=1, lang_max=160)
     lt = O.bf16_round(O.randn(61, (1, c.lang_max, c.lang_token_dim)))
     it = bf(O.bf16_round(O.randn(62, (1, c.img_len, c.img_token_dim))))
     st = bf(O.bf16_round(O.randn(63, (1, c.state_dim))))
@@ -310,14 +320,14 @@ def test_lang_rows_infer_reencodes_and_recaptures():
     m = build(c)
     a_full, e0 = m.infer(1, bf(lt), ll_all, it, st, noise_seed=5)
     assert e0
-    m.set_lang_rows(120)
+    m.set_lang_rows(140)
     lt_nan = lt.copy()
-    lt_nan[:, 120:] = np.nan
-    a_120, e1 = m.infer(1, bf(lt_nan), ll_all, it, st, noise_seed=5)
-    assert e1 and np.isfinite(a_120).all() and not np.array_equal(a_120, a_full)
+    lt_nan[:, 140:] = np.nan
+    a_140, e1 = m.infer(1, bf(lt_nan), ll_all, it, st, noise_seed=5)
+    assert e1 and np.isfinite(a_140).all() and not np.array_equal(a_140, a_full)
     m2 = build(c)
-    a_ref, _ = m2.infer(1, bf(lt), torch.tensor([120], dtype=torch.int32, device=DEV), it, st, noise_seed=5)
-    assert mean_rel(a_120, a_ref) < 2e-3
+    a_ref, _ = m2.infer(1, bf(lt), torch.tensor([140], dtype=torch.int32, device=DEV), it, st, noise_seed=5)
+    assert mean_rel(a_140, a_ref) < 2e-3
     m.set_lang_rows(c.lang_max)
     a_back, e2 = m.infer(1, bf(lt), ll_all, it, st, noise_seed=5)
     assert e2 and np.array_equal(a_back, a_full)
