@@ -77,7 +77,10 @@ typedef enum sf_dtype {
  * mask argument of IBackend::attention (backend.h:104) that the reference
  * implementations ignore.
  * num_splits: 0 chooses the split-K factor automatically; n > 0 forces n
- * (at most 64).
+ * (at most 64).  Automatic: no split when B*H*ceil(Sq/80) fills the 256
+ * CUs, none either when it does not and Sk <= 1024 (the call then runs one
+ * workgroup per 16 query rows over all keys), key splits for about one
+ * workgroup per CU otherwise.
  * exact_pv: 0 (default) runs the key-split kernel's (Sk > 128) P.V
  * contraction in fp16: a bf16 V converted with rounding to nearest, exact for
  * 2^-14 <= |v| < 2^16 (bf16's 8 significant bits fit fp16's 11; smaller

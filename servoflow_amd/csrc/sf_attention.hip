@@ -208,27 +208,27 @@ __device__ __forceinline__ float max_xor32(float x) {
 // caller switches on the wave index): the owner's block is then a constant
 // register index, and every LDS read of the merge is issued before the
 // first one is used (one LDS round trip instead of one per row block).
-template <int W>
+template <int W, int QB>
 __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo_base,
-                                                    const f32x4 (&acc)[kQB][4], const f32x4 (&accl)[kQB],
-                                                    const float (&m)[kQB], int g, int r, int lane, int b,
+                                                    const f32x4 (&acc)[QB][4], const f32x4 (&accl)[QB],
+                                                    const float (&m)[QB], int g, int r, int lane, int b,
                                                     int h, int q0, int split, int nsplit) {
-    constexpr int QR = 16 * kQB;
-    float* xo = xo_base;                                  // [4 writer][3 slot][kQB][64 lanes][4]
-    float* sm = xo + 4 * 3 * kQB * 64 * 4;                // [QR][4 writer]
+    constexpr int QR = 16 * QB;
+    float* xo = xo_base;                                  // [4 writer][3 slot][QB][64 lanes][4]
+    float* sm = xo + 4 * 3 * QB * 64 * 4;                // [QR][4 writer]
     float* sl = sm + 4 * QR;                              // [QR][4 writer]
-    static_assert((4 * 3 * kQB * 64 * 4 + 2 * 4 * QR) * 4 <= 2 * 32768, "fits the ring's LDS");
+    static_assert((4 * 3 * QB * 64 * 4 + 2 * 4 * QR) * 4 <= 2 * 32768, "fits the ring's LDS");
 #pragma unroll
     for (int o = 0; o < 4; ++o) {
         if (o == W) continue;
         const int slot = o - (o > W ? 1 : 0);
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb)
-            *reinterpret_cast<f32x4*>(xo + (((W * 3 + slot) * kQB + qb) * 64 + lane) * 4) = acc[qb][o];
+        for (int qb = 0; qb < QB; ++qb)
+            *reinterpret_cast<f32x4*>(xo + (((W * 3 + slot) * QB + qb) * 64 + lane) * 4) = acc[qb][o];
     }
     if (g == 0) {
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
+        for (int qb = 0; qb < QB; ++qb) {
             sm[(16 * qb + r) * 4 + W] = m[qb];
             sl[(16 * qb + r) * 4 + W] = accl[qb][0];
         }
@@ -236,23 +236,23 @@ __device__ __forceinline__ void attn_split_epilogue(const AttnArgs& a, float* xo
     __syncthreads();
 
     // every read, then the arithmetic
-    f32x4 mk[kQB], lk[kQB], c[kQB][3];
+    f32x4 mk[QB], lk[QB], c[QB][3];
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         mk[qb] = *reinterpret_cast<const f32x4*>(sm + (16 * qb + r) * 4);
         lk[qb] = *reinterpret_cast<const f32x4*>(sl + (16 * qb + r) * 4);
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
             const int k = j + (j >= W ? 1 : 0);          // the other writers, in wave order
             const int slot = W - (W > k ? 1 : 0);        // W's slot in writer k's blocks
-            c[qb][j] = *reinterpret_cast<const f32x4*>(xo + (((k * 3 + slot) * kQB + qb) * 64 + lane) * 4);
+            c[qb][j] = *reinterpret_cast<const f32x4*>(xo + (((k * 3 + slot) * QB + qb) * 64 + lane) * 4);
         }
     }
     const size_t bh = (size_t)b * a.H + h;
     const size_t pbase = (bh * nsplit + split) * (size_t)a.Sq;
     const int d0 = 16 * W + 4 * g;
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         const float M = fmaxf(fmaxf(mk[qb][0], mk[qb][1]), fmaxf(mk[qb][2], mk[qb][3]));
         const float Muse = M == -INFINITY ? 0.f : M;
         float f[4];
@@ -332,10 +332,10 @@ __device__ __forceinline__ void ring_wait_k() {
 // exact for 2^-14 <= |v| < 2^16; an fp16 V as is).  true: V in its input
 // type and P as a (hi, lo) pair of that type.  kF16: Q/K/V are fp16 (S on
 // the fp16 MFMA) instead of bf16.
-template <bool kExactPV, bool kF16>
+template <bool kExactPV, bool kF16, int QB>
 __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     using v8 = typename In16<kF16>::v8;
-    constexpr int QR = 16 * kQB;
+    constexpr int QR = 16 * QB;
     __shared__ __attribute__((aligned(16))) char ring[kRingStages * kStageBytes];
 
     const int tid = threadIdx.x;
@@ -346,10 +346,26 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     const int g = lane >> 4;
     const int r = lane & 15;
     const int nsplit = a.nsplit;
-    const int split = blockIdx.x % nsplit;
-    const int qc = blockIdx.x / nsplit;
-    const int h = blockIdx.y;
-    const int b = blockIdx.z;
+    int split, qc, h, b;
+    if constexpr (QB == 1) {
+        // 1-D grid of one 16-row query block per workgroup, no key split:
+        // id = slot + 8 (chunk + nqc * head group), so the blocks of head
+        // 8 group + slot sit at ids congruent mod 8, on one XCD, and its K/V
+        // are fetched into that L2 once and read from there by every block.
+        const int id = blockIdx.x;
+        const int rest = id >> 3;
+        const int bh = (id & 7) + 8 * (rest / a.nqc);
+        if (bh >= a.B * a.H) return;   // the grid's last head group is padded to 8
+        qc = rest % a.nqc;
+        h = bh % a.H;
+        b = bh / a.H;
+        split = 0;
+    } else {
+        split = blockIdx.x % nsplit;
+        qc = blockIdx.x / nsplit;
+        h = blockIdx.y;
+        b = blockIdx.z;
+    }
     const int q0 = qc * QR;
 
     int valid = a.Sk;
@@ -374,9 +390,9 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                   a.kv_mask ? (uint32_t)((a.Sk + 3) & ~3) : 0u);
 
     // Q fragments (B operand of S^T = K.Q^T): row 16qb + r, dims 32hh + 8g..
-    v8 qf[kQB][2];
+    v8 qf[QB][2];
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
             qf[qb][hh] = __builtin_bit_cast(
@@ -436,20 +452,20 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     // outstanding and wait for every in-flight ring load before the first
     // S contraction of each tile.
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) asm volatile("" ::"v"(qf[qb][hh]));
 
-    f32x4 acc[kQB][4];   // O^T blocks: lane holds d = 16db + 4g + i, q = 16qb + r
-    f32x4 accl[kQB];     // row sums: element 0 of lanes 0..15 holds l of query 16qb + r
+    f32x4 acc[QB][4];   // O^T blocks: lane holds d = 16db + 4g + i, q = 16qb + r
+    f32x4 accl[QB];     // row sums: element 0 of lanes 0..15 holds l of query 16qb + r
     // m: running max of each query row in log2 units (-inf until a finite
     // score has been seen); nm: the offset the weights use, -m (0 while m is
     // -inf).  A tile whose raw scores stay at or below (m + 8) / scale_log2
     // keeps m, so every weight is <= 2^8.
-    float m[kQB], nm[kQB];
+    float m[QB], nm[QB];
     const float inv_sl2 = 1.f / a.scale_log2;
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         m[qb] = -INFINITY;
         nm[qb] = 0.f;
         accl[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -510,9 +526,9 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                 for (int hh = 0; hh < 2; ++hh) kf[kb][hh] = __builtin_bit_cast(v8, kw[2 * kb + hh]);
             const bool need_mask = a.causal || kt + kKT > kend || a.kv_mask;
             const uint32_t mw[2] = {mw_next[0], mw_next[1]};
-            f32x4 s[kQB][2];
+            f32x4 s[QB][2];
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
+            for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
                     f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -522,7 +538,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
             }
             if (need_mask) {
 #pragma unroll
-                for (int qb = 0; qb < kQB; ++qb) {
+                for (int qb = 0; qb < QB; ++qb) {
                     const int qrow = q0 + 16 * qb + r;
 #pragma unroll
                     for (int kb = 0; kb < 2; ++kb) {
@@ -541,19 +557,19 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
             // one of the four lanes holding that row does, so the wave-wide
             // test needs no cross-lane maximum; that is taken only when the
             // rows are rescaled.
-            float lmx[kQB];
+            float lmx[QB];
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
+            for (int qb = 0; qb < QB; ++qb) {
                 const f32x4 u = s[qb][0], v = s[qb][1];
                 lmx[qb] = fmaxf(fmaxf(fmaxf(fmaxf(fmaxf(fmaxf(fmaxf(u[0], u[1]), u[2]), u[3]), v[0]), v[1]), v[2]),
                                 v[3]);
             }
             bool grow = false;
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) grow |= lmx[qb] > fmaf(m[qb], inv_sl2, 8.f * inv_sl2);
+            for (int qb = 0; qb < QB; ++qb) grow |= lmx[qb] > fmaf(m[qb], inv_sl2, 8.f * inv_sl2);
             if (__any(grow)) {
 #pragma unroll
-                for (int qb = 0; qb < kQB; ++qb) {
+                for (int qb = 0; qb < QB; ++qb) {
                     const float mx = max_xor32(max_xor16(lmx[qb])) * a.scale_log2;
                     const float mnew = fmaxf(m[qb], mx);
                     if constexpr (!kExactPV) nm[qb] = mnew == -INFINITY ? 0.f : -mnew;
@@ -572,11 +588,11 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
             // Weights: P rounded to the nearest fp16 (P <= 2^8 by the lazy
             // rescale; l sums the same rounded weights), or a (hi, lo) pair
             // of the input type in the exact form.
-            f16x8 p8[kQB];
-            bf16x8 ph8[kQB], pl8[kQB];
-            f16x8 hh8[kQB], hl8[kQB];
+            f16x8 p8[QB];
+            bf16x8 ph8[QB], pl8[QB];
+            f16x8 hh8[QB], hl8[QB];
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
+            for (int qb = 0; qb < QB; ++qb) {
                 if constexpr (!kExactPV) {
                     float pf[8];
 #pragma unroll
@@ -641,7 +657,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                 }
             }
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
+            for (int qb = 0; qb < QB; ++qb) {
                 if constexpr (!kExactPV) {
 #pragma unroll
                     for (int db = 0; db < 4; ++db) acc[qb][db] = mfma16x16x32_f16(vh[db], p8[qb], acc[qb][db]);
@@ -681,10 +697,10 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     float* xo = reinterpret_cast<float*>(ring);
     switch (w) {   // wave-uniform
-        case 0: attn_split_epilogue<0>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
-        case 1: attn_split_epilogue<1>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
-        case 2: attn_split_epilogue<2>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
-        default: attn_split_epilogue<3>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
+        case 0: attn_split_epilogue<0, QB>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
+        case 1: attn_split_epilogue<1, QB>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
+        case 2: attn_split_epilogue<2, QB>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
+        default: attn_split_epilogue<3, QB>(a, xo, acc, accl, m, g, r, lane, b, h, q0, split, nsplit); break;
     }
 }
 
@@ -1050,6 +1066,11 @@ using sfk::kMaxSplits;
 
 int query_chunks(const sf_attn_desc* d) { return (d->Sq + 16 * sfk::kQB - 1) / (16 * sfk::kQB); }
 
+// Keys up to which a grid that leaves CUs idle runs one workgroup per 16-row
+// query block (all of a head's keys each, no split, no merge pass) instead
+// of key splits.
+constexpr int kQGroupMaxKeys = 1024;
+
 // MI355X has 256 CUs.  When B*H*query-chunks alone fills them the keys are
 // not split (no partials, no merge pass: measured faster at B = 8 and 16 than
 // two splits).  Otherwise the keys are split so that the grid is about one
@@ -1068,6 +1089,7 @@ int choose_splits(const sf_attn_desc* d) {
     const long base = (long)d->B * d->H * query_chunks(d);
     if (base <= 0) return 1;
     if (base >= kNumCUs) return 1;
+    if (d->Sk <= kQGroupMaxKeys && d->in_dtype != SF_F32) return 1;   // query blocks instead
     const long tiles = ((long)d->Sk + 127) / 128;
     long ns = kNumCUs / base;
     // at least two tiles per split: one-tile splits cost their fixed start
@@ -1093,6 +1115,19 @@ void launch_short(bool f16, int kb, dim3 grid, hipStream_t s, const sfk::AttnArg
         else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, false, NW>), grid, block, 0, s, a);
         else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, false, NW>), grid, block, 0, s, a);
         else hipLaunchKernelGGL((sfk::attn_short_kernel<8, false, NW>), grid, block, 0, s, a);
+    }
+}
+
+// QB: 16-row query blocks per workgroup (kQB: 80-row chunks on a (split x
+// chunk, H, B) grid; 1: the XCD-grouped 1-D query-block grid).
+template <int QB>
+void launch_ring(bool exact, bool f16, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
+    if (exact) {
+        if (f16) hipLaunchKernelGGL((sfk::attn_ring_kernel<true, true, QB>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((sfk::attn_ring_kernel<true, false, QB>), grid, dim3(256), 0, s, a);
+    } else {
+        if (f16) hipLaunchKernelGGL((sfk::attn_ring_kernel<false, true, QB>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((sfk::attn_ring_kernel<false, false, QB>), grid, dim3(256), 0, s, a);
     }
 }
 
@@ -1219,7 +1254,12 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
 
     const bool short_keys = d->Sk <= sfk::kShortMaxKeys && d->num_splits <= 1;
     const int ns = short_keys ? 1 : choose_splits(d);
-    const int nqc = query_chunks(d);
+    // one workgroup per 16-row query block: no key split, and a grid of
+    // 80-row chunks that would leave CUs idle
+    const long bh = (long)d->B * d->H;
+    const bool qblocks = !short_keys && ns == 1 && d->in_dtype != SF_F32 && d->Sk <= kQGroupMaxKeys &&
+                         bh * query_chunks(d) < kNumCUs;
+    const int nqc = qblocks ? (d->Sq + 15) / 16 : query_chunks(d);
     sfk::AttnArgs a{};
     a.q = static_cast<const uint16_t*>(q);
     a.k = static_cast<const uint16_t*>(k);
@@ -1266,13 +1306,12 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
             launch_short<1>(f16, kb, dim3(qb, d->H, d->B), s, a);
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
     } else {
-        const dim3 grid(ns * nqc, d->H, d->B);
-        if (d->exact_pv) {
-            if (f16) hipLaunchKernelGGL((sfk::attn_ring_kernel<true, true>), grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((sfk::attn_ring_kernel<true, false>), grid, dim3(256), 0, s, a);
+        if (qblocks) {
+            const long groups = (bh + 7) / 8;
+            if (8L * nqc * groups > 0x7fffffffL) return SF_ENOTSUP;
+            launch_ring<1>(d->exact_pv != 0, f16, dim3((unsigned)(8L * nqc * groups)), s, a);
         } else {
-            if (f16) hipLaunchKernelGGL((sfk::attn_ring_kernel<false, true>), grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((sfk::attn_ring_kernel<false, false>), grid, dim3(256), 0, s, a);
+            launch_ring<sfk::kQB>(d->exact_pv != 0, f16, dim3(ns * nqc, d->H, d->B), s, a);
         }
     }
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;

@@ -142,6 +142,23 @@ def test_workspace_contract():
     assert _fwd(d1) == abi.SF_ENOTSUP
 
 
+def test_query_block_calls_need_no_workspace():
+    """Calls whose 80-row grid leaves CUs idle and whose keys fit 1024 run
+    one workgroup per query block without a key split: split count 1, no
+    workspace.  Longer key sets and grids that fill the CUs keep their
+    split choice; a forced split count is honoured."""
+    lib = abi.lib()
+    for B, H, Sk in ((1, 32, 1024), (1, 32, 129), (2, 32, 700), (4, 32, 1024), (1, 3, 600)):
+        d = abi.attn_desc_bhsd(B, H, 67, Sk)
+        assert lib.sf_attn_num_splits(ctypes.byref(d)) == 1, (B, H, Sk)
+        assert lib.sf_attn_workspace_bytes(ctypes.byref(d)) == 0, (B, H, Sk)
+    assert lib.sf_attn_num_splits(ctypes.byref(abi.attn_desc_bhsd(1, 32, 67, 1025))) > 1
+    assert lib.sf_attn_num_splits(ctypes.byref(abi.attn_desc_bhsd(1, 32, 67, 4374))) == 7
+    d = abi.attn_desc_bhsd(1, 32, 67, 1024)
+    d.num_splits = 2
+    assert lib.sf_attn_workspace_bytes(ctypes.byref(d)) == 32 * 2 * 67 * 66 * 4
+
+
 def test_backend_library_loads_and_exports_the_operator():
     """libsf_backend.so (the C++ RocmBackend over the C-ABI) loads on the host
     and exports RocmBackend::attention."""

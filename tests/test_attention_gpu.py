@@ -427,3 +427,37 @@ def test_short_keys_grouped_waves(B, H, Sq, Sk, causal, vl, dt):
                         valid_len=None if lens is None else to_dev(lens[b:b + 1], torch.int32), **kw)
         torch.cuda.synchronize()
         assert np.array_equal(one.float().cpu().numpy()[0], got[b]), b
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,causal,vl,dt,exact", [
+    (1, 32, 67, 1024, False, "rand", torch.bfloat16, False),   # batch-1 language call
+    (1, 3, 67, 600, False, None, torch.bfloat16, False),       # one head group, 5 of 8 slots empty
+    (2, 5, 200, 700, False, None, torch.bfloat16, False),      # 13 query blocks, 2 groups (last padded)
+    (1, 4, 150, 150, True, None, torch.bfloat16, False),       # causal, 10 blocks
+    (4, 32, 67, 1024, False, "rand", torch.float16, False),
+    (1, 32, 67, 1024, False, "rand", torch.bfloat16, True),    # exact P.V form
+])
+def test_query_block_grid(B, H, Sq, Sk, causal, vl, dt, exact):
+    """Calls whose 80-row grid would leave CUs idle and whose keys fit 1024
+    run one workgroup per 16-row query block over all keys (no split), the
+    blocks of a head on one XCD: against the oracle, bit-identical per batch
+    element to that element run alone, and within the fp16-P rounding of the
+    key-split kernel (forced with num_splits)."""
+    q, k, v = rounded(251, (B, H, Sq, 64)), rounded(252, (B, H, Sk, 64)), rounded(253, (B, H, Sk, 64))
+    lens = None if vl is None else lang_valid_lengths(254 + B, B, 1, Sk)
+    kw = {"is_causal": causal, "exact_pv": exact}
+    dq, dk, dv = (to_dev(x, dt) for x in (q, k, v))
+    vdev = None if lens is None else to_dev(lens, torch.int32)
+    got = attention(dq, dk, dv, out_dtype=torch.float32, valid_len=vdev, **kw)
+    split = attention(dq, dk, dv, out_dtype=torch.float32, valid_len=vdev, num_splits=2, **kw)
+    torch.cuda.synchronize()
+    got, split = got.cpu().numpy(), split.cpu().numpy()
+    ref = O.attention_f32(q, k, v, causal=causal, valid_len=lens)
+    assert_close_bf16(got, ref, f"query blocks {B},{H},{Sq},{Sk}")
+    assert mean_rel(got, ref) < (1e-4 if exact else 5e-4)
+    assert np.abs(got - split).max() < 1e-3
+    for b in range(B):
+        one = attention(dq[b:b + 1], dk[b:b + 1], dv[b:b + 1], out_dtype=torch.float32,
+                        valid_len=None if lens is None else to_dev(lens[b:b + 1], torch.int32), **kw)
+        torch.cuda.synchronize()
+        assert np.array_equal(one.cpu().numpy()[0], got[b]), b
