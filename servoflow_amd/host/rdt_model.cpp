@@ -126,10 +126,13 @@ struct sf_rdt {
     size_t attn_ws_bytes = 0;
     void* gemm_ws = nullptr;       // split-K partial sums, shared by the stream's GEMMs
     size_t gemm_ws_bytes = 0;
-    // int8 models above 160 rows (the library path): the current block's six
-    // projection weights widened to bf16 codes in one launch at the block's
-    // start (sf_int8_codes_to_bf16), instead of one widening pass per GEMM;
-    // codes16_of[param] points at a weight's copy while its block runs.
+    // int8 models above 160 rows (the library path): every block's six
+    // projection weights widened to bf16 codes (sf_int8_codes_to_bf16, up to
+    // eight matrices per launch) once at the start of each entry point's
+    // pass -- once per sampled loop, not once per block and step -- instead
+    // of one widening pass per GEMM.  codes16_of[param] is a weight's copy
+    // (fixed at creation).  The widening runs inside the captured loop, so
+    // a replay after the int8 weights change widens the new codes.
     char* codes16 = nullptr;
     size_t codes16_bytes = 0;
     std::vector<const void*> codes16_of;
@@ -463,32 +466,38 @@ int next_norm(const sf_rdt* m, int i) {
     return i + 1 < m->cfg.layers ? m->layers[i + 1].norm1 : m->fnorm;
 }
 
+// Refreshes the bf16 code copies of blocks [first, first + count)'s int8
+// weights (no-op without them), up to SF_CODES_MAX_JOBS matrices per launch.
+int widen_codes(sf_rdt* m, int first, int count, hipStream_t s) {
+    if (!m->codes16) return SF_OK;
+    sf_codes_job jobs[SF_CODES_MAX_JOBS];
+    int n = 0;
+    for (int i = first; i < first + count; ++i) {
+        for (int w : block_weights(m->layers[i])) {
+            const Param& P = m->params[w];
+            if (!m->codes16_of[w]) continue;
+            jobs[n].q = static_cast<const int8_t*>(P.data);
+            jobs[n].ldq = P.shape[1];
+            jobs[n].out = const_cast<void*>(m->codes16_of[w]);
+            jobs[n].N = (int32_t)P.shape[0];
+            jobs[n].K = (int32_t)P.shape[1];
+            if (++n == SF_CODES_MAX_JOBS) {
+                SF_TRY(sf_int8_codes_to_bf16(jobs, n, s));
+                n = 0;
+            }
+        }
+    }
+    return n ? sf_int8_codes_to_bf16(jobs, n, s) : SF_OK;
+}
+
 // RDTBlock::forward (dit_block.cu:349-387) on the fp32 residual m->x, with
 // m->n holding norm1(x) on entry; on exit m->n holds the next norm of x.
+// The block's int8 code copies (if any) are current (widen_codes).
 int block_forward(sf_rdt* m, int i, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const LayerIdx& L = m->layers[i];
     const int D = c.hidden, S = c.horizon + 3, M = c.batch * S;
     const int fd = m->ffn_dtype;
-    if (m->codes16) {   // int8 weights above 160 rows: widen the block's six in one pass
-        sf_codes_job jobs[6];
-        int n = 0;
-        char* dst = m->codes16;
-        for (int w : block_weights(L)) {
-            const Param& P = m->params[w];
-            m->codes16_of[w] = nullptr;
-            if (P.dtype != SF_I8) continue;
-            jobs[n].q = static_cast<const int8_t*>(P.data);
-            jobs[n].ldq = P.shape[1];
-            jobs[n].out = dst;
-            jobs[n].N = (int32_t)P.shape[0];
-            jobs[n].K = (int32_t)P.shape[1];
-            m->codes16_of[w] = dst;
-            dst += align256((size_t)P.shape[0] * P.shape[1] * 2);
-            ++n;
-        }
-        SF_TRY(sf_int8_codes_to_bf16(jobs, n, s));
-    }
     // self-attention branch
     uint16_t* qkv[3] = {m->q, m->k, m->v};
     const int qk_g[3] = {L.q_norm, L.k_norm, -1};
@@ -521,7 +530,7 @@ int entry_norm(sf_rdt* m, int first, hipStream_t s) {
 }
 
 // RDT1BModel::denoise_step up to the final layer: velocity rows [B*S, A].
-int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s) {
+int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s, bool widen = true) {
     const sf_rdt_config& c = m->cfg;
     const int D = c.hidden, T = c.horizon, A = c.action_dim, S = T + 3;
     const int BT = c.batch * T, M = c.batch * S;
@@ -539,6 +548,7 @@ int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s) {
     SF_TRY(sf_assemble_tokens(m->x, m->t_emb, m->f_emb, m->state_tok, m->act_out, pf(m, m->xpos),
                               c.batch, T, D, s));
     SF_TRY(entry_norm(m, 0, s));
+    if (widen) SF_TRY(widen_codes(m, 0, c.layers, s));
     for (int i = 0; i < c.layers; ++i) SF_TRY(block_forward(m, i, s));
     // FinalLayer (dit_block.cu:407-412); m->n = norm_final(x) from the last block
     SF_TRY(linear(m, m->n, D, M, m->f1w, m->f1b, SF_ACT_GELU_TANH, m->h, D, m->ffn_dtype, false, s));
@@ -559,8 +569,9 @@ std::vector<float> schedule(int num_steps) {
 int sample_body(sf_rdt* m, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const std::vector<float> ts = schedule(c.num_steps);
+    SF_TRY(widen_codes(m, 0, c.layers, s));   // once for every step of the loop
     for (int step = 0; step < c.num_steps; ++step) {
-        SF_TRY(step_forward(m, m->x_state, ts[step], s));
+        SF_TRY(step_forward(m, m->x_state, ts[step], s, false));
         const float dt = ts[step + 1] - ts[step];
         SF_TRY(sf_euler_update(m->x_state, m->vel_rows, c.batch, c.horizon, c.action_dim,
                                c.horizon + 3, dt, s));
@@ -694,14 +705,11 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     bufs.push_back({&m->attn_ws, std::max<size_t>(m->attn_ws_bytes, 256)});
     m->gemm_ws_bytes = gemm_ws_for(m, false, nullptr);
     bufs.push_back({&m->gemm_ws, std::max<size_t>(m->gemm_ws_bytes, 256)});
-    if (S * B > 160) {
-        for (const LayerIdx& L : m->layers) {
-            size_t bytes = 0;
+    if (S * B > 160) {   // every block's int8 weights as bf16 codes
+        for (const LayerIdx& L : m->layers)
             for (int w : block_weights(L))
                 if (m->params[w].dtype == SF_I8)
-                    bytes += align256((size_t)m->params[w].shape[0] * m->params[w].shape[1] * 2);
-            m->codes16_bytes = std::max(m->codes16_bytes, bytes);
-        }
+                    m->codes16_bytes += align256((size_t)m->params[w].shape[0] * m->params[w].shape[1] * 2);
         if (m->codes16_bytes) bufs.push_back({(void**)&m->codes16, m->codes16_bytes});
     }
     std::vector<size_t> boff(bufs.size());
@@ -720,6 +728,16 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     }
     for (size_t i = 0; i < bufs.size(); ++i) *bufs[i].ptr = m->arena + boff[i];
     m->codes16_of.assign(m->params.size(), nullptr);
+    if (m->codes16) {
+        char* dst = m->codes16;
+        for (const LayerIdx& L : m->layers)
+            for (int w : block_weights(L)) {
+                const Param& P = m->params[w];
+                if (P.dtype != SF_I8) continue;
+                m->codes16_of[w] = dst;
+                dst += align256((size_t)P.shape[0] * P.shape[1] * 2);
+            }
+    }
     m->exact_pv.assign(c.layers, 0);
     m->lang_rows = m->cond_lang_rows = c.lang_max;
     if (hipStreamCreate(&m->own_stream) != hipSuccess) {
@@ -955,6 +973,7 @@ extern "C" int sf_rdt_run_blocks(sf_rdt* m, float* x, int32_t first, int32_t cou
     const size_t nbytes = (size_t)c.batch * (c.horizon + 3) * c.hidden * 4;
     SF_HIP(hipMemcpyAsync(m->x, x, nbytes, hipMemcpyDeviceToDevice, s));
     SF_TRY(entry_norm(m, first, s));
+    SF_TRY(widen_codes(m, first, count, s));
     for (int i = first; i < first + count; ++i) SF_TRY(block_forward(m, i, s));
     SF_HIP(hipMemcpyAsync(x, m->x, nbytes, hipMemcpyDeviceToDevice, s));
     return SF_OK;
