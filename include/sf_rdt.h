@@ -68,6 +68,16 @@ int sf_euler_update(float* x, const float* v, int32_t B, int32_t T, int32_t A, i
  * gives NaN.  The runtime checks each layer's cached V against the fp16
  * range of the fast P.V form with it. */
 int sf_absmax_bf16(const void* p, int64_t n, float* out, void* stream);
+/* sf_absmax_bf16 over up to SF_ABSMAX_MAX_JOBS buffers in one launch, each
+ * merged into its own *out (the runtime's per-layer V range check: one
+ * launch instead of one per layer). */
+#define SF_ABSMAX_MAX_JOBS 64
+typedef struct sf_absmax_job {
+    const void* p;   /* bf16, 16-byte aligned */
+    int64_t n;
+    float* out;
+} sf_absmax_job;
+int sf_absmax_bf16_batched(const sf_absmax_job* jobs, int32_t count, void* stream);
 
 /* ---- model runtime (libsf_rdt.so) ---------------------------------------- */
 

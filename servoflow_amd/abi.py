@@ -96,6 +96,15 @@ class CodesJob(ctypes.Structure):
 SF_CODES_MAX_JOBS = 8
 
 
+class AbsmaxJob(ctypes.Structure):
+    """Mirror of `sf_absmax_job`."""
+
+    _fields_ = [("p", ctypes.c_void_p), ("n", ctypes.c_int64), ("out", ctypes.c_void_p)]
+
+
+SF_ABSMAX_MAX_JOBS = 64
+
+
 class SfError(RuntimeError):
     def __init__(self, status: int, what: str):
         super().__init__(f"{what}: {strerror(status)} (status {status})")
@@ -143,6 +152,8 @@ def lib() -> ctypes.CDLL:
     L.sf_dequant_int8.restype = ctypes.c_int
     L.sf_int8_codes_to_bf16.argtypes = [ctypes.POINTER(CodesJob), i32, vp]
     L.sf_int8_codes_to_bf16.restype = ctypes.c_int
+    L.sf_absmax_bf16_batched.argtypes = [ctypes.POINTER(AbsmaxJob), i32, vp]
+    L.sf_absmax_bf16_batched.restype = ctypes.c_int
     L.sf_strerror.argtypes = [ctypes.c_int]
     L.sf_strerror.restype = ctypes.c_char_p
     _lib = L

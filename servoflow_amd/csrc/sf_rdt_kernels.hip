@@ -152,6 +152,40 @@ __global__ __launch_bounds__(256) void absmax_bf16_kernel(const uint16_t* __rest
     }
 }
 
+// absmax_bf16_kernel over up to SF_ABSMAX_MAX_JOBS buffers in one launch:
+// workgroup row blockIdx.y takes buffer j (its own output word), the x
+// extent strides over it.
+struct AbsmaxJobs {
+    const uint16_t* p[SF_ABSMAX_MAX_JOBS];
+    int64_t n[SF_ABSMAX_MAX_JOBS];
+    unsigned int* out[SF_ABSMAX_MAX_JOBS];
+};
+
+__global__ __launch_bounds__(256) void absmax_jobs_kernel(const AbsmaxJobs J) {
+    const int j = blockIdx.y;
+    const uint16_t* __restrict__ p = J.p[j];
+    const int64_t n = J.n[j];
+    uint32_t m = 0;
+    const int64_t n8 = n / 8;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += stride) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(p + 8 * i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = max(m, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
+    }
+    for (int64_t i = 8 * n8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        m = max(m, (uint32_t)(p[i] & 0x7fffu));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
+    __shared__ uint32_t wm[4];
+    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = max(max(wm[0], wm[1]), max(wm[2], wm[3]));
+        if (m) atomicMax(J.out[j], m << 16);
+    }
+}
+
 }  // namespace sfk
 
 using sfk::blocks_for;
@@ -225,6 +259,26 @@ extern "C" int sf_euler_update(float* x, const float* v, int32_t B, int32_t T, i
     if (!n) return SF_OK;
     hipLaunchKernelGGL(sfk::euler_update_kernel, dim3(blocks_for(n)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, v, B, T, A, S, dt);
+    return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+}
+
+extern "C" int sf_absmax_bf16_batched(const sf_absmax_job* jobs, int32_t count, void* stream) {
+    if (count < 0 || count > SF_ABSMAX_MAX_JOBS || (count && !jobs)) return SF_EINVAL;
+    sfk::AbsmaxJobs J{};
+    int64_t most = 0;
+    for (int j = 0; j < count; ++j) {
+        const sf_absmax_job& b = jobs[j];
+        if (!b.out || b.n < 0 || (b.n && !b.p) || (reinterpret_cast<uintptr_t>(b.p) & 15)) return SF_EINVAL;
+        J.p[j] = static_cast<const uint16_t*>(b.p);
+        J.n[j] = b.n;
+        J.out[j] = reinterpret_cast<unsigned int*>(b.out);
+        most = std::max(most, b.n);
+    }
+    if (!count || !most) return SF_OK;
+    const int64_t want = (most / 8 + 255) / 256;
+    const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 256));
+    hipLaunchKernelGGL(sfk::absmax_jobs_kernel, dim3(blocks, (unsigned)count), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), J);
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
 }
 

@@ -894,9 +894,15 @@ extern "C" int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t
     // each layer's max |V| for the choice of P.V form (resolve_pv_forms)
     if (c.layers > 0) {
         SF_TRY(sf_fill_f32(m->v_absmax, c.layers, 0.f, s));
-        for (int i = 0; i < c.layers; ++i) {
-            const int64_t Sc = (i % 2 == 0) ? c.lang_max : c.img_len;
-            SF_TRY(sf_absmax_bf16(m->cv[i], (int64_t)B * c.heads * Sc * 64, m->v_absmax + i, s));
+        for (int i0 = 0; i0 < c.layers; i0 += SF_ABSMAX_MAX_JOBS) {
+            sf_absmax_job jobs[SF_ABSMAX_MAX_JOBS];
+            const int n = std::min(SF_ABSMAX_MAX_JOBS, c.layers - i0);
+            for (int j = 0; j < n; ++j) {
+                const int i = i0 + j;
+                const int64_t Sc = (i % 2 == 0) ? c.lang_max : c.img_len;
+                jobs[j] = sf_absmax_job{m->cv[i], (int64_t)B * c.heads * Sc * 64, m->v_absmax + i};
+            }
+            SF_TRY(sf_absmax_bf16_batched(jobs, n, s));
         }
         SF_HIP(hipMemcpyAsync(m->v_absmax_host, m->v_absmax, (size_t)c.layers * 4, hipMemcpyDeviceToHost, s));
         SF_HIP(hipEventRecord(m->cond_event, s));

@@ -214,3 +214,21 @@ def test_int8_codes_to_bf16_rejects_bad_jobs():
         one[0].q, one[0].ldq, one[0].out, one[0].N, one[0].K = 256, 64, 512, 4, 64
         setattr(one[0], field, bad)
         assert lib.sf_int8_codes_to_bf16(one, 1, None) == abi.SF_EINVAL, (field, bad)
+
+
+def test_absmax_batched_rejects_bad_jobs():
+    """Argument checks of the batched max-|x| scan, before any launch: job
+    count outside 0..SF_ABSMAX_MAX_JOBS, a missing output, a negative
+    length, a misaligned buffer."""
+    lib = abi.lib()
+    jobs = (abi.AbsmaxJob * (abi.SF_ABSMAX_MAX_JOBS + 1))()
+    for j in jobs:
+        j.p, j.n, j.out = 256, 64, 512
+    assert lib.sf_absmax_bf16_batched(jobs, 0, None) == abi.SF_OK
+    assert lib.sf_absmax_bf16_batched(jobs, abi.SF_ABSMAX_MAX_JOBS + 1, None) == abi.SF_EINVAL
+    assert lib.sf_absmax_bf16_batched(jobs, -1, None) == abi.SF_EINVAL
+    for field, bad in (("out", None), ("n", -1), ("p", 264), ("p", None)):
+        one = (abi.AbsmaxJob * 1)()
+        one[0].p, one[0].n, one[0].out = 256, 64, 512
+        setattr(one[0], field, bad)
+        assert lib.sf_absmax_bf16_batched(one, 1, None) == abi.SF_EINVAL, (field, bad)

@@ -564,3 +564,34 @@ def test_gemm_fp16_activations_library_path():
     w, b = rounded(152, (N, Kd), 0.02), O.randn(153, (N,), 0.02)
     got = host(K.gemm(dev(a, torch.float16), dev(w), dev(b, torch.float32), out_dtype=torch.float32))
     close(got, O.linear(O.bf16_round(a), w, b), "fp16-activation library gemm")
+
+
+def test_absmax_bf16_batched_matches_torch():
+    """One launch over buffers of different lengths (a ragged tail, an
+    empty one, a NaN, an inf) gives each its own max |x|, merged into an
+    output that already holds a value."""
+    import ctypes
+    dev = torch.device(DEV)
+    g = torch.Generator(device=dev).manual_seed(77)
+    lens = [4374 * 64, 1000003, 0, 17, 64 * 1024]
+    bufs = [(torch.randn(max(n, 8), device=dev, generator=g) * (i + 1)).to(torch.bfloat16) for i, n in enumerate(lens)]
+    bufs[3][5] = float("nan")
+    bufs[4][123] = float("-inf")
+    out = torch.zeros(len(lens), dtype=torch.float32, device=dev)
+    out[2] = 3.5   # kept: the empty buffer merges nothing
+    jobs = (abi.AbsmaxJob * len(lens))()
+    for j, (b, n) in enumerate(zip(bufs, lens)):
+        jobs[j].p, jobs[j].n, jobs[j].out = b.data_ptr(), n, out.data_ptr() + 4 * j
+    abi.check(abi.lib().sf_absmax_bf16_batched(jobs, len(lens), torch.cuda.current_stream().cuda_stream),
+              "sf_absmax_bf16_batched")
+    torch.cuda.synchronize()
+    got = out.cpu()
+    for j, (b, n) in enumerate(zip(bufs, lens)):
+        if j == 2:
+            assert got[j] == 3.5
+        elif j == 3:
+            assert torch.isnan(got[j])
+        elif j == 4:
+            assert torch.isinf(got[j])
+        else:
+            assert got[j] == b[:n].float().abs().max().cpu(), j
