@@ -245,11 +245,26 @@ typedef struct sf_gemm_desc {
                                 widening the codes itself on every call */
 } sf_gemm_desc;
 
-/* Bytes of workspace the split-K path needs for this shape (0: the shape
- * always runs single-pass). */
+/* Bytes of workspace sf_gemm needs for this call (0: it always runs
+ * single-pass): the split-K partials (M <= 160), or on the library path the
+ * product buffer of the epilogue (none when hipBLASLt writes a plain bf16 C
+ * itself), the int8 weights' bf16 copy and hipBLASLt's scratch. */
 size_t sf_gemm_workspace_bytes(const sf_gemm_desc* desc);
 
 int sf_gemm(const sf_gemm_desc* desc, void* stream);
+
+/* The SF_EPI_HEADS epilogue on a bf16 projection already in memory -- the
+ * reference's split_qkv / split_kv followed by apply_qk_norm
+ * (split_ops.cuh:62-84, dit_block.cu:185-196, 300-308) in one pass: row m of
+ * P [M][ldp] (bias applied) is cut into N / (H*64) <= 3 sections of H heads,
+ * each head's 64 values RMS-normalised with head_gamma[j] (when not NULL)
+ * and written to head_out[j] at (m / S, h, m % S) with head_stride[j].
+ * desc: M, N (a multiple of 64), H, S, eps, head_out, head_gamma,
+ * head_stride as for sf_gemm; the GEMM fields are not read.  P 8-byte
+ * aligned, ldp >= N a multiple of 4 (16 bytes and 8 take 16-byte loads).
+ * Lets a caller run several projections as one GEMM (the runtime's K/V
+ * cache: every layer's K/V weights in one matrix) and split per layer. */
+int sf_heads_bf16(const sf_gemm_desc* desc, const void* P, int64_t ldp, void* stream);
 
 /* Setup of the library path (M > 160) for this shape, once per shape and
  * process: for the fp32 product and the two bf16 products with bias (plain,

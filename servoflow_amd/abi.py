@@ -152,6 +152,8 @@ def lib() -> ctypes.CDLL:
     L.sf_dequant_int8.restype = ctypes.c_int
     L.sf_int8_codes_to_bf16.argtypes = [ctypes.POINTER(CodesJob), i32, vp]
     L.sf_int8_codes_to_bf16.restype = ctypes.c_int
+    L.sf_heads_bf16.argtypes = [ctypes.POINTER(GemmDesc), vp, i64, vp]
+    L.sf_heads_bf16.restype = ctypes.c_int
     L.sf_absmax_bf16_batched.argtypes = [ctypes.POINTER(AbsmaxJob), i32, vp]
     L.sf_absmax_bf16_batched.restype = ctypes.c_int
     L.sf_strerror.argtypes = [ctypes.c_int]

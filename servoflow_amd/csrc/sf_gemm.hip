@@ -495,7 +495,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
 
 struct EpiArgs {
     const float* part;     // [splits][M][N]
-    const uint16_t* part16;  // or the library path's bf16 product [M][N], bias and scale already in
+    const uint16_t* part16;  // or the library path's bf16 product [M][ld16], bias and scale already in
+    int64_t ld16;            // row stride of part16 (elements)
     int heads16;             // heads outputs take 16-byte stores (8-aligned head_out, strides)
     int splits;
     int M, N;
@@ -534,7 +535,7 @@ struct Quad {
 template <int NS>
 __device__ __forceinline__ void load_quad(const EpiArgs& e, int m, int n, Quad<NS>& q) {
     if (e.part16) {   // one "slice": the rounded product, bias and scale applied
-        const uint2 h = *reinterpret_cast<const uint2*>(e.part16 + (int64_t)m * e.N + n);
+        const uint2 h = *reinterpret_cast<const uint2*>(e.part16 + (int64_t)m * e.ld16 + n);
         q.part[0] = f32x4{bf16_bits_to_f32(h.x & 0xffffu), bf16_bits_to_f32(h.x >> 16),
                           bf16_bits_to_f32(h.y & 0xffffu), bf16_bits_to_f32(h.y >> 16)};
 #pragma unroll
@@ -649,7 +650,7 @@ __global__ __launch_bounds__(256) void heads16_kernel(const EpiArgs e) {
     const int m = (int)(blockIdx.x / ntl) * 32 + (int)(threadIdx.x >> 3);
     const int n = 64 * (int)(blockIdx.x % ntl) + 8 * (int)(threadIdx.x & 7);
     if (m >= e.M) return;   // whole 8-lane groups
-    const u32x4 raw = *reinterpret_cast<const u32x4*>(e.part16 + (int64_t)m * e.N + n);
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(e.part16 + (int64_t)m * e.ld16 + n);
     float v[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1176,6 +1177,32 @@ int act_kind(const sf_gemm_desc* d) {
     return d->a_dtype == SF_F32 ? sfk::kActF32 : (d->a_dtype == SF_F16 ? sfk::kActF16 : sfk::kActBF16);
 }
 
+// The per-head outputs of an SF_EPI_HEADS descriptor (sections of H*64 of
+// the N columns, at most 3; 8-byte aligned outputs and strides that are
+// multiples of 4 elements, 16-byte / 8 for the 16-byte-store kernel).
+int fill_heads(const sf_gemm_desc* d, sfk::EpiArgs& e) {
+    if (d->H <= 0 || d->S <= 0) return SF_EINVAL;   // row m -> (m / S, m % S); a partial last element is fine
+    const int cols = d->H * 64;
+    if (d->N % cols || d->N / cols > 3) return SF_EINVAL;
+    e.heads16 = 1;
+    for (int j = 0; j < d->N / cols; ++j) {
+        if (!d->head_out[j] || !al8(d->head_out[j])) return SF_EINVAL;
+        if (!al16(d->head_out[j])) e.heads16 = 0;
+        for (int q = 0; q < 3; ++q) {
+            if (d->head_stride[j][q] & 3) return SF_EINVAL;
+            if (d->head_stride[j][q] & 7) e.heads16 = 0;
+        }
+        e.head_out[j] = static_cast<uint16_t*>(d->head_out[j]);
+        e.head_gamma[j] = d->head_gamma[j];
+        e.head_sb[j] = d->head_stride[j][0];
+        e.head_sh[j] = d->head_stride[j][1];
+        e.head_ss[j] = d->head_stride[j][2];
+    }
+    e.H = d->H;
+    e.S = d->S;
+    return SF_OK;
+}
+
 // Shape / pointer checks shared by both paths; fills the epilogue fields.
 int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
     if (d->K == 0 || (d->K & 31)) return SF_ENOTSUP;
@@ -1196,25 +1223,7 @@ int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
     e.act = d->act;
     e.eps = d->eps;
     if (d->epilogue == SF_EPI_HEADS) {
-        if (d->H <= 0 || d->S <= 0) return SF_EINVAL;   // row m -> (m / S, m % S); a partial last element is fine
-        const int cols = d->H * 64;
-        if (d->N % cols || d->N / cols > 3) return SF_EINVAL;
-        e.heads16 = 1;
-        for (int j = 0; j < d->N / cols; ++j) {
-            if (!d->head_out[j] || !al8(d->head_out[j])) return SF_EINVAL;
-            if (!al16(d->head_out[j])) e.heads16 = 0;
-            for (int q = 0; q < 3; ++q) {
-                if (d->head_stride[j][q] & 3) return SF_EINVAL;
-                if (d->head_stride[j][q] & 7) e.heads16 = 0;
-            }
-            e.head_out[j] = static_cast<uint16_t*>(d->head_out[j]);
-            e.head_gamma[j] = d->head_gamma[j];
-            e.head_sb[j] = d->head_stride[j][0];
-            e.head_sh[j] = d->head_stride[j][1];
-            e.head_ss[j] = d->head_stride[j][2];
-        }
-        e.H = d->H;
-        e.S = d->S;
+        SF_CHECK_OK(fill_heads(d, e));
     } else if (d->epilogue == SF_EPI_PLAIN || d->epilogue == SF_EPI_ADD_NORM) {
         if (!d->C || d->ldc < d->N) return SF_EINVAL;
         if (d->c_dtype != SF_BF16 && d->c_dtype != SF_F32 && d->c_dtype != SF_F16) return SF_ENOTSUP;
@@ -1346,12 +1355,17 @@ bool lib_available(const sf_gemm_desc* d, const LibPlan& lp, const LtKind& kind,
     return true;
 }
 
+// A plain bf16 C that hipBLASLt writes itself needs no product buffer in
+// the workspace.
+bool lib_direct(const sf_gemm_desc* d) { return lib_kind(d).out16 && d->epilogue == SF_EPI_PLAIN; }
+size_t lib_need(const sf_gemm_desc* d, const LibPlan& lp) { return lp.total - (lib_direct(d) ? lp.c_bytes : 0); }
+
 extern "C" size_t sf_gemm_workspace_bytes(const sf_gemm_desc* d) {
     if (!d) return 0;
     const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K, d->a_dtype == SF_F32);
     if (p.split) return p.ws_bytes;
     const LibPlan lp = plan_library(d->M, d->N, d->K, d->w_dtype == SF_I8, d->a_dtype != SF_BF16);
-    return lp.ok ? lp.total : 0;
+    return lp.ok ? lib_need(d, lp) : 0;
 }
 
 extern "C" int sf_gemm_prepare(const sf_gemm_desc* d) {
@@ -1372,6 +1386,25 @@ extern "C" int sf_gemm_prepare(const sf_gemm_desc* d) {
     return SF_OK;
 }
 
+extern "C" int sf_heads_bf16(const sf_gemm_desc* d, const void* P, int64_t ldp, void* stream) {
+    if (!d || !P || d->epilogue != SF_EPI_HEADS || d->M < 0 || d->N <= 0 || (d->N & 63)) return SF_EINVAL;
+    if (ldp < d->N || (ldp & 3) || !al8(P)) return SF_EINVAL;
+    sfk::EpiArgs e{};
+    SF_CHECK_OK(fill_heads(d, e));
+    if (!d->M) return SF_OK;
+    e.M = d->M;
+    e.N = d->N;
+    e.splits = 1;
+    e.part16 = static_cast<const uint16_t*>(P);
+    e.ld16 = ldp;
+    e.act = SF_ACT_NONE;
+    e.eps = d->eps;
+    if (!al16(P) || (ldp & 7)) e.heads16 = 0;   // 16-byte rows for the 8-lane kernel
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    sfk::launch_reduce<1>(d, e, s);
+    return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+}
+
 extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     if (!d) return SF_EINVAL;
     if (d->M < 0 || d->N < 0 || d->K < 0) return SF_EINVAL;
@@ -1388,12 +1421,15 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
         const LibPlan lp = plan_library(d->M, d->N, d->K, w8, a_conv);
         const LtKind kind = lib_kind(d);
         if (lp.ok && lib_available(d, lp, kind, false)) {
-            if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < lp.total) return SF_EWORKSPACE;
+            const bool direct = kind.out16 && d->epilogue == SF_EPI_PLAIN;   // hipBLASLt writes C
+            if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < lib_need(d, lp)) return SF_EWORKSPACE;
             if (!al16(d->workspace)) return SF_EINVAL;
+            // [fp32 / bf16 product (not when direct)][int8 widened][activation rows][hipBLASLt]
             char* ws = static_cast<char*>(d->workspace);
             float* cbuf = reinterpret_cast<float*>(ws);
-            uint16_t* abuf = reinterpret_cast<uint16_t*>(ws + lp.c_bytes + lp.w_bytes);
-            void* ltws = ws + lp.c_bytes + lp.w_bytes + lp.a_bytes;
+            const size_t c_bytes = direct ? 0 : lp.c_bytes;
+            uint16_t* abuf = reinterpret_cast<uint16_t*>(ws + c_bytes + lp.w_bytes);
+            void* ltws = ws + c_bytes + lp.w_bytes + lp.a_bytes;
             const void* W = d->W;
             int64_t ldw = d->ldw;
             if (w8 && d->w_codes16) {   // the caller's widened copy
@@ -1401,7 +1437,7 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
                 W = d->w_codes16;
                 ldw = d->K;
             } else if (w8) {
-                uint16_t* wb = reinterpret_cast<uint16_t*>(ws + lp.c_bytes);
+                uint16_t* wb = reinterpret_cast<uint16_t*>(ws + c_bytes);
                 const bool c16 = (d->ldw & 15) == 0 && (d->K & 15) == 0;
                 const int64_t nch = (int64_t)d->N * (d->K / (c16 ? 16 : 8));
                 if (nch >= 0x7fffffffLL) return SF_ENOTSUP;
@@ -1416,7 +1452,6 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
                 W = wb;
                 ldw = d->K;
             }
-            const bool direct = kind.out16 && d->epilogue == SF_EPI_PLAIN;   // hipBLASLt writes C
             for (int m0 = 0; m0 < d->M; m0 += lp.chunk) {
                 const int rows = std::min(lp.chunk, d->M - m0);
                 hipblasLtHandle_t h;
@@ -1445,6 +1480,7 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
                 if (kind.out16) {   // bias, GELU and the int8 scale are in the bf16 product
                     ec.part = nullptr;
                     ec.part16 = reinterpret_cast<const uint16_t*>(cbuf);
+                    ec.ld16 = d->N;
                     ec.bias = nullptr;
                     ec.w_scale = nullptr;
                     ec.act = SF_ACT_NONE;

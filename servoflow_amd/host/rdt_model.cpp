@@ -122,6 +122,23 @@ struct sf_rdt {
     uint16_t* img_c = nullptr;     // [B, img_len, D]
     uint16_t* ad_h = nullptr;      // adaptor hidden [B*max(Lmax, I), D]
     std::vector<uint16_t*> ck, cv; // per-layer cross K/V cache [B, H, Sc, 64]
+    // The K/V projections of the blocks that attend to one condition (group
+    // 0: language, even blocks; 1: image, odd blocks), laid out back to back
+    // in the arena -- weights, then biases, then int8 row scales, in block
+    // order -- so that one GEMM of N = blocks * 2D computes all of them
+    // when the rows run on the library path and the product fits kv_prod
+    // (sf_heads_bf16 then splits it per block).
+    struct KvGroup {
+        std::vector<int> blocks;
+        const void* W = nullptr;       // [blocks * 2D][D]
+        const float* bias = nullptr;   // [blocks * 2D]
+        const float* scale = nullptr;  // int8 row scales or null
+        int32_t w_dtype = SF_BF16;
+        bool contiguous = false;
+        int rows_max = 0;              // condition rows of one set (batch 1: L <= lang_max)
+    } kvg[2];
+    uint16_t* kv_prod = nullptr;   // [rows][blocks * 2D] bf16 product of a batched group
+    size_t kv_prod_bytes = 0;
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     void* gemm_ws = nullptr;       // split-K partial sums, shared by the stream's GEMMs
@@ -277,6 +294,44 @@ void build_param_table(sf_rdt* m) {
 // ---- launch helpers -------------------------------------------------------
 
 const float* pf(sf_rdt* m, int idx) { return static_cast<const float*>(m->params[idx].data); }
+
+// A batched K/V group's GEMM: rows x (blocks * 2D), bf16 C with the bias
+// (the library path writes it directly).
+sf_gemm_desc kv_group_desc(const sf_rdt* m, int g, const void* A, int rows) {
+    const sf_rdt::KvGroup& G = m->kvg[g];
+    const int D = m->cfg.hidden;
+    sf_gemm_desc d{};
+    d.M = rows;
+    d.N = (int32_t)G.blocks.size() * 2 * D;
+    d.K = D;
+    d.A = A;
+    d.lda = D;
+    d.a_dtype = SF_BF16;
+    d.W = G.W;
+    d.ldw = D;
+    d.w_dtype = G.w_dtype;
+    d.w_scale = G.scale;
+    d.bias = G.bias;
+    d.act = SF_ACT_NONE;
+    d.epilogue = SF_EPI_PLAIN;
+    d.C = m->kv_prod;
+    d.ldc = d.N;
+    d.c_dtype = SF_BF16;
+    d.workspace = m->gemm_ws;
+    d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
+    return d;
+}
+
+// Whether group g's K/V projections run as one GEMM at this many rows: the
+// library path (more than 160 rows), back-to-back weights, and a product
+// that fits kv_prod.
+constexpr size_t kKvProdMaxBytes = size_t(1) << 30;
+bool kv_batched(const sf_rdt* m, int g, int rows) {
+    const sf_rdt::KvGroup& G = m->kvg[g];
+    const size_t bytes = (size_t)rows * G.blocks.size() * 2 * m->cfg.hidden * 2;
+    return G.contiguous && G.blocks.size() > 1 && rows > 160 && bytes <= kKvProdMaxBytes &&
+           bytes <= m->kv_prod_bytes;
+}
 
 int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, int act, void* C,
            int64_t ldc, int c_dtype, bool accumulate, hipStream_t s, int a_dtype = SF_BF16) {
@@ -437,6 +492,15 @@ size_t gemm_ws_for(const sf_rdt* m, bool prepare, int* status) {
                 if (prepare && status && *status == SF_OK) *status = sf_gemm_prepare(&d);
             }
         }
+    }
+    // each condition group's K/V projections as one GEMM (kv_batched)
+    for (int g = 0; g < 2; ++g) {
+        const int rows = m->kvg[g].rows_max;
+        if (!kv_batched(m, g, rows)) continue;
+        sf_gemm_desc d = kv_group_desc(m, g, nullptr, rows);
+        best = std::max(best, sf_gemm_workspace_bytes(&d));
+        if (g == 0 && c.batch == 1) d.M = m->lang_rows;   // the language rows set now
+        if (prepare && status && *status == SF_OK && kv_batched(m, g, d.M)) *status = sf_gemm_prepare(&d);
     }
     return best;
 }
@@ -654,15 +718,55 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
 
     const int64_t B = c.batch, D = c.hidden, T = c.horizon, S = T + 3, A = c.action_dim;
     const int64_t H = c.heads;
-    // arena layout: parameters, then buffers
+    // arena layout: parameters (each condition group's K/V projections back
+    // to back), then buffers
     size_t off = 0;
-    for (Param& p : m->params) {
+    std::vector<char> in_group(m->params.size(), 0);
+    for (int i = 0; i < c.layers; ++i) {
+        m->kvg[i % 2].blocks.push_back(i);
+        in_group[m->layers[i].ckv_w] = in_group[m->layers[i].ckv_b] = 1;
+    }
+    for (size_t j = 0; j < m->params.size(); ++j) {
+        if (in_group[j]) continue;
+        Param& p = m->params[j];
         p.offset = off;
         off += align256(p.bytes());
         if (p.dtype == SF_I8) {
             p.scale_offset = off;
             off += align256((size_t)p.shape[0] * 4);
         }
+    }
+    size_t kv_w_off[2] = {0, 0}, kv_b_off[2] = {0, 0}, kv_s_off[2] = {0, 0};
+    for (int g = 0; g < 2; ++g) {
+        sf_rdt::KvGroup& G = m->kvg[g];
+        if (G.blocks.empty()) continue;
+        const Param& W0 = m->params[m->layers[G.blocks[0]].ckv_w];
+        const Param& B0 = m->params[m->layers[G.blocks[0]].ckv_b];
+        G.w_dtype = W0.dtype;
+        // back to back when every piece is a multiple of 256 bytes (always
+        // for D = 64 * heads); otherwise the group runs per block
+        G.contiguous = W0.bytes() % 256 == 0 && B0.bytes() % 256 == 0 && (W0.shape[0] * 4) % 256 == 0;
+        kv_w_off[g] = off;
+        for (int i : G.blocks) {
+            m->params[m->layers[i].ckv_w].offset = off;
+            off += align256(m->params[m->layers[i].ckv_w].bytes());
+        }
+        kv_b_off[g] = off;
+        for (int i : G.blocks) {
+            m->params[m->layers[i].ckv_b].offset = off;
+            off += align256(m->params[m->layers[i].ckv_b].bytes());
+        }
+        kv_s_off[g] = off;
+        for (int i : G.blocks) {
+            Param& p = m->params[m->layers[i].ckv_w];
+            if (p.dtype != SF_I8) continue;
+            p.scale_offset = off;
+            off += align256((size_t)p.shape[0] * 4);
+        }
+        G.rows_max = g == 0 ? (int)(B * c.lang_max) : (int)(B * c.img_len);
+        const size_t prod = (size_t)G.rows_max * G.blocks.size() * 2 * D * 2;
+        if (G.contiguous && G.blocks.size() > 1 && G.rows_max > 160 && prod <= kKvProdMaxBytes)
+            m->kv_prod_bytes = std::max(m->kv_prod_bytes, prod);
     }
     struct Buf { void** ptr; size_t bytes; };
     const int64_t adapt_rows = B * std::max(c.lang_max, c.img_len);
@@ -703,6 +807,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     m->attn_ws_bytes = std::max(attn_ws_for(c, c.lang_max), attn_ws_for(c, c.img_len));
     m->attn_ws_bytes = std::max(m->attn_ws_bytes, attn_ws_for(c, (int)S));
     bufs.push_back({&m->attn_ws, std::max<size_t>(m->attn_ws_bytes, 256)});
+    if (m->kv_prod_bytes) bufs.push_back({(void**)&m->kv_prod, m->kv_prod_bytes});
     m->gemm_ws_bytes = gemm_ws_for(m, false, nullptr);
     bufs.push_back({&m->gemm_ws, std::max<size_t>(m->gemm_ws_bytes, 256)});
     if (S * B > 160) {   // every block's int8 weights as bf16 codes
@@ -725,6 +830,13 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     for (Param& p : m->params) {
         p.data = m->arena + p.offset;
         if (p.dtype == SF_I8) p.scale = reinterpret_cast<float*>(m->arena + p.scale_offset);
+    }
+    for (int g = 0; g < 2; ++g) {
+        sf_rdt::KvGroup& G = m->kvg[g];
+        if (G.blocks.empty()) continue;
+        G.W = m->arena + kv_w_off[g];
+        G.bias = reinterpret_cast<const float*>(m->arena + kv_b_off[g]);
+        G.scale = G.w_dtype == SF_I8 ? reinterpret_cast<const float*>(m->arena + kv_s_off[g]) : nullptr;
     }
     for (size_t i = 0; i < bufs.size(); ++i) *bufs[i].ptr = m->arena + boff[i];
     m->codes16_of.assign(m->params.size(), nullptr);
@@ -878,18 +990,48 @@ extern "C" int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t
     // lang_c + lang_cond_pos_embed[:L], img_c + img_cond_pos_embed (rdt1b.cpp:342-349)
     SF_TRY(sf_add_pos_bf16(lang_c, pf(m, m->lpos), m->lang_c, B, Lr, D, s));
     SF_TRY(sf_add_pos_bf16(img_c, pf(m, m->ipos), m->img_c, B, c.img_len, D, s));
-    // every block's K/V projection with k_norm, once per inference
-    for (int i = 0; i < c.layers; ++i) {
-        const bool lang = (i % 2) == 0;
+    // every block's K/V projection with k_norm, once per inference: above
+    // 160 rows the projection is stored in bf16 before split_kv / k_norm, as
+    // the reference's kv = gemm_bias_act(...) is (dit_block.cu:291-308) --
+    // there the blocks attending to one condition run as one GEMM when it
+    // fits (kv_batched), split per block by sf_heads_bf16
+    for (int grp = 0; grp < 2; ++grp) {
+        const sf_rdt::KvGroup& G = m->kvg[grp];
+        const bool lang = grp == 0;
         const int Sc = lang ? c.lang_max : c.img_len;
         const int rows = lang && B == 1 ? Lr : B * Sc;   // batch 1: the L language rows only
-        uint16_t* kv[2] = {m->ck[i], m->cv[i]};
-        const int g[2] = {m->layers[i].ck_norm, -1};
-        // above 160 rows the projection is stored in bf16 before split_kv /
-        // k_norm, as the reference's kv = gemm_bias_act(...) is
-        // (dit_block.cu:291-308)
-        SF_TRY(linear_heads(m, lang ? m->lang_c : m->img_c, rows, Sc, m->layers[i].ckv_w,
-                            m->layers[i].ckv_b, kv, g, 2, s, SF_BF16, true));
+        const void* A = lang ? m->lang_c : m->img_c;
+        const bool batched = kv_batched(m, grp, rows);
+        if (batched) {
+            const sf_gemm_desc d = kv_group_desc(m, grp, A, rows);
+            SF_TRY(sf_gemm(&d, s));
+        }
+        for (size_t j = 0; j < G.blocks.size(); ++j) {
+            const int i = G.blocks[j];
+            uint16_t* kv[2] = {m->ck[i], m->cv[i]};
+            const int g[2] = {m->layers[i].ck_norm, -1};
+            if (!batched) {
+                SF_TRY(linear_heads(m, A, rows, Sc, m->layers[i].ckv_w, m->layers[i].ckv_b, kv, g, 2, s,
+                                    SF_BF16, true));
+                continue;
+            }
+            sf_gemm_desc h{};
+            h.M = rows;
+            h.N = 2 * D;
+            h.epilogue = SF_EPI_HEADS;
+            h.H = c.heads;
+            h.S = Sc;
+            h.eps = c.eps;
+            for (int q = 0; q < 2; ++q) {
+                h.head_out[q] = kv[q];
+                h.head_gamma[q] = g[q] >= 0 ? pf(m, g[q]) : nullptr;
+                h.head_stride[q][0] = (int64_t)c.heads * Sc * 64;
+                h.head_stride[q][1] = (int64_t)Sc * 64;
+                h.head_stride[q][2] = 64;
+            }
+            const int64_t ldp = (int64_t)G.blocks.size() * 2 * D;
+            SF_TRY(sf_heads_bf16(&h, m->kv_prod + j * 2 * D, ldp, s));
+        }
     }
     // each layer's max |V| for the choice of P.V form (resolve_pv_forms)
     if (c.layers > 0) {
@@ -933,6 +1075,10 @@ extern "C" int sf_rdt_set_lang_rows(sf_rdt* m, int32_t rows) {
         d.a_dtype = SF_BF16;
         d.ldw = d.K;
         d.w_dtype = m->params[widx[j]].dtype;
+        SF_TRY(sf_gemm_prepare(&d));
+    }
+    if (kv_batched(m, 0, rows)) {   // the language blocks' K/V projections as one GEMM
+        const sf_gemm_desc d = kv_group_desc(m, 0, nullptr, rows);
         SF_TRY(sf_gemm_prepare(&d));
     }
     return SF_OK;

@@ -595,3 +595,46 @@ def test_absmax_bf16_batched_matches_torch():
             assert torch.isinf(got[j])
         else:
             assert got[j] == b[:n].float().abs().max().cpu(), j
+
+
+@pytest.mark.parametrize("ldp_extra,aligned", [(4096, True), (4, False)])
+def test_heads_bf16_splits_a_strided_product(ldp_extra, aligned):
+    """sf_heads_bf16 on a bf16 product inside a wider matrix (row stride
+    ldp > N): section 0 per-head RMS-normalised with its gamma, section 1
+    copied, both scattered to [B, H, S, 64]; against the oracle's split_kv
+    + rms_norm on the same bf16 values, within one bf16 ulp.  A row stride
+    that is not a multiple of 8 runs the 4-column kernel."""
+    import ctypes
+    dev = torch.device(DEV)
+    B, S, H = 2, 203, 32
+    M, N = B * S, 2 * H * 64
+    ldp = N + ldp_extra
+    g = torch.Generator(device=dev).manual_seed(5)
+    big = torch.randn(M, ldp, device=dev, generator=g).to(torch.bfloat16)
+    col0 = 64 if aligned else 4
+    P = big[:, col0:col0 + N]
+    gamma = (torch.rand(64, device=dev, generator=g) + 0.5).float()
+    outs = [torch.full((B, H, S, 64), float("nan"), device=dev, dtype=torch.bfloat16) for _ in range(2)]
+    d = abi.GemmDesc()
+    d.M, d.N = M, N
+    d.epilogue = abi.SF_EPI_HEADS
+    d.H, d.S, d.eps = H, S, 1e-6
+    for j, o in enumerate(outs):
+        d.head_out[j] = o.data_ptr()
+        d.head_stride[j][:] = (o.stride(0), o.stride(1), o.stride(2))
+    d.head_gamma[0] = gamma.data_ptr()
+    abi.check(abi.lib().sf_heads_bf16(ctypes.byref(d), P.data_ptr(), ldp, torch.cuda.current_stream().cuda_stream),
+              "sf_heads_bf16")
+    torch.cuda.synchronize()
+    kv = P.float().cpu().numpy().reshape(B, S, N)
+    k_ref, v_ref = O.split_kv(kv, H, 64)
+    k_ref = O.bf16_round(O.rms_norm(k_ref, gamma.cpu().numpy(), 1e-6))
+    for got, ref in ((outs[0], k_ref), (outs[1], v_ref)):
+        got = got.float().cpu().numpy()
+        assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
+        assert np.mean(got == ref) > 0.99
+    # argument checks (no launch)
+    assert abi.lib().sf_heads_bf16(ctypes.byref(d), P.data_ptr(), N - 4, None) == abi.SF_EINVAL
+    assert abi.lib().sf_heads_bf16(ctypes.byref(d), P.data_ptr() + 2, ldp, None) == abi.SF_EINVAL
+    d.N = N + 64
+    assert abi.lib().sf_heads_bf16(ctypes.byref(d), P.data_ptr(), ldp, None) == abi.SF_EINVAL

@@ -130,8 +130,13 @@ def test_block_stack_matches_oracle():
     assert_within_floor(got, ref, floor, "3-block stack residual")
 
 
-def test_kv_cache_matches_oracle():
-    c = small_cfg()
+@pytest.mark.parametrize("layers,int8", [(2, 0), (4, 0), (4, 1)])
+def test_kv_cache_matches_oracle(layers, int8):
+    """Every block's cached K/V against the oracle.  With 4 layers each
+    condition has two blocks and more than 160 rows (192 language, 400
+    image at batch 2): their projections run as one GEMM over the blocks'
+    back-to-back weights, split per block by sf_heads_bf16."""
+    c = small_cfg(layers=layers, int8_weights=int8)
     m = build(c)
     lang, ll, img, state = make_condition(c)
     set_cond(m, lang, ll, img, state)
