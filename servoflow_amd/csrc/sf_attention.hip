@@ -12,7 +12,10 @@
 //   * grid = (splits x query-chunks, H, B); a workgroup of 4 waves owns one
 //     (b, h, query chunk of 80 rows, key split); up to two fit on a CU.
 //     Splitting the keys (flash-decoding) is what fills 256 CUs when
-//     B*H = 32.
+//     B*H = 32 and the keys are many (the image).  With at most 1024 keys
+//     (the language) such grids run one 16-row query block per workgroup
+//     over all keys instead (QB = 1: no split, no merge pass), a head's
+//     blocks on one XCD so its K/V are fetched into that L2 once.
 //   * K/V tiles of 128 keys are streamed HBM -> LDS by buffer_load ... lds
 //     (16-byte, coalesced, no VGPR staging) into a two-stage ring, so the
 //     next tile's loads are in flight while the current one is contracted;
@@ -331,7 +334,8 @@ __device__ __forceinline__ void ring_wait_k() {
 // kExactPV false: P.V in fp16 with P rounded to fp16 (a bf16 V converted,
 // exact for 2^-14 <= |v| < 2^16; an fp16 V as is).  true: V in its input
 // type and P as a (hi, lo) pair of that type.  kF16: Q/K/V are fp16 (S on
-// the fp16 MFMA) instead of bf16.
+// the fp16 MFMA) instead of bf16.  QB: 16-row query blocks per workgroup
+// (kQB on the (split x chunk, H, B) grid; 1 on the XCD-grouped 1-D grid).
 template <bool kExactPV, bool kF16, int QB>
 __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     using v8 = typename In16<kF16>::v8;
