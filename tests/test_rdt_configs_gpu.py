@@ -156,6 +156,33 @@ def test_run_blocks_int8_large_batch_block_range():
     assert mx <= 2e-2 * scale and mr <= 4 * floor
 
 
+@pytest.mark.parametrize("int8", [0, 1])
+def test_odd_shapes_denoise_step(int8):
+    """A configuration off the RDT-1B grid: hidden 1024 (16 heads), 3
+    blocks, batch 3 (201 rows per projection: the library path), 77
+    language and 129 image condition tokens.  B*H = 48 leaves the
+    query-block grid's last head group padded; the language blocks (0, 2)
+    project their K/V as one GEMM, the single image block per call; lengths
+    off every multiple of 16.  Denoise step against the oracle."""
+    print(f"odd shapes int8={int8}", flush=True)
+    c = small_cfg(hidden=1024, heads=16, layers=3, batch=3, lang_max=77, img_len=129, int8_weights=int8)
+    m = build(c)
+    lang, ll, img, state = make_condition(c, lang_len=[5, 40, 77])
+    set_cond(m, lang, ll, img, state)
+    x_t = O.randn(98, (c.batch, c.horizon, c.action_dim))
+    v = m.denoise_step(torch.from_numpy(x_t).to(DEV), 0.6)
+    got = v.cpu().numpy()
+    p = m.state_dict()
+    oc = oracle_cfg(c)
+    caches = OR.encode_caches(p, lang, img, oc, rb=rb_of(c))
+    for i in range(c.layers):
+        for wv in (0, 1):
+            assert mean_rel(m.cache_numpy(i, wv), caches[i][wv]) < 2e-3, (i, wv)
+    ref, floor = oracle_noise_floor(lambda: OR.denoise_step(p, x_t, 0.6, state, caches, ll, oc, rb=rb_of(c)))
+    print(f"odd shapes int8={int8}: mean-rel {mean_rel(got, ref):.3e} floor {floor:.3e}")
+    assert_within_floor(got, ref, floor, f"odd shapes int8={int8}")
+
+
 # ---- config 3 as written: the MLP 4x block ------------------------------------
 
 def test_mlp4x_block_stack():
