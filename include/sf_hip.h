@@ -120,6 +120,24 @@ typedef struct sf_attn_desc {
     const uint8_t* kv_mask;
     int64_t kv_mask_stride;
     int32_t exact_pv;
+    /* Optional (q_partials != NULL): Q given as the split-K partial sums of
+     * its projection instead of q (which may then be NULL), the per-head
+     * finish of the reference's q = gemm_bias_act(...), split and
+     * apply_qk_norm (dit_block.cu:282-307) done inside the attention:
+     * Q[b][h][s][d] = rmsnorm over d of (sum_j q_partials[j][b*Sq + s][n]
+     * * q_scale[n] + q_bias[n]) * q_gamma[d], rounded to bf16, n = h*64 + d
+     * (q_scale, q_bias, q_gamma each optional; q_eps the norm's epsilon).
+     * q_partials: fp32 [q_splits][B*Sq][H*64] (sf_gemm's SF_EPI_PARTIALS
+     * output), 1 <= q_splits <= 8, summed in ascending order.  bf16 inputs
+     * on the query-block grid only (no key split, B*H*ceil(Sq/80) < 256 and
+     * Sk <= 1024; such calls take that grid even for Sk <= 128); other calls
+     * return SF_ENOTSUP. */
+    const float* q_partials;
+    int32_t q_splits;
+    const float* q_bias;
+    const float* q_scale;
+    const float* q_gamma;
+    float q_eps;
 } sf_attn_desc;
 
 /* Fills a descriptor for contiguous [B,H,S,D] tensors (the layout
@@ -210,7 +228,17 @@ int sf_attn_fwd_noalloc(const sf_attn_desc* desc, const void* q, const void* k,
  * workspaces.
  * ------------------------------------------------------------------------- */
 typedef enum sf_act { SF_ACT_NONE = 0, SF_ACT_GELU_TANH = 1, SF_ACT_SILU = 2 } sf_act;
-typedef enum sf_epilogue { SF_EPI_PLAIN = 0, SF_EPI_HEADS = 1, SF_EPI_ADD_NORM = 2 } sf_epilogue;
+typedef enum sf_epilogue {
+    SF_EPI_PLAIN = 0,
+    SF_EPI_HEADS = 1,
+    SF_EPI_ADD_NORM = 2,
+    /* The split-K path's fp32 K-slice sums stay in the workspace,
+     * [sf_gemm_num_splits][M][N] (no bias, scale, activation; C not
+     * written), for a consumer to finish -- the attention's q_partials.
+     * Only for calls that run split-K (M <= 160 with a workspace); others
+     * return SF_ENOTSUP. */
+    SF_EPI_PARTIALS = 3
+} sf_epilogue;
 
 typedef struct sf_gemm_desc {
     int32_t M, N, K;
@@ -252,6 +280,10 @@ typedef struct sf_gemm_desc {
 size_t sf_gemm_workspace_bytes(const sf_gemm_desc* desc);
 
 int sf_gemm(const sf_gemm_desc* desc, void* stream);
+
+/* K slices the split-K path uses for this shape (M, N, K, a_dtype), 0 when
+ * the call does not run split-K. */
+int32_t sf_gemm_num_splits(const sf_gemm_desc* desc);
 
 /* The SF_EPI_HEADS epilogue on a bf16 projection already in memory -- the
  * reference's split_qkv / split_kv followed by apply_qk_norm

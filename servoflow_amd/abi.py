@@ -50,6 +50,12 @@ class AttnDesc(ctypes.Structure):
         ("kv_mask", ctypes.c_void_p),
         ("kv_mask_stride", ctypes.c_int64),
         ("exact_pv", ctypes.c_int32),
+        ("q_partials", ctypes.c_void_p),
+        ("q_splits", ctypes.c_int32),
+        ("q_bias", ctypes.c_void_p),
+        ("q_scale", ctypes.c_void_p),
+        ("q_gamma", ctypes.c_void_p),
+        ("q_eps", ctypes.c_float),
     ]
 
 
@@ -59,6 +65,7 @@ SF_ACT_SILU = 2
 SF_EPI_PLAIN = 0
 SF_EPI_HEADS = 1
 SF_EPI_ADD_NORM = 2
+SF_EPI_PARTIALS = 3
 
 
 class GemmDesc(ctypes.Structure):
@@ -152,6 +159,8 @@ def lib() -> ctypes.CDLL:
     L.sf_dequant_int8.restype = ctypes.c_int
     L.sf_int8_codes_to_bf16.argtypes = [ctypes.POINTER(CodesJob), i32, vp]
     L.sf_int8_codes_to_bf16.restype = ctypes.c_int
+    L.sf_gemm_num_splits.argtypes = [ctypes.POINTER(GemmDesc)]
+    L.sf_gemm_num_splits.restype = ctypes.c_int32
     L.sf_heads_bf16.argtypes = [ctypes.POINTER(GemmDesc), vp, i64, vp]
     L.sf_heads_bf16.restype = ctypes.c_int
     L.sf_absmax_bf16_batched.argtypes = [ctypes.POINTER(AbsmaxJob), i32, vp]

@@ -69,6 +69,14 @@ struct AttnArgs {
     int out_kind;     // OutKind
     int causal;
     float scale_log2;   // scale * log2(e)
+    // Q from split-K partials (the kQP instance): [q_splits][B*Sq][H*64]
+    const float* qp;
+    int q_splits;
+    uint32_t qp_bytes;   // the partials' extent (buffer range)
+    const float* q_bias;
+    const float* q_scale;
+    const float* q_gamma;
+    float q_eps;
 };
 
 enum OutKind { kOutBF16 = 0, kOutF32 = 1, kOutF16 = 2 };
@@ -336,7 +344,9 @@ __device__ __forceinline__ void ring_wait_k() {
 // type and P as a (hi, lo) pair of that type.  kF16: Q/K/V are fp16 (S on
 // the fp16 MFMA) instead of bf16.  QB: 16-row query blocks per workgroup
 // (kQB on the (split x chunk, H, B) grid; 1 on the XCD-grouped 1-D grid).
-template <bool kExactPV, bool kF16, int QB>
+// kQP (QB = 1, bf16): Q is finished here from its projection's split-K
+// partials (sum, scale, bias, per-head RMSNorm, bf16) instead of loaded.
+template <bool kExactPV, bool kF16, int QB, bool kQP = false>
 __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     using v8 = typename In16<kF16>::v8;
     constexpr int QR = 16 * QB;
@@ -395,12 +405,43 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 
     // Q fragments (B operand of S^T = K.Q^T): row 16qb + r, dims 32hh + 8g..
     v8 qf[QB][2];
+    // kQP: wave w finishes rows q0 + 4w .. q0 + 4w + 3, lane l row
+    // q0 + 4w + l/16 and dims 4(l%16) .. +3 -- the reduce_heads epilogue's
+    // layout and arithmetic, so Q is bit-identical to the unfused path.
+    // Every split's loads go out here, before the ring's first tiles; rows
+    // past Sq and splits past q_splits read as zeros.
+    constexpr int kQPMax = 8;
+    f32x4 qpv[kQP ? kQPMax : 1];
+    f32x4 qbias, qscale, qgam;
+    if constexpr (kQP) {
+        static_assert(QB == 1 && !kF16, "Q from partials: the bf16 query-block instance");
+        const int row = q0 + 4 * w + (lane >> 4);
+        const int c4 = 4 * (lane & 15);
+        const bool rlive = row < a.Sq;
+        const uint32_t rowoff = rlive ? (uint32_t)(((int64_t)b * a.Sq + row) * (a.H * 64) + h * 64 + c4) : 0u;
+        const uint32_t sstride = (uint32_t)((int64_t)a.B * a.Sq * a.H * 64);
+        const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.qp, a.qp_bytes);
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
+        for (int j = 0; j < kQPMax; ++j) {
+            const uint32_t off = j < a.q_splits && rlive ? (rowoff + j * sstride) * 4u
+                                                         : 0x80000000u;   // past the buffer range: zeros
+            qpv[j] = __builtin_bit_cast(f32x4, buffer_load16(prs, off));
+        }
+        const int nb = h * 64 + c4;
+        const __amdgpu_buffer_rsrc_t brs = make_rsrc(a.q_bias, a.q_bias ? (uint32_t)(a.H * 64 * 4) : 0u);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.q_scale, a.q_scale ? (uint32_t)(a.H * 64 * 4) : 0u);
+        const __amdgpu_buffer_rsrc_t grs = make_rsrc(a.q_gamma, a.q_gamma ? 64u * 4u : 0u);
+        qbias = __builtin_bit_cast(f32x4, buffer_load16(brs, (uint32_t)(nb * 4)));
+        qscale = __builtin_bit_cast(f32x4, buffer_load16(srs, (uint32_t)(nb * 4)));
+        qgam = __builtin_bit_cast(f32x4, buffer_load16(grs, (uint32_t)(c4 * 4)));
+    } else {
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-            qf[qb][hh] = __builtin_bit_cast(
-                v8, buffer_load16(qrs, (uint32_t)(((q0 + 16 * qb + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+                qf[qb][hh] = __builtin_bit_cast(
+                    v8, buffer_load16(qrs, (uint32_t)(((q0 + 16 * qb + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
+    }
 
     // DMA of one tile into a stage: wave w, op j fills LDS chunks
     // (4w + j) * 64 + lane = key * 8 + slot of K (and of V), loading global
@@ -451,6 +492,39 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     // the mask words, and ring_wait waits for one tile at a time.
     issue(0);
     issue(1);
+    if constexpr (kQP) {
+        // Q = rmsnorm_64(sum_j part_j * scale + bias) * gamma in bf16, as
+        // reduce_heads_kernel computes it (slices summed in ascending order;
+        // no scale = 1, no bias = 0, no gamma = no norm), rows exchanged
+        // through LDS so that every wave holds the fragments of all 16.  The
+        // LDS accesses are inline asm: the compiler would otherwise wait for
+        // the in-flight ring DMA in front of them.
+        __shared__ __attribute__((aligned(16))) uint16_t qlds[16 * 64];
+        f32x4 v = qpv[0];
+#pragma unroll
+        for (int j = 1; j < kQPMax; ++j)
+            if (j < a.q_splits) v += qpv[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = v[i] * (a.q_scale ? qscale[i] : 1.f) + qbias[i];
+        if (a.q_gamma) {
+            float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+            ss = row16_sum(ss);
+            const float inv_rms = 1.f / sqrtf(ss / 64.f + a.q_eps);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = v[i] * inv_rms * qgam[i];
+        }
+        const uint32_t qbase = lds_addr(qlds);
+        const uint32_t waddr = qbase + (uint32_t)(((4 * w + (lane >> 4)) * 64 + 4 * (lane & 15)) * 2);
+        const uint32_t wlo = pack_bf16x2(v[0], v[1]), whi = pack_bf16x2(v[2], v[3]);
+        asm volatile("ds_write_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier"
+                     :: "v"(waddr), "v"(uint2{wlo, whi}) : "memory");
+        u32x4 q0w, q1w;
+        const uint32_t raddr = qbase + (uint32_t)((r * 64 + 8 * g) * 2);
+        asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:64\n\ts_waitcnt lgkmcnt(0)"
+                     : "=&v"(q0w), "=&v"(q1w) : "v"(raddr) : "memory");
+        qf[0][0] = __builtin_bit_cast(v8, q0w);
+        qf[0][1] = __builtin_bit_cast(v8, q1w);
+    }
     // Wait for the Q fragments here, behind the first tiles' loads.  Inside
     // the tile loop the compiler would otherwise still count them as
     // outstanding and wait for every in-flight ring load before the first
@@ -1135,6 +1209,12 @@ void launch_ring(bool exact, bool f16, dim3 grid, hipStream_t s, const sfk::Attn
     }
 }
 
+// The query-block grid with Q finished from split-K partials (bf16).
+void launch_ring_qp(bool exact, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
+    if (exact) hipLaunchKernelGGL((sfk::attn_ring_kernel<true, false, 1, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((sfk::attn_ring_kernel<false, false, 1, true>), grid, dim3(256), 0, s, a);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int validate(const sf_attn_desc* d) {
@@ -1158,6 +1238,14 @@ int validate(const sf_attn_desc* d) {
     if (d->kv_mask && ((reinterpret_cast<uintptr_t>(d->kv_mask) & 3) || (d->kv_mask_stride & 3) ||
                        (d->B > 1 && d->kv_mask_stride < d->Sk)))
         return SF_EINVAL;
+    if (d->q_partials) {   // Q finished from its projection's split-K partials
+        if (d->in_dtype != SF_BF16) return SF_ENOTSUP;
+        if (d->q_splits < 1 || d->q_splits > 8) return SF_EINVAL;
+        const void* ptrs[4] = {d->q_partials, d->q_bias, d->q_scale, d->q_gamma};
+        for (const void* p : ptrs)
+            if (reinterpret_cast<uintptr_t>(p) & 15) return SF_EINVAL;
+        if ((int64_t)d->q_splits * d->B * d->Sq * d->H * 64 * 4 > 0x7fffffffLL) return SF_ENOTSUP;
+    }
     // Per-head byte ranges are addressed with 32-bit buffer offsets.
     const int64_t es = d->in_dtype == SF_F32 ? 4 : 2;
     if ((int64_t)d->Sq * d->q_stride[2] * es > 0x7fffffffLL ||
@@ -1252,11 +1340,14 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     int st = validate(d);
     if (st != SF_OK) return st;
     if ((long)d->B * d->H * d->Sq == 0) return SF_OK;
-    if (!q || !k || !v || !out) return SF_EINVAL;
+    const bool q_from_partials = d->q_partials != nullptr;
+    if (!q_from_partials && !q) return SF_EINVAL;
+    if (!k || !v || !out) return SF_EINVAL;
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return SF_EINVAL;
     if (d->B > 65535 || d->H > 65535) return SF_ENOTSUP;
 
-    const bool short_keys = d->Sk <= sfk::kShortMaxKeys && d->num_splits <= 1;
+    // (Q from partials runs the query-block grid whatever the key count)
+    const bool short_keys = d->Sk <= sfk::kShortMaxKeys && d->num_splits <= 1 && !q_from_partials;
     const int ns = short_keys ? 1 : choose_splits(d);
     // one workgroup per 16-row query block: no key split, and a grid of
     // 80-row chunks that would leave CUs idle
@@ -1264,8 +1355,18 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     const bool qblocks = !short_keys && ns == 1 && d->in_dtype != SF_F32 && d->Sk <= kQGroupMaxKeys &&
                          bh * query_chunks(d) < kNumCUs;
     const int nqc = qblocks ? (d->Sq + 15) / 16 : query_chunks(d);
+    if (q_from_partials && !qblocks) return SF_ENOTSUP;
     sfk::AttnArgs a{};
-    a.q = static_cast<const uint16_t*>(q);
+    a.q = static_cast<const uint16_t*>(q_from_partials && !q ? k : q);   // not read with partials
+    if (q_from_partials) {
+        a.qp = d->q_partials;
+        a.q_splits = d->q_splits;
+        a.qp_bytes = (uint32_t)((int64_t)d->q_splits * d->B * d->Sq * d->H * 64 * 4);
+        a.q_bias = d->q_bias;
+        a.q_scale = d->q_scale;
+        a.q_gamma = d->q_gamma;
+        a.q_eps = d->q_eps;
+    }
     a.k = static_cast<const uint16_t*>(k);
     a.v = static_cast<const uint16_t*>(v);
     a.o = out;
@@ -1313,7 +1414,9 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         if (qblocks) {
             const long groups = (bh + 7) / 8;
             if (8L * nqc * groups > 0x7fffffffL) return SF_ENOTSUP;
-            launch_ring<1>(d->exact_pv != 0, f16, dim3((unsigned)(8L * nqc * groups)), s, a);
+            const dim3 grid((unsigned)(8L * nqc * groups));
+            if (q_from_partials) launch_ring_qp(d->exact_pv != 0, grid, s, a);
+            else launch_ring<1>(d->exact_pv != 0, f16, grid, s, a);
         } else {
             launch_ring<sfk::kQB>(d->exact_pv != 0, f16, dim3(ns * nqc, d->H, d->B), s, a);
         }

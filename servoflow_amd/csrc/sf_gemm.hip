@@ -324,16 +324,6 @@ struct SkArgs {
 
 // LDS barrier that leaves outstanding global loads in flight (a plain
 // __syncthreads also waits for every vector-memory load of the wave).
-// Sum over the 16 lanes of each row (DPP quad permutes, then the row's half
-// mirror and mirror: VALU only, no LDS round trip); every lane of the row
-// gets the sum, added in the order of an xor butterfly over 1, 2, 4, 8.
-__device__ __forceinline__ float row16_sum(float x) {
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));   // quad_perm 1,0,3,2
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));   // quad_perm 2,3,0,1
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, true));  // row_half_mirror
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF, true));  // row_mirror
-    return x;
-}
 
 // Sum over the 64 lanes of a wave: the row sums, then the rows paired by
 // v_permlane16_swap and v_permlane32_swap (VALU lane swaps of gfx950).
@@ -1224,6 +1214,8 @@ int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
     e.eps = d->eps;
     if (d->epilogue == SF_EPI_HEADS) {
         SF_CHECK_OK(fill_heads(d, e));
+    } else if (d->epilogue == SF_EPI_PARTIALS) {
+        // no outputs besides the workspace
     } else if (d->epilogue == SF_EPI_PLAIN || d->epilogue == SF_EPI_ADD_NORM) {
         if (!d->C || d->ldc < d->N) return SF_EINVAL;
         if (d->c_dtype != SF_BF16 && d->c_dtype != SF_F32 && d->c_dtype != SF_F16) return SF_ENOTSUP;
@@ -1252,6 +1244,7 @@ int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
 // The split path reads bias / scale / gamma and writes its outputs as
 // 16-byte quads.
 bool splittable(const sf_gemm_desc* d) {
+    if (d->epilogue == SF_EPI_PARTIALS) return true;   // the kernel reads neither bias nor scale
     if (!al16(d->bias) || (d->w_dtype == SF_I8 && !al16(d->w_scale))) return false;
     if (d->epilogue == SF_EPI_HEADS) {
         for (int j = 0; j < 3; ++j)
@@ -1405,6 +1398,12 @@ extern "C" int sf_heads_bf16(const sf_gemm_desc* d, const void* P, int64_t ldp, 
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
 }
 
+extern "C" int32_t sf_gemm_num_splits(const sf_gemm_desc* d) {
+    if (!d) return 0;
+    const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K, d->a_dtype == SF_F32);
+    return p.split ? p.splits : 0;
+}
+
 extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     if (!d) return SF_EINVAL;
     if (d->M < 0 || d->N < 0 || d->K < 0) return SF_EINVAL;
@@ -1416,6 +1415,20 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     const bool a_conv = d->a_dtype != SF_BF16;   // library path: activations rounded to bf16 first
     if (a32 && ((d->lda & 3) || !al16(d->A))) return SF_EINVAL;
     const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K, a32);
+    if (d->epilogue == SF_EPI_PARTIALS) {   // the K-slice sums only, for a consumer to finish
+        if (!p.split || !d->workspace) return SF_ENOTSUP;
+        if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < p.ws_bytes) return SF_EWORKSPACE;
+        if (!al16(d->workspace)) return SF_EINVAL;
+        sfk::SkArgs a{};
+        a.a = d->A;
+        a.w = d->W;
+        a.part = static_cast<float*>(d->workspace);
+        a.lda = d->lda;
+        a.ldw = d->ldw;
+        a.M = d->M; a.N = d->N; a.K = d->K;
+        sfk::launch_splitk(a, p, d->w_dtype == SF_I8, act_kind(d), s);
+        return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+    }
     if (d->workspace && !p.split && splittable(d)) {
         const bool w8 = d->w_dtype == SF_I8;
         const LibPlan lp = plan_library(d->M, d->N, d->K, w8, a_conv);

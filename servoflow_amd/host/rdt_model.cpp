@@ -139,6 +139,11 @@ struct sf_rdt {
     } kvg[2];
     uint16_t* kv_prod = nullptr;   // [rows][blocks * 2D] bf16 product of a batched group
     size_t kv_prod_bytes = 0;
+    // Language blocks at <= 160 rows: the cross-q projection leaves its
+    // split-K partials (SF_EPI_PARTIALS) and the language attention, on its
+    // query-block grid, finishes Q from them (sum, scale, bias, q_norm) --
+    // one launch less per language block.  cq_splits: the partials' count.
+    int cq_splits = 0;
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     void* gemm_ws = nullptr;       // split-K partial sums, shared by the stream's GEMMs
@@ -435,10 +440,21 @@ int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
     return sf_gemm(&d, s);
 }
 
+// Q of a cross-attention given as the cross-q projection's split-K
+// partials (sf_attn_desc.q_partials).
+struct QPartials {
+    const float* p = nullptr;
+    int splits = 0;
+    const float* bias = nullptr;
+    const float* scale = nullptr;
+    const float* gamma = nullptr;
+};
+
 // Sc: the rows per head of the K/V buffer (its capacity), Sk <= Sc the keys
-// read.
+// read.  qp: Q from partials instead of q (which is then not read).
 int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v, int Sk,
-              const int32_t* valid_len, void* out, bool exact_pv, hipStream_t s, int Sc = 0) {
+              const int32_t* valid_len, void* out, bool exact_pv, hipStream_t s, int Sc = 0,
+              const QPartials* qp = nullptr) {
     const sf_rdt_config& c = m->cfg;
     const int S = c.horizon + 3;
     sf_attn_desc d;
@@ -458,6 +474,14 @@ int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v
     }
     d.kv_valid_len = valid_len;
     d.exact_pv = exact_pv ? 1 : 0;
+    if (qp) {
+        d.q_partials = qp->p;
+        d.q_splits = qp->splits;
+        d.q_bias = qp->bias;
+        d.q_scale = qp->scale;
+        d.q_gamma = qp->gamma;
+        d.q_eps = c.eps;
+    }
     // output straight into [B, S, H*64] (head_to_seq fused away)
     d.o_stride[0] = (int64_t)S * c.hidden;
     d.o_stride[1] = 64;
@@ -570,13 +594,40 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     SF_TRY(linear_add_norm(m, m->a, SF_BF16, M, L.proj_w, L.proj_b, L.norm2, m->n, SF_BF16, s));
     // cross-attention branch: even blocks attend to language, odd to image
     // (dit_block.cu:369)
-    uint16_t* cq[1] = {m->q};
-    const int cq_g[1] = {L.cq_norm};
-    SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s, SF_BF16, true));
     const bool lang = (i % 2) == 0;
-    SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? m->cond_lang_rows : c.img_len,
-                     lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,
-                     lang ? c.lang_max : c.img_len));
+    if (lang && m->cq_splits > 0) {   // Q finished inside the attention
+        const Param& W = m->params[L.cq_w];
+        sf_gemm_desc d{};
+        d.M = M;
+        d.N = (int32_t)W.shape[0];
+        d.K = (int32_t)W.shape[1];
+        d.A = m->n;
+        d.lda = D;
+        d.a_dtype = SF_BF16;
+        d.W = W.data;
+        d.ldw = W.shape[1];
+        d.w_dtype = W.dtype;
+        d.w_scale = W.scale;
+        d.epilogue = SF_EPI_PARTIALS;
+        d.workspace = m->gemm_ws;
+        d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
+        SF_TRY(sf_gemm(&d, s));
+        QPartials qp;
+        qp.p = static_cast<const float*>(m->gemm_ws);
+        qp.splits = m->cq_splits;
+        qp.bias = pf(m, L.cq_b);
+        qp.scale = W.scale;
+        qp.gamma = pf(m, L.cq_norm);
+        SF_TRY(attention(m, nullptr, m->ck[i], m->cv[i], m->cond_lang_rows, m->lang_len, m->a,
+                         m->exact_pv[i] != 0, s, c.lang_max, &qp));
+    } else {
+        uint16_t* cq[1] = {m->q};
+        const int cq_g[1] = {L.cq_norm};
+        SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s, SF_BF16, true));
+        SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? m->cond_lang_rows : c.img_len,
+                         lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,
+                         lang ? c.lang_max : c.img_len));
+    }
     SF_TRY(linear_add_norm(m, m->a, SF_BF16, M, L.cproj_w, L.cproj_b, L.norm3, m->n3, fd, s));
     // FFN branch (Mlp::forward, dit_block.cu:143-163); fc2's add + norm
     // writes the next block's norm1 (bf16, the QKV input)
@@ -852,6 +903,19 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     }
     m->exact_pv.assign(c.layers, 0);
     m->lang_rows = m->cond_lang_rows = c.lang_max;
+    if (c.layers > 0) {   // the fused cross-q finish (see cq_splits)
+        sf_gemm_desc g{};
+        g.M = (int32_t)(B * S);
+        g.N = (int32_t)D;
+        g.K = (int32_t)D;
+        g.a_dtype = SF_BF16;
+        const int splits = sf_gemm_num_splits(&g);
+        sf_attn_desc a;
+        sf_attn_desc_init_bhsd(&a, (int32_t)B, (int32_t)H, (int32_t)S, c.lang_max, 64, SF_BF16, SF_BF16);
+        const bool qblocks = B * H * ((S + 79) / 80) < 256 && c.lang_max <= 1024 && sf_attn_num_splits(&a) == 1;
+        if (splits >= 1 && splits <= 8 && qblocks && (size_t)splits * B * S * D * 4 <= m->gemm_ws_bytes)
+            m->cq_splits = splits;
+    }
     if (hipStreamCreate(&m->own_stream) != hipSuccess) {
         (void)hipFree(m->arena);
         delete m;

@@ -232,3 +232,24 @@ def test_absmax_batched_rejects_bad_jobs():
         one[0].p, one[0].n, one[0].out = 256, 64, 512
         setattr(one[0], field, bad)
         assert lib.sf_absmax_bf16_batched(one, 1, None) == abi.SF_EINVAL, (field, bad)
+
+
+def test_gemm_partials_mode_contract():
+    """sf_gemm_num_splits: the split-K slice count of a shape (0 above 160
+    rows); SF_EPI_PARTIALS needs a call that runs split-K with a workspace
+    (SF_ENOTSUP otherwise, before any launch)."""
+    lib = abi.lib()
+    g = abi.GemmDesc()
+    g.M, g.N, g.K = 67, 2048, 2048
+    g.A, g.lda, g.a_dtype = 256, 2048, abi.SF_BF16
+    g.W, g.ldw, g.w_dtype = 512, 2048, abi.SF_BF16
+    g.epilogue = abi.SF_EPI_PARTIALS
+    assert lib.sf_gemm_num_splits(ctypes.byref(g)) == 8
+    g.K = 8192   # 32 slices of 256 would exceed 16: 512-wide slices
+    assert lib.sf_gemm_num_splits(ctypes.byref(g)) == 16
+    g.K = 2048
+    assert lib.sf_gemm(ctypes.byref(g), None) == abi.SF_ENOTSUP          # no workspace
+    g.M = 161
+    assert lib.sf_gemm_num_splits(ctypes.byref(g)) == 0
+    g.workspace, g.workspace_bytes = 1024, 1 << 30
+    assert lib.sf_gemm(ctypes.byref(g), None) == abi.SF_ENOTSUP          # library path

@@ -461,3 +461,107 @@ def test_query_block_grid(B, H, Sq, Sk, causal, vl, dt, exact):
                         valid_len=None if lens is None else to_dev(lens[b:b + 1], torch.int32), **kw)
         torch.cuda.synchronize()
         assert np.array_equal(one.cpu().numpy()[0], got[b]), b
+
+
+@pytest.mark.parametrize("B,H,Sk,vl,splits,scale,gamma,exact", [
+    (1, 32, 1024, [517], 8, True, True, False),    # the batch-1 language call of the runtime
+    (2, 32, 100, [100, 37], 4, False, True, False),  # <= 128 keys: still the query-block grid
+    (1, 3, 300, None, 1, True, False, True),         # padded head group, no norm, exact P.V
+])
+def test_q_from_split_k_partials(B, H, Sk, vl, splits, scale, gamma, exact):
+    """sf_attn_desc.q_partials: Q finished inside the attention from its
+    projection's split-K partials (sum in slice order, row scale, bias,
+    per-head RMSNorm, bf16) equals the attention over the same Q finished
+    on the host, up to Q's rare one-ulp roundings (the norm's sum of squares
+    is added in another order); q is not read."""
+    import ctypes
+    dev = torch.device(DEV)
+    Sq, N = 67, H * 64
+    g = torch.Generator(device=dev).manual_seed(300 + splits)
+    part = torch.randn(splits, B * Sq, N, device=dev, generator=g) * 0.3
+    bias = torch.randn(N, device=dev, generator=g) * 0.1
+    sc = (torch.rand(N, device=dev, generator=g) + 0.5) if scale else None
+    gam = (torch.rand(64, device=dev, generator=g) + 0.5) if gamma else None
+    q = part.sum(0, dtype=torch.float32) if splits == 1 else part[0].clone()
+    for j in range(1, splits):
+        q = q + part[j]                               # slice order
+    q = q * (sc if sc is not None else 1.0) + bias
+    q = q.view(B, Sq, H, 64).permute(0, 2, 1, 3).contiguous()
+    if gam is not None:
+        q = q * torch.rsqrt(q.pow(2).mean(-1, keepdim=True) + 1e-6) * gam
+    qb = q.to(torch.bfloat16)
+    k = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    vld = None if vl is None else torch.tensor(vl, dtype=torch.int32, device=dev)
+    ref = attention(qb, k, v, out_dtype=torch.float32, valid_len=vld, exact_pv=exact)
+    out = torch.full((B, H, Sq, 64), float("nan"), device=dev, dtype=torch.float32)
+    d = make_desc(qb, k, v, out, valid_len=vld, exact_pv=exact)
+    d.q_partials, d.q_splits = part.data_ptr(), splits
+    d.q_bias = bias.data_ptr()
+    d.q_scale = sc.data_ptr() if sc is not None else None
+    d.q_gamma = gam.data_ptr() if gam is not None else None
+    d.q_eps = 1e-6
+    st = abi.lib().sf_attn_fwd(ctypes.byref(d), None, k.data_ptr(), v.data_ptr(), out.data_ptr(), None, 0,
+                               torch.cuda.current_stream().cuda_stream)
+    assert st == abi.SF_OK, st
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    diff = (out - ref).abs()
+    assert float(diff.max()) < 2e-2 and float(diff.sum() / ref.abs().sum()) < 2e-3
+    # rejected before any launch: key-split grids, a bad slice count, fp16
+    kk = torch.zeros(1, H, 4374, 64, device=dev, dtype=torch.bfloat16)
+    d2 = make_desc(qb[:1], kk, kk, out[:1])
+    d2.q_partials, d2.q_splits = part.data_ptr(), splits
+    assert abi.lib().sf_attn_fwd(ctypes.byref(d2), None, kk.data_ptr(), kk.data_ptr(), out.data_ptr(), None, 0,
+                                 None) == abi.SF_ENOTSUP
+    d.q_splits = 9
+    assert abi.lib().sf_attn_fwd(ctypes.byref(d), None, k.data_ptr(), v.data_ptr(), out.data_ptr(), None, 0,
+                                 None) == abi.SF_EINVAL
+    d.q_splits, d.in_dtype = splits, abi.SF_F16
+    assert abi.lib().sf_attn_fwd(ctypes.byref(d), None, k.data_ptr(), v.data_ptr(), out.data_ptr(), None, 0,
+                                 None) == abi.SF_ENOTSUP
+
+
+@pytest.mark.parametrize("w8", [False, True])
+def test_q_partials_bit_identical_to_heads_epilogue(w8):
+    """The runtime's two routes to a batch-1 language cross-attention give
+    the same bits: (a) the cross-q projection with the per-head RMSNorm
+    epilogue (SF_EPI_HEADS, split-K + reduce) writing Q, then sf_attn_fwd;
+    (b) the projection's partials (SF_EPI_PARTIALS) finished inside
+    sf_attn_fwd (q_partials) -- the same sums, scale, bias and norm in the
+    same order."""
+    import ctypes
+    from servoflow_amd import kernels as Kn
+    dev = torch.device(DEV)
+    B, H, S, D, Sk = 1, 32, 67, 2048, 1024
+    g = torch.Generator(device=dev).manual_seed(41)
+    a = torch.randn(B * S, D, device=dev, generator=g).to(torch.bfloat16)
+    if w8:
+        w = torch.randint(-127, 128, (D, D), device=dev, generator=g, dtype=torch.int8)
+        ws = torch.rand(D, device=dev, generator=g) * 2e-4 + 1e-4
+    else:
+        w = (torch.randn(D, D, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        ws = None
+    bias = torch.randn(D, device=dev, generator=g) * 0.02
+    gam = torch.rand(64, device=dev, generator=g) + 0.5
+    k = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    vl = torch.tensor([517], dtype=torch.int32, device=dev)
+    q = torch.empty(B, H, S, 64, device=dev, dtype=torch.bfloat16)
+    Kn.gemm_heads(a, w, bias, S, H, [q], (gam,), w_scale=ws)
+    ref = attention(q, k, v, out_dtype=torch.float32, valid_len=vl)
+    d = Kn._desc(a, w, None, abi.SF_ACT_NONE, ws)
+    d.epilogue = abi.SF_EPI_PARTIALS
+    ns = abi.lib().sf_gemm_num_splits(ctypes.byref(d))
+    part = torch.empty(ns, B * S, D, device=dev, dtype=torch.float32)
+    d.workspace, d.workspace_bytes = part.data_ptr(), part.numel() * 4
+    abi.check(abi.lib().sf_gemm(ctypes.byref(d), torch.cuda.current_stream().cuda_stream), "partials")
+    out = torch.empty(B, H, S, 64, device=dev, dtype=torch.float32)
+    ad = make_desc(q, k, v, out, valid_len=vl)
+    ad.q_partials, ad.q_splits = part.data_ptr(), ns
+    ad.q_bias, ad.q_scale, ad.q_gamma, ad.q_eps = bias.data_ptr(), ws.data_ptr() if ws is not None else None, \
+        gam.data_ptr(), 1e-6
+    abi.check(abi.lib().sf_attn_fwd(ctypes.byref(ad), None, k.data_ptr(), v.data_ptr(), out.data_ptr(), None, 0,
+                                    torch.cuda.current_stream().cuda_stream), "attention from partials")
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)

@@ -638,3 +638,42 @@ def test_heads_bf16_splits_a_strided_product(ldp_extra, aligned):
     assert abi.lib().sf_heads_bf16(ctypes.byref(d), P.data_ptr() + 2, ldp, None) == abi.SF_EINVAL
     d.N = N + 64
     assert abi.lib().sf_heads_bf16(ctypes.byref(d), P.data_ptr(), ldp, None) == abi.SF_EINVAL
+
+
+@pytest.mark.parametrize("w8", [False, True])
+def test_gemm_partials_sum_to_the_fp32_product(w8):
+    """SF_EPI_PARTIALS leaves the split-K path's K-slice sums in the
+    workspace ([sf_gemm_num_splits][M][N] fp32, no bias or scale): summed
+    in slice order they equal the fp32 product of the same call with an
+    fp32 C (whose epilogue adds the slices in that order), bit for bit."""
+    import ctypes
+    dev = torch.device(DEV)
+    M, N, KD = 67, 2048, 2048
+    g = torch.Generator(device=dev).manual_seed(11)
+    a = torch.randn(M, KD, device=dev, generator=g).to(torch.bfloat16)
+    if w8:
+        w = torch.randint(-127, 128, (N, KD), device=dev, generator=g, dtype=torch.int8)
+        ws = torch.ones(N, device=dev)
+    else:
+        w = (torch.randn(N, KD, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        ws = None
+    full = K.gemm(a, w, None, out_dtype=torch.float32, w_scale=ws)
+    d = K._desc(a, w, None, abi.SF_ACT_NONE, ws)
+    d.epilogue = abi.SF_EPI_PARTIALS
+    ns = abi.lib().sf_gemm_num_splits(ctypes.byref(d))
+    assert ns == 8
+    buf = torch.empty(ns, M, N, dtype=torch.float32, device=dev)
+    d.workspace, d.workspace_bytes = buf.data_ptr(), buf.numel() * 4
+    abi.check(abi.lib().sf_gemm(ctypes.byref(d), torch.cuda.current_stream().cuda_stream), "sf_gemm partials")
+    torch.cuda.synchronize()
+    tot = buf[0].clone()
+    for j in range(1, ns):
+        tot += buf[j]
+    assert torch.equal(tot, full)
+    # 161 rows take the library path: no partials there
+    a2 = torch.zeros(161, KD, device=dev, dtype=torch.bfloat16)
+    d2 = K._desc(a2, w, None, abi.SF_ACT_NONE, ws)
+    d2.epilogue = abi.SF_EPI_PARTIALS
+    assert abi.lib().sf_gemm_num_splits(ctypes.byref(d2)) == 0
+    d2.workspace, d2.workspace_bytes = buf.data_ptr(), buf.numel() * 4
+    assert abi.lib().sf_gemm(ctypes.byref(d2), None) == abi.SF_ENOTSUP
