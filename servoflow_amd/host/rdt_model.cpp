@@ -489,6 +489,35 @@ int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v
     return sf_attn_fwd(&d, q, k, v, out, m->attn_ws, m->attn_ws_bytes, s);
 }
 
+// The cross-q projection of block L over the M rows of m->n, left as its
+// split-K partials in the GEMM workspace (SF_EPI_PARTIALS); *qp describes
+// them for the language attention, which finishes Q (bias, int8 scale,
+// q_norm) as the heads epilogue would (dit_block.cu:282-307).
+int cross_q_partials(sf_rdt* m, const LayerIdx& L, int M, hipStream_t s, QPartials* qp) {
+    const Param& W = m->params[L.cq_w];
+    sf_gemm_desc d{};
+    d.M = M;
+    d.N = (int32_t)W.shape[0];
+    d.K = (int32_t)W.shape[1];
+    d.A = m->n;
+    d.lda = m->cfg.hidden;
+    d.a_dtype = SF_BF16;
+    d.W = W.data;
+    d.ldw = W.shape[1];
+    d.w_dtype = W.dtype;
+    d.w_scale = W.scale;
+    d.epilogue = SF_EPI_PARTIALS;
+    d.workspace = m->gemm_ws;
+    d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
+    SF_TRY(sf_gemm(&d, s));
+    qp->p = static_cast<const float*>(m->gemm_ws);
+    qp->splits = m->cq_splits;
+    qp->bias = pf(m, L.cq_b);
+    qp->scale = W.scale;
+    qp->gamma = pf(m, L.cq_norm);
+    return SF_OK;
+}
+
 // Every GEMM the runtime issues: each matrix at each row count it is used
 // with (step rows B*S, B*T, B, 1; condition rows B*lang_max, B*img_len).
 // Returns the largest workspace; with prepare, also selects the library
@@ -596,28 +625,8 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     // (dit_block.cu:369)
     const bool lang = (i % 2) == 0;
     if (lang && m->cq_splits > 0) {   // Q finished inside the attention
-        const Param& W = m->params[L.cq_w];
-        sf_gemm_desc d{};
-        d.M = M;
-        d.N = (int32_t)W.shape[0];
-        d.K = (int32_t)W.shape[1];
-        d.A = m->n;
-        d.lda = D;
-        d.a_dtype = SF_BF16;
-        d.W = W.data;
-        d.ldw = W.shape[1];
-        d.w_dtype = W.dtype;
-        d.w_scale = W.scale;
-        d.epilogue = SF_EPI_PARTIALS;
-        d.workspace = m->gemm_ws;
-        d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
-        SF_TRY(sf_gemm(&d, s));
         QPartials qp;
-        qp.p = static_cast<const float*>(m->gemm_ws);
-        qp.splits = m->cq_splits;
-        qp.bias = pf(m, L.cq_b);
-        qp.scale = W.scale;
-        qp.gamma = pf(m, L.cq_norm);
+        SF_TRY(cross_q_partials(m, L, M, s, &qp));
         SF_TRY(attention(m, nullptr, m->ck[i], m->cv[i], m->cond_lang_rows, m->lang_len, m->a,
                          m->exact_pv[i] != 0, s, c.lang_max, &qp));
     } else {

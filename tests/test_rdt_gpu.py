@@ -409,6 +409,33 @@ def test_full_rdt1b_shape_graph_loop():
     assert float((xe - torch.from_numpy(x0).to(DEV)).abs().max()) > 0
 
 
+def test_full_rdt1b_denoise_step_matches_oracle():
+    """The headline configuration at full size: one denoise step of the
+    28-layer batch-1 model (language condition with 517 valid of 1024 rows,
+    4374 image keys, every block's K/V from the cache) against the oracle's
+    storage model within its noise floor, and against the pure-fp32 oracle."""
+    import time
+    c = R.default_config()
+    m = build(c)
+    lang, ll, img, state = make_condition(c, lang_len=[517])
+    set_cond(m, lang, ll, img, state)
+    x_t = O.randn(97, (1, c.horizon, c.action_dim))
+    got = m.denoise_step(torch.from_numpy(x_t).to(DEV), 0.8).cpu().numpy()
+    t0 = time.time()
+    p = m.state_dict()
+    m.close()
+    oc = oracle_cfg(c)
+    caches = OR.encode_caches(p, lang, img, oc, rb=rb_of(c))
+    ref, floor = oracle_noise_floor(lambda: OR.denoise_step(p, x_t, 0.8, state, caches, ll, oc, rb=rb_of(c)))
+    print(f"full-size step: mean-rel {mean_rel(got, ref):.3e} floor {floor:.3e} "
+          f"max-abs {float(np.abs(got - ref).max()):.3e} (oracle {time.time() - t0:.1f} s)", flush=True)
+    assert_within_floor(got, ref, floor, "full-size denoise step")
+    del caches
+    ref32 = OR.denoise_step(p, x_t, 0.8, state, OR.encode_caches(p, lang, img, oc, rb=False), ll, oc, rb=False)
+    print(f"full-size step vs fp32: mean-rel {mean_rel(got, ref32):.3e}", flush=True)
+    assert mean_rel(got, ref32) < 2e-2
+
+
 def _hf_checkpoint(model, path, int8_as_fp32=False):
     """Writes model's parameters with HuggingFace naming (blocks and final
     layer under "model.", adaptors as-is) plus entries the loader must skip,
