@@ -3,7 +3,7 @@
 
 Prints ONE JSON line (the driver's contract).
 
-Headline (`value`, BASELINE config 4 at batch 1): latency of one full
+Headline (`value`, the denoise-loop configuration at batch 1): latency of one full
 denoise loop -- 5 Euler steps of the 28-layer RDT-1B (hidden 2048, 32 heads,
 67 tokens, FFN 1x) with the condition K/V projected once per inference and
 cached -- replayed as one hipGraph.  One bench "step" is one such inference

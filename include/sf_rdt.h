@@ -83,8 +83,9 @@ int sf_absmax_bf16_batched(const sf_absmax_job* jobs, int32_t count, void* strea
 
 /* RDT1BConfig (include/servoflow/models/rdt1b/config.h:26-71) plus the batch
  * and weight format.  The reference's FFN has no expansion (config.h:60-61);
- * mlp_ratio > 1 builds the D -> mlp_ratio*D -> D variant (BASELINE's
- * "MLP 4x" block, no reference counterpart). */
+ * mlp_ratio > 1 builds the D -> mlp_ratio*D -> D variant (the "MLP 4x"
+ * block of the benchmarked block-stack configuration, no reference
+ * counterpart). */
 typedef struct sf_rdt_config {
     int32_t hidden;              /* 2048 */
     int32_t layers;              /* 28 */

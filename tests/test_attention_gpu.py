@@ -4,7 +4,7 @@ Inputs are N(0,1) from the oracle's SplitMix64/Box-Muller generator, rounded
 to bf16; the oracle receives the same rounded values in fp32.  The kernel's
 fp32 output must satisfy max-abs <= 2e-2 and sum|d|/sum|ref| <= 1e-3; its bf16
 output must be the fp32 output rounded to nearest (within one bf16 ulp).
-Full-size shapes follow BASELINE configs 1-2: self-attention 67x67, image
+Full-size shapes are the benchmarked ops: self-attention 67x67, image
 cross-attention 67x4374 and language cross-attention 67x<=1024 with a
 per-batch valid length, 32 heads x 64, batch 1 and 8.
 """
@@ -366,7 +366,7 @@ def test_key_padding_mask(Sk):
 
 @pytest.mark.parametrize("exact_pv", [False, True])
 def test_full_size_b8_image_properties(exact_pv):
-    """The BASELINE batch-8 image shape (8x32x67x4374), checked through
+    """The benchmarked batch-8 image shape (8x32x67x4374), checked through
     properties that hold at any size: doubling V doubles the fp32 output bit
     for bit (the fp16 conversion of V -- exact in fp16's normal range, so V
     is kept at |v| >= 2^-13 here --, the bf16 (hi, lo) form and the fp32

@@ -1,7 +1,7 @@
-"""GPU parity of the RDT-1B runtime at the BASELINE configurations the
+"""GPU parity of the RDT-1B runtime at the benchmarked configurations the
 other model tests do not reach: one full-width block against the pure-fp32
 oracle, batch 16 and int8 batch 32 (the library-path
-GEMMs at M = 1072 / 2144), the "MLP 4x" block of config 3, and full-depth
+GEMMs at M = 1072 / 2144), the "MLP 4x" block-stack variant, and full-depth
 batch-slot consistency at batch 16.
 
 Oracle: oracle/rdt.py (pinned against the reference's PyTorch RDT by
@@ -186,7 +186,7 @@ def test_odd_shapes_denoise_step(int8):
 # ---- config 3 as written: the MLP 4x block ------------------------------------
 
 def test_mlp4x_block_stack():
-    """BASELINE config 3 names an MLP 4x block (fc1 2048 -> 8192, fc2
+    """The benchmarked block-stack configuration names an MLP 4x block (fc1 2048 -> 8192, fc2
     8192 -> 2048); the reference's RDT-1B has 1x (config.h:60-61), so this
     is the synthetic variant.  Two full-width blocks against the oracle."""
     print("mlp4x block stack", flush=True)
