@@ -131,13 +131,25 @@ typedef struct sf_attn_desc {
      * output), 1 <= q_splits <= 8, summed in ascending order.  bf16 inputs
      * on the query-block grid only (no key split, B*H*ceil(Sq/80) < 256 and
      * Sk <= 1024; such calls take that grid even for Sk <= 128); other calls
-     * return SF_ENOTSUP. */
+     * return SF_ENOTSUP.
+     * Without q_partials, q_gamma and k_gamma (each optional, fp32 [64],
+     * 16-byte aligned) apply the reference's per-head RMSNorm
+     * (apply_qk_norm, dit_block.cu:185-196 and 262-272, called at 218-220
+     * and 306-308; rms_norm_kernel_impl, norm.cuh:89-122) to every Q / K
+     * row as it is loaded:
+     * row[d] * (1 / sqrt(sum_d row[d]^2 / 64 + q_eps)) * gamma[d], rounded to
+     * bf16 -- bit for bit what sf_gemm's per-head epilogue over a bf16
+     * product (SF_EPI_HEADS above 160 rows) stores.  With q/k/v and their
+     * strides pointing into a projection's bf16 output (row b*S + s, column
+     * section*H*64 + h*64 + d) this takes the place of split_qkv / split_kv +
+     * apply_qk_norm.  bf16 inputs only (SF_ENOTSUP otherwise). */
     const float* q_partials;
     int32_t q_splits;
     const float* q_bias;
     const float* q_scale;
     const float* q_gamma;
     float q_eps;
+    const float* k_gamma;
 } sf_attn_desc;
 
 /* Fills a descriptor for contiguous [B,H,S,D] tensors (the layout

@@ -56,6 +56,7 @@ class AttnDesc(ctypes.Structure):
         ("q_scale", ctypes.c_void_p),
         ("q_gamma", ctypes.c_void_p),
         ("q_eps", ctypes.c_float),
+        ("k_gamma", ctypes.c_void_p),
     ]
 
 

@@ -24,7 +24,7 @@ def _strides3(t: torch.Tensor):
 
 
 def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_splits=0, kv_mask=None,
-              exact_pv=False):
+              exact_pv=False, q_gamma=None, k_gamma=None, qk_eps=1e-6):
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     if k.shape != (B, H, Sk, D) or v.shape != (B, H, Sk, D) or out.shape != (B, H, Sq, D):
@@ -48,6 +48,12 @@ def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_spli
         d.kv_mask = kv_mask.data_ptr()
         d.kv_mask_stride = kv_mask.stride(0)
     d.exact_pv = 1 if exact_pv else 0
+    for name, gm in (("q_gamma", q_gamma), ("k_gamma", k_gamma)):
+        if gm is not None:
+            if gm.dtype != torch.float32 or gm.numel() != D or not gm.is_cuda or not gm.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous device float32 tensor of D elements")
+            setattr(d, name, gm.data_ptr())
+    d.q_eps = float(qk_eps)
     for name, t in (("q_stride", q), ("k_stride", k), ("v_stride", v), ("o_stride", out)):
         getattr(d, name)[:] = _strides3(t)
     return d
@@ -58,18 +64,23 @@ def workspace_bytes(desc) -> int:
 
 
 def attention(q, k, v, out=None, scale=0.0, is_causal=False, valid_len=None, num_splits=0,
-              out_dtype=None, workspace=None, stream=None, kv_mask=None, exact_pv=False):
+              out_dtype=None, workspace=None, stream=None, kv_mask=None, exact_pv=False,
+              q_gamma=None, k_gamma=None, qk_eps=1e-6):
     """Runs sf_attn_fwd on torch's current stream (or `stream`) and returns `out`.
     kv_mask: optional device bool [B, Sk] key-padding mask (True = attend);
     its rows must be readable for Sk rounded up to 4 bytes.
     exact_pv: bf16 V and P as a bf16 (hi, lo) pair instead of the fp16 P.V
     contraction (which converts V exactly for 2^-14 <= |V| < 2^16, to within
     2^-25 below; a larger element makes its output column inf/NaN; see
-    sf_attn_desc)."""
+    sf_attn_desc).
+    q_gamma / k_gamma: optional float32 [D] weights of a per-head RMSNorm
+    (epsilon qk_eps) applied to each Q / K row as it is loaded (bf16 inputs;
+    K only for key sets of at most 128)."""
     if out is None:
         od = out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=od, device=q.device)
-    desc = make_desc(q, k, v, out, scale, is_causal, valid_len, num_splits, kv_mask, exact_pv)
+    desc = make_desc(q, k, v, out, scale, is_causal, valid_len, num_splits, kv_mask, exact_pv,
+                     q_gamma, k_gamma, qk_eps)
     need = workspace_bytes(desc)
     if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)   # needs no init

@@ -75,8 +75,9 @@ struct AttnArgs {
     uint32_t qp_bytes;   // the partials' extent (buffer range)
     const float* q_bias;
     const float* q_scale;
-    const float* q_gamma;
+    const float* q_gamma;   // per-head RMSNorm weight of Q (with or without partials)
     float q_eps;
+    const float* k_gamma;   // per-head RMSNorm weight of K (the short-key kernel)
 };
 
 enum OutKind { kOutBF16 = 0, kOutF32 = 1, kOutF16 = 2 };
@@ -205,6 +206,66 @@ __device__ __forceinline__ float max_xor16(float x) {
 __device__ __forceinline__ float max_xor32(float x) {
     const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
+// x of lane l plus x of lane l ^ 16 (l ^ 32): lanes l, l ^ 16, l ^ 32 and
+// l ^ 48 hold the four 8-element pieces of one MFMA operand row per register.
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
+// Per-head RMSNorm of one bf16 row held as an MFMA operand (lane 16g + r:
+// head dims 8g..8g+7 in f[0], 32+8g..32+8g+7 in f[1]), times gamma
+// (gm[hh][0..1]: gamma[32hh + 8g ..+7]), rounded to bf16 in place -- the
+// reference's rms_norm over head_dim (norm.cuh:89-122).  The arithmetic and
+// the summation order are those of sf_gemm's per-head epilogue over a bf16
+// product (heads16_kernel): each lane's eight squares in dim order, then
+// the row's eight partial sums as ((s0 + s1) + (s2 + s3)) + ((s4 + s5) +
+// (s6 + s7)), so the result is bit-identical to that epilogue's.
+__device__ __forceinline__ void rms_norm_row_bf16(bf16x8 (&f)[2], const f32x4 (&gm)[2][2], float eps) {
+    float v[2][8];
+    float part[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const u32x4 w = __builtin_bit_cast(u32x4, f[hh]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[hh][2 * e] = bf16_bits_to_f32(w[e] & 0xffffu);
+            v[hh][2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += v[hh][j] * v[hh][j];
+        part[hh] = sum_xor32(sum_xor16(ss));
+    }
+    const float inv_rms = 1.f / sqrtf((part[0] + part[1]) / 64.f + eps);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const f32x4 g4 = gm[hh][e >> 1];
+            w[e] = pack_bf16x2(v[hh][2 * e] * inv_rms * g4[(2 * e) & 3],
+                               v[hh][2 * e + 1] * inv_rms * g4[(2 * e + 1) & 3]);
+        }
+        f[hh] = u32x4_as_bf16x8(w);
+    }
+}
+
+// The eight gamma values of each of a lane's two operand pieces (zeros for
+// a null gamma: a zero-range buffer reads zeros).
+__device__ __forceinline__ void load_norm_gamma(const float* gamma, int g, f32x4 (&gm)[2][2]) {
+    const __amdgpu_buffer_rsrc_t grs = make_rsrc(gamma, gamma ? 64u * 4u : 0u);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            gm[hh][i] = __builtin_bit_cast(f32x4, buffer_load16(grs, (uint32_t)((32 * hh + 8 * g + 4 * i) * 4)));
 }
 
 // Epilogue of the ring kernel: the four waves' (m, l, O) merged through LDS
@@ -442,6 +503,9 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
                 qf[qb][hh] = __builtin_bit_cast(
                     v8, buffer_load16(qrs, (uint32_t)(((q0 + 16 * qb + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
     }
+    // q_norm weight for Q rows normalised as they are loaded (bf16)
+    f32x4 qgm[2][2];
+    if constexpr (!kQP && !kF16) load_norm_gamma(a.q_gamma, g, qgm);
 
     // DMA of one tile into a stage: wave w, op j fills LDS chunks
     // (4w + j) * 64 + lane = key * 8 + slot of K (and of V), loading global
@@ -533,6 +597,12 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) asm volatile("" ::"v"(qf[qb][hh]));
+    if constexpr (!kQP && !kF16) {
+        if (a.q_gamma) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) rms_norm_row_bf16(qf[qb], qgm, a.q_eps);
+        }
+    }
 
     f32x4 acc[QB][4];   // O^T blocks: lane holds d = 16db + 4g + i, q = 16qb + r
     f32x4 accl[QB];     // row sums: element 0 of lanes 0..15 holds l of query 16qb + r
@@ -916,6 +986,12 @@ __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
     for (int hh = 0; hh < 2; ++hh)
         qf[hh] = __builtin_bit_cast(
             v8, buffer_load16(qrs, (uint32_t)(((q0 + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
+    // q_norm / k_norm weights for rows normalised as they are loaded (bf16)
+    f32x4 qgm[2][2], kgm[2][2];
+    if constexpr (!kF16) {
+        load_norm_gamma(a.q_gamma, g, qgm);
+        load_norm_gamma(a.k_gamma, g, kgm);
+    }
 #pragma unroll
     for (int j = 0; j < 2 * KB; ++j) {
         const int c = lane + 64 * j;
@@ -923,6 +999,13 @@ __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
     }
     asm volatile("" ::: "memory");
 
+    if constexpr (!kF16) {
+        if (a.q_gamma) rms_norm_row_bf16(qf, qgm, a.q_eps);
+        if (a.k_gamma) {
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) rms_norm_row_bf16(kf[kb], kgm, a.q_eps);
+        }
+    }
     // S^T blocks: lane holds keys 16kb + 4g + i of query q0 + r (raw scores)
     f32x4 s[KB];
 #pragma unroll
@@ -1246,6 +1329,15 @@ int validate(const sf_attn_desc* d) {
             if (reinterpret_cast<uintptr_t>(p) & 15) return SF_EINVAL;
         if ((int64_t)d->q_splits * d->B * d->Sq * d->H * 64 * 4 > 0x7fffffffLL) return SF_ENOTSUP;
     }
+    if (d->q_gamma || d->k_gamma) {   // per-head Q / K RMSNorm on load
+        if (d->in_dtype != SF_BF16) return SF_ENOTSUP;
+        if ((reinterpret_cast<uintptr_t>(d->q_gamma) & 15) || (reinterpret_cast<uintptr_t>(d->k_gamma) & 15))
+            return SF_EINVAL;
+        // K rows are normalised by the short-key kernel only (the key-split
+        // kernels stream K tiles straight into LDS)
+        const bool short_keys = d->Sk <= sfk::kShortMaxKeys && d->num_splits <= 1 && !d->q_partials;
+        if (d->k_gamma && !short_keys) return SF_ENOTSUP;
+    }
     // Per-head byte ranges are addressed with 32-bit buffer offsets.
     const int64_t es = d->in_dtype == SF_F32 ? 4 : 2;
     if ((int64_t)d->Sq * d->q_stride[2] * es > 0x7fffffffLL ||
@@ -1364,9 +1456,10 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         a.qp_bytes = (uint32_t)((int64_t)d->q_splits * d->B * d->Sq * d->H * 64 * 4);
         a.q_bias = d->q_bias;
         a.q_scale = d->q_scale;
-        a.q_gamma = d->q_gamma;
-        a.q_eps = d->q_eps;
     }
+    a.q_gamma = d->q_gamma;
+    a.q_eps = d->q_eps;
+    a.k_gamma = d->k_gamma;
     a.k = static_cast<const uint16_t*>(k);
     a.v = static_cast<const uint16_t*>(v);
     a.o = out;

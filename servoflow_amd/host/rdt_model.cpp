@@ -98,6 +98,13 @@ struct sf_rdt {
     float* x = nullptr;            // [B*S, D] fp32 residual stream
     uint16_t* n = nullptr;         // [B*S, D] bf16 norm1 / norm2 / final-norm output
     uint16_t *q = nullptr, *k = nullptr, *v = nullptr;   // [B, H, S, 64]
+    // Above 160 rows (the library-path GEMMs) the QKV projection is kept as
+    // its bf16 output [B*S, 3D] and the cross-q projection's as [B*S, D] in
+    // q; the attention reads Q / K / V from those rows and applies q_norm /
+    // k_norm as it loads them (sf_attn_desc.q_gamma / k_gamma) in place of
+    // the per-head epilogue pass.
+    bool rows_qkv = false;
+    uint16_t* qkv_rows = nullptr;
     uint16_t* a = nullptr;         // [B*S, D] bf16 attention output
     // The FFN's inputs (norm3 output, GELU hidden) in ffn_dtype: fp16 while
     // B*S rows fit the split-K regime (3 more significant bits than bf16 at
@@ -450,15 +457,41 @@ struct QPartials {
     const float* gamma = nullptr;
 };
 
+// Q (and for the self-attention K, V) read from a projection's bf16 output
+// rows instead of [B, H, S, 64]: row b*S + s, row length q_ld / kv_ld
+// elements, head h at column h*64; q_gamma / k_gamma: the per-head norms the
+// attention applies as it loads them.
+struct RowsIn {
+    int64_t q_ld = 0;
+    int64_t kv_ld = 0;   // 0: K, V in [B, H, Sc, 64]
+    const float* q_gamma = nullptr;
+    const float* k_gamma = nullptr;
+};
+
 // Sc: the rows per head of the K/V buffer (its capacity), Sk <= Sc the keys
 // read.  qp: Q from partials instead of q (which is then not read).
 int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v, int Sk,
               const int32_t* valid_len, void* out, bool exact_pv, hipStream_t s, int Sc = 0,
-              const QPartials* qp = nullptr) {
+              const QPartials* qp = nullptr, const RowsIn* rows = nullptr) {
     const sf_rdt_config& c = m->cfg;
     const int S = c.horizon + 3;
     sf_attn_desc d;
     sf_attn_desc_init_bhsd(&d, c.batch, c.heads, S, Sk, 64, SF_BF16, SF_BF16);
+    if (rows) {
+        d.q_stride[0] = (int64_t)S * rows->q_ld;
+        d.q_stride[1] = 64;
+        d.q_stride[2] = rows->q_ld;
+        if (rows->kv_ld) {
+            for (int64_t* st : {d.k_stride, d.v_stride}) {
+                st[0] = (int64_t)Sk * rows->kv_ld;
+                st[1] = 64;
+                st[2] = rows->kv_ld;
+            }
+        }
+        d.q_gamma = rows->q_gamma;
+        d.k_gamma = rows->k_gamma;
+        d.q_eps = c.eps;
+    }
     if (Sc > Sk) {
         d.k_stride[0] = d.v_stride[0] = (int64_t)c.heads * Sc * 64;
         d.k_stride[1] = d.v_stride[1] = (int64_t)Sc * 64;
@@ -616,10 +649,22 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     const int D = c.hidden, S = c.horizon + 3, M = c.batch * S;
     const int fd = m->ffn_dtype;
     // self-attention branch
-    uint16_t* qkv[3] = {m->q, m->k, m->v};
-    const int qk_g[3] = {L.q_norm, L.k_norm, -1};
-    SF_TRY(linear_heads(m, m->n, M, S, L.qkv_w, L.qkv_b, qkv, qk_g, 3, s, SF_BF16, true));
-    SF_TRY(attention(m, m->q, m->k, m->v, S, nullptr, m->a, false, s));
+    if (m->rows_qkv) {
+        // qkv = x W^T + b in bf16 (dit_block.cu:206-207); split_qkv and
+        // apply_qk_norm (:209-220) happen as the attention loads the rows
+        SF_TRY(linear(m, m->n, D, M, L.qkv_w, L.qkv_b, SF_ACT_NONE, m->qkv_rows, 3 * D, SF_BF16, false, s));
+        RowsIn r;
+        r.q_ld = r.kv_ld = 3 * D;
+        r.q_gamma = pf(m, L.q_norm);
+        r.k_gamma = pf(m, L.k_norm);
+        SF_TRY(attention(m, m->qkv_rows, m->qkv_rows + D, m->qkv_rows + 2 * D, S, nullptr, m->a, false, s, 0,
+                         nullptr, &r));
+    } else {
+        uint16_t* qkv[3] = {m->q, m->k, m->v};
+        const int qk_g[3] = {L.q_norm, L.k_norm, -1};
+        SF_TRY(linear_heads(m, m->n, M, S, L.qkv_w, L.qkv_b, qkv, qk_g, 3, s, SF_BF16, true));
+        SF_TRY(attention(m, m->q, m->k, m->v, S, nullptr, m->a, false, s));
+    }
     SF_TRY(linear_add_norm(m, m->a, SF_BF16, M, L.proj_w, L.proj_b, L.norm2, m->n, SF_BF16, s));
     // cross-attention branch: even blocks attend to language, odd to image
     // (dit_block.cu:369)
@@ -629,6 +674,16 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
         SF_TRY(cross_q_partials(m, L, M, s, &qp));
         SF_TRY(attention(m, nullptr, m->ck[i], m->cv[i], m->cond_lang_rows, m->lang_len, m->a,
                          m->exact_pv[i] != 0, s, c.lang_max, &qp));
+    } else if (m->rows_qkv) {
+        // q = x W^T + b in bf16 rows (dit_block.cu:282-284); seq_to_head and
+        // q_norm (:298-307) happen as the attention loads them
+        SF_TRY(linear(m, m->n, D, M, L.cq_w, L.cq_b, SF_ACT_NONE, m->q, D, SF_BF16, false, s));
+        RowsIn r;
+        r.q_ld = D;
+        r.q_gamma = pf(m, L.cq_norm);
+        SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? m->cond_lang_rows : c.img_len,
+                         lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,
+                         lang ? c.lang_max : c.img_len, nullptr, &r));
     } else {
         uint16_t* cq[1] = {m->q};
         const int cq_g[1] = {L.cq_norm};
@@ -870,6 +925,8 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     if (m->kv_prod_bytes) bufs.push_back({(void**)&m->kv_prod, m->kv_prod_bytes});
     m->gemm_ws_bytes = gemm_ws_for(m, false, nullptr);
     bufs.push_back({&m->gemm_ws, std::max<size_t>(m->gemm_ws_bytes, 256)});
+    m->rows_qkv = S * B > 160;
+    if (m->rows_qkv) bufs.push_back({(void**)&m->qkv_rows, (size_t)(B * S * 3 * D * 2)});
     if (S * B > 160) {   // every block's int8 weights as bf16 codes
         for (const LayerIdx& L : m->layers)
             for (int w : block_weights(L))

@@ -253,3 +253,59 @@ def test_gemm_partials_mode_contract():
     assert lib.sf_gemm_num_splits(ctypes.byref(g)) == 0
     g.workspace, g.workspace_bytes = 1024, 1 << 30
     assert lib.sf_gemm(ctypes.byref(g), None) == abi.SF_ENOTSUP          # library path
+
+
+def test_ctypes_mirrors_match_the_c_layout(tmp_path):
+    """Every ctypes mirror of an include/*.h struct has the C compiler's size
+    and field offsets (a field added to a header but not to its mirror would
+    shift every later field the Python front ends write)."""
+    import shutil
+    import subprocess
+
+    from servoflow_amd import rdt
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    mirrors = {"sf_attn_desc": abi.AttnDesc, "sf_gemm_desc": abi.GemmDesc, "sf_codes_job": abi.CodesJob,
+               "sf_absmax_job": abi.AbsmaxJob, "sf_rdt_config": rdt.RdtConfig, "sf_st_entry": rdt.StEntry}
+    lines = ['#include <stdio.h>', '#include "sf_rdt.h"', 'int main(void) {']
+    for cname, py in mirrors.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, *_ in py._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ['  return 0;', '}']
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        cname, field, val = line.split()
+        got[(cname, field)] = int(val)
+    for cname, py in mirrors.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for fname, *_ in py._fields_:
+            assert got[(cname, fname)] == getattr(py, fname).offset, (cname, fname)
+
+
+def test_qk_norm_on_load_contract():
+    """q_gamma / k_gamma without q_partials: bf16 inputs only, 16-byte
+    aligned weights, K normalised only on the short-key (Sk <= 128) path."""
+    d = abi.attn_desc_bhsd(1, 2, 67, 67)
+    d.q_gamma = 24
+    assert _fwd(d) == abi.SF_EINVAL
+    d.q_gamma, d.k_gamma = 16, 40
+    assert _fwd(d) == abi.SF_EINVAL
+    d = abi.attn_desc_bhsd(1, 2, 67, 67, in_dtype=abi.SF_F16)
+    d.q_gamma = 16
+    assert _fwd(d) == abi.SF_ENOTSUP
+    d = abi.attn_desc_bhsd(1, 2, 67, 67, in_dtype=abi.SF_F32)
+    d.k_gamma = 16
+    assert _fwd(d) == abi.SF_ENOTSUP
+    d = abi.attn_desc_bhsd(1, 2, 67, 4374)
+    d.k_gamma = 16
+    assert _fwd(d) == abi.SF_ENOTSUP
+    d = abi.attn_desc_bhsd(1, 2, 67, 67)
+    d.num_splits, d.k_gamma = 2, 16
+    assert _fwd(d) == abi.SF_ENOTSUP

@@ -565,3 +565,79 @@ def test_q_partials_bit_identical_to_heads_epilogue(w8):
                                     torch.cuda.current_stream().cuda_stream), "attention from partials")
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+def _heads_epilogue(P, S, H, gammas):
+    """sf_heads_bf16 (the per-head epilogue over a bf16 projection) on P
+    [B*S, nsec*H*64]: section j RMS-normalised per head with gammas[j] (None:
+    copied) and scattered to [B, H, S, 64]."""
+    import ctypes
+    M, N = P.shape
+    outs = [torch.empty(M // S, H, S, 64, device=P.device, dtype=torch.bfloat16) for _ in range(N // (H * 64))]
+    d = abi.GemmDesc()
+    d.M, d.N = M, N
+    d.epilogue = abi.SF_EPI_HEADS
+    d.H, d.S, d.eps = H, S, 1e-6
+    for j, o in enumerate(outs):
+        d.head_out[j] = o.data_ptr()
+        d.head_stride[j][:] = (o.stride(0), o.stride(1), o.stride(2))
+        if gammas[j] is not None:
+            d.head_gamma[j] = gammas[j].data_ptr()
+    abi.check(abi.lib().sf_heads_bf16(ctypes.byref(d), P.data_ptr(), P.stride(0),
+                                      torch.cuda.current_stream().cuda_stream), "sf_heads_bf16")
+    return outs
+
+
+def _rows_as_heads(P, S, H, section):
+    """[B, H, S, 64] view of section `section` of the projection rows P."""
+    B = P.shape[0] // S
+    return P.view(B, S, -1, H, 64)[:, :, section].permute(0, 2, 1, 3)
+
+
+@pytest.mark.parametrize("B", [3, 16, 32])
+def test_qk_norm_on_load_self_attention_bit_identical(B):
+    """The self-attention reading Q, K and V straight from the QKV
+    projection's bf16 rows, q_norm / k_norm applied as the rows are loaded
+    (q_gamma / k_gamma), gives the bits of the per-head epilogue pass
+    (sf_heads_bf16: split_qkv + apply_qk_norm) followed by the attention on
+    [B, H, S, 64] -- the two routes of the runtime above 160 rows."""
+    H, S = 32, 67
+    dev = torch.device(DEV)
+    g = torch.Generator(device=dev).manual_seed(300 + B)
+    P = (torch.randn(B * S, 3 * H * 64, device=dev, generator=g) * 3.0).to(torch.bfloat16)
+    gq = torch.rand(64, device=dev, generator=g) + 0.5
+    gk = torch.rand(64, device=dev, generator=g) + 0.5
+    q, k, v = _heads_epilogue(P, S, H, (gq, gk, None))
+    ref = attention(q, k, v, out_dtype=torch.float32)
+    got = attention(*(_rows_as_heads(P, S, H, j) for j in range(3)), out_dtype=torch.float32,
+                    q_gamma=gq, k_gamma=gk)
+    torch.cuda.synchronize()
+    assert torch.isfinite(ref).all()
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("B,Sk,lang,exact", [(16, 4374, False, False), (3, 4374, False, True),
+                                             (3, 1024, True, False), (16, 1024, True, False)])
+def test_q_norm_on_load_cross_attention_bit_identical(B, Sk, lang, exact):
+    """Cross-attention with Q read from the cross-q projection's bf16 rows
+    and q_norm applied on load equals the per-head epilogue pass + attention
+    bit for bit, on every grid the runtime uses above 160 rows: one
+    workgroup per (batch, head) (batch 16), key splits + merge (batch-3
+    image), one workgroup per 16-row query block (batch-3 language)."""
+    H, S = 32, 67
+    dev = torch.device(DEV)
+    g = torch.Generator(device=dev).manual_seed(400 + B + Sk)
+    P = (torch.randn(B * S, H * 64, device=dev, generator=g) * 3.0).to(torch.bfloat16)
+    gq = torch.rand(64, device=dev, generator=g) + 0.5
+    k = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    vl = None
+    if lang:
+        vl = torch.from_numpy(lang_valid_lengths(B, B)).to(dev)
+    (q,) = _heads_epilogue(P, S, H, (gq,))
+    ref = attention(q, k, v, out_dtype=torch.float32, valid_len=vl, exact_pv=exact)
+    got = attention(_rows_as_heads(P, S, H, 0), k, v, out_dtype=torch.float32, valid_len=vl, exact_pv=exact,
+                    q_gamma=gq)
+    torch.cuda.synchronize()
+    assert torch.isfinite(ref).all()
+    assert torch.equal(got, ref)
