@@ -375,6 +375,11 @@ constexpr int kStageBytes = 2 * kTileBytes;       // K then V
 
 __device__ __forceinline__ int ring_swz(int key) { return (key >> 1) & 7; }
 
+// Cache policy of the K/V tile loads: nt (non-temporal), since every K/V
+// byte is read once per call.  A plain streaming read of a cold 1 GiB
+// buffer on MI355X moves 7.1 TB/s with nt against 6.2 TB/s without.
+constexpr int kKvPolicy = 2;
+
 template <int V> struct StageOff { static constexpr int value = V; };
 
 // Key-padding mask bytes of keys k..k+3 (k a multiple of 4) as a 32-bit
@@ -531,12 +536,13 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                krs, (__attribute__((address_space(3))) void*)(st + (4 * w + j) * 1024), 16, koffj[j], 0, 0, 0);
+                krs, (__attribute__((address_space(3))) void*)(st + (4 * w + j) * 1024), 16, koffj[j], 0, 0,
+                kKvPolicy);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 vrs, (__attribute__((address_space(3))) void*)(st + kTileBytes + (4 * w + j) * 1024), 16,
-                voffj[j], 0, 0, 0);
+                voffj[j], 0, 0, kKvPolicy);
     };
     // Key-padding mask words of tile t, loaded one tile ahead and always
     // BEFORE the next tile's DMA is issued: vector loads complete in issue
