@@ -952,7 +952,14 @@ __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
     const int g = lane >> 4;
     const int r = lane & 15;
     const int q0 = 16 * ((int)blockIdx.x * NW + w);
-    if (q0 >= a.Sq) return;   // no barrier below: a wave past the queries just ends
+    // With K normalised on load (k_gamma), a grouped workgroup's waves share
+    // that work: wave w normalises K blocks w, w + NW, ... and the others
+    // read them from its LDS region, so every wave, even one past the
+    // queries, takes part in the two barriers of that exchange.  Otherwise
+    // there is no barrier and a wave past the queries just ends.
+    constexpr bool kShareK = NW > 1 && !kF16;
+    const bool share_k = kShareK && a.k_gamma != nullptr;
+    if (q0 >= a.Sq && !share_k) return;
     const int h = blockIdx.y;
     const int b = blockIdx.z;
 
@@ -998,20 +1005,49 @@ __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
         load_norm_gamma(a.q_gamma, g, qgm);
         load_norm_gamma(a.k_gamma, g, kgm);
     }
+    if constexpr (!kF16) {
+        if (a.q_gamma) rms_norm_row_bf16(qf, qgm, a.q_eps);
+        if (!share_k && a.k_gamma) {
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) rms_norm_row_bf16(kf[kb], kgm, a.q_eps);
+        }
+    }
+    if constexpr (kShareK) {
+        if (share_k) {
+            // normalised blocks of wave w in its V region (not yet holding
+            // V): [slot kb / NW][64 lanes][2] 16-byte fragments; blocks of
+            // keys past the valid ones stay zero rows and are not exchanged
+            u32x4* own = reinterpret_cast<u32x4*>(vls[w]);
+            static_assert(((KB + NW - 1) / NW) * 64 * 2 * 16 <= KROWS * kVPitch * 2, "fits a V region");
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                if (kb % NW == w && 16 * kb < valid) {
+                    rms_norm_row_bf16(kf[kb], kgm, a.q_eps);
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+                        own[((kb / NW) * 64 + lane) * 2 + hh] = __builtin_bit_cast(u32x4, kf[kb][hh]);
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                if (kb % NW != w && 16 * kb < valid) {
+                    const u32x4* src = reinterpret_cast<const u32x4*>(vls[kb % NW]);
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+                        kf[kb][hh] = __builtin_bit_cast(v8, src[((kb / NW) * 64 + lane) * 2 + hh]);
+                }
+            }
+            __syncthreads();   // every read done before the regions take V
+            if (q0 >= a.Sq) return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < 2 * KB; ++j) {
         const int c = lane + 64 * j;
         *reinterpret_cast<u32x4*>(vl + (c >> 3) * kVPitch + (c & 7) * 8) = vv[j];
     }
     asm volatile("" ::: "memory");
-
-    if constexpr (!kF16) {
-        if (a.q_gamma) rms_norm_row_bf16(qf, qgm, a.q_eps);
-        if (a.k_gamma) {
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) rms_norm_row_bf16(kf[kb], kgm, a.q_eps);
-        }
-    }
     // S^T blocks: lane holds keys 16kb + 4g + i of query q0 + r (raw scores)
     f32x4 s[KB];
 #pragma unroll
@@ -1503,6 +1539,9 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         // one wave per query block while B*H*blocks leaves CUs idle; five
         // per workgroup once B*H alone fills the chip (up to the bound)
         const long bh = (long)d->B * d->H;
+        // (with K normalised on load the grouped form shares that work
+        // between a head's waves: batch 16 14.8 vs 15.5 us; at B*H = 1024
+        // the one-wave form still wins, 23.1 vs 27.1 us)
         const bool grouped = bh >= sfk::kShortGroupMinHeads && bh < sfk::kShortGroupMaxHeads;
         if (grouped)
             launch_short<5>(f16, kb, dim3((qb + 4) / 5, d->H, d->B), s, a);

@@ -641,3 +641,28 @@ def test_q_norm_on_load_cross_attention_bit_identical(B, Sk, lang, exact):
     torch.cuda.synchronize()
     assert torch.isfinite(ref).all()
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("B,S,lens", [(8, 40, None), (8, 67, (20, 67, 33, 1, 0, 48, 64, 17)),
+                                      (12, 100, None)])
+def test_qk_norm_on_load_grouped_waves(B, S, lens):
+    """Grouped short-key workgroups (B*H >= 256: one wave per 16-query block)
+    share the K normalisation through LDS: wave w normalises K blocks w, w+5
+    and the others read them.  Bit-identical to the per-head epilogue pass +
+    attention with waves past the queries (S = 40: two of five), key valid
+    lengths that leave whole blocks unnormalised (0, 1, 17, ...) and two
+    K blocks per wave (S = 100: blocks 0..6)."""
+    H = 32
+    dev = torch.device(DEV)
+    g = torch.Generator(device=dev).manual_seed(500 + B + S)
+    P = (torch.randn(B * S, 3 * H * 64, device=dev, generator=g) * 2.0).to(torch.bfloat16)
+    gq = torch.rand(64, device=dev, generator=g) + 0.5
+    gk = torch.rand(64, device=dev, generator=g) + 0.5
+    vl = None if lens is None else torch.tensor(lens, dtype=torch.int32, device=dev)
+    q, k, v = _heads_epilogue(P, S, H, (gq, gk, None))
+    ref = attention(q, k, v, out_dtype=torch.float32, valid_len=vl)
+    got = attention(*(_rows_as_heads(P, S, H, j) for j in range(3)), out_dtype=torch.float32, valid_len=vl,
+                    q_gamma=gq, k_gamma=gk)
+    torch.cuda.synchronize()
+    assert torch.isfinite(ref).all()
+    assert torch.equal(got, ref)
