@@ -388,7 +388,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
         const uint32_t off = (c < NCH && k < g.K) ? (uint32_t)((row * g.lda + k) * AB) : 0x80000000u;
         av[i] = buffer_load16(ars, off);
     }
-    // every weight fragment of this wave in flight at once; rows past N read 0
+    // every weight fragment of this wave in flight at once (non-temporal
+    // cache policy: each weight byte is read once per step); rows past N read 0
     constexpr int WB = W8 ? 1 : 2;
     const int wrows = min(kSkRows, g.N - nw);
     const __amdgpu_buffer_rsrc_t wrs =
@@ -406,9 +407,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
             const uint32_t wrow_off = (uint32_t)((16 * (NB * w + nb) + r) * g.ldw * WB);
             const uint32_t off = t < nsteps ? wrow_off + (uint32_t)(k * WB) : 0x80000000u;
             if constexpr (W8)
-                wq[nb][t] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wrs, off, 0, 0));
+                wq[nb][t] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wrs, off, 0, 2));
             else
-                wv[nb][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
+                wv[nb][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2);
         }
     }
 #pragma unroll
