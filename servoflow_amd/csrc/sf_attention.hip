@@ -491,7 +491,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
         for (int j = 0; j < kQPMax; ++j) {
             const uint32_t off = j < a.q_splits && rlive ? (rowoff + j * sstride) * 4u
                                                          : 0x80000000u;   // past the buffer range: zeros
-            qpv[j] = __builtin_bit_cast(f32x4, buffer_load16(prs, off));
+            qpv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kKvPolicy));
         }
         const int nb = h * 64 + c4;
         const __amdgpu_buffer_rsrc_t brs = make_rsrc(a.q_bias, a.q_bias ? (uint32_t)(a.H * 64 * 4) : 0u);

@@ -538,8 +538,8 @@ __device__ __forceinline__ void load_quad(const EpiArgs& e, int m, int n, Quad<N
     const float* p = e.part + (int64_t)m * e.N + n;
     const int64_t stride = (int64_t)e.M * e.N;
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-        q.part[s] = *reinterpret_cast<const f32x4*>(p + min(s, e.splits - 1) * stride);
+    for (int s = 0; s < NS; ++s)   // each partial is read once: non-temporal loads
+        q.part[s] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + min(s, e.splits - 1) * stride));
     q.bias = e.bias ? *reinterpret_cast<const f32x4*>(e.bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
     q.scale = e.w_scale ? *reinterpret_cast<const f32x4*>(e.w_scale + n) : f32x4{1.f, 1.f, 1.f, 1.f};
 }
