@@ -223,6 +223,7 @@ def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
 # one-time condition K/V projection of the image tokens (M = 4374 per batch).
 GEMM_SHAPES = (
     ("proj_b1", 67, 2048, 2048, False),
+    ("proj_int8_b1", 67, 2048, 2048, True),
     ("qkv_b1", 67, 6144, 2048, False),
     ("proj_b16", 1072, 2048, 2048, False),
     ("qkv_b16", 1072, 6144, 2048, False),
@@ -583,7 +584,8 @@ def main():
             if M <= 160:   # weight streaming: the HBM rate is the bound that matters
                 extra[f"gemm_{name}_GBps"] = round(r["GBps"], 1)
                 extra[f"gemm_{name}_hbm_frac"] = round(r["hbm_frac"], 4)
-        for B, int8, key in ((16, False, "loop_b16_ms"), (32, True, "loop_int8_b32_ms")):
+        for B, int8, key in ((1, True, "loop_int8_b1_ms"), (16, False, "loop_b16_ms"),
+                             (32, True, "loop_int8_b32_ms")):
             m, enc = make_model(B, int8=int8)
             extra[key] = round(bench_loop(m, max(3, args.steps // 10), 2), 3)
             extra[key.replace("loop", "encode")] = round(enc, 3)
