@@ -320,6 +320,18 @@ int sf_heads_bf16(const sf_gemm_desc* desc, const void* P, int64_t ldp, void* st
  * timing.  Call this before capturing a graph that contains the call. */
 int sf_gemm_prepare(const sf_gemm_desc* desc);
 
+/* Whether sf_gemm_prepare times hipBLASLt's candidates (timed = 1, the
+ * default) or takes the first candidate of hipBLASLt's heuristic (0).  The
+ * timed pick can differ from one process to the next, and with it the
+ * bits of library-path products (M > 160); with 0 every process picks the
+ * same algorithm for a given hipBLASLt, GPU and shape, so those products
+ * are reproducible bit for bit, at up to ~35% more time per call.  Applies
+ * to shapes prepared after the call (a shape keeps the algorithm it was
+ * prepared with for the life of the process).  No counterpart in the
+ * reference, whose cuBLASLt calls take cuBLASLt's heuristic choice
+ * (cuda_backend.cu:414-447).  SF_EINVAL for other values. */
+int sf_gemm_set_algo_timing(int32_t timed);
+
 /* ---------------------------------------------------------------------------
  * Normalisation and dequant.
  * ------------------------------------------------------------------------- */

@@ -166,6 +166,8 @@ def lib() -> ctypes.CDLL:
     L.sf_heads_bf16.restype = ctypes.c_int
     L.sf_absmax_bf16_batched.argtypes = [ctypes.POINTER(AbsmaxJob), i32, vp]
     L.sf_absmax_bf16_batched.restype = ctypes.c_int
+    L.sf_gemm_set_algo_timing.argtypes = [i32]
+    L.sf_gemm_set_algo_timing.restype = ctypes.c_int
     L.sf_strerror.argtypes = [ctypes.c_int]
     L.sf_strerror.restype = ctypes.c_char_p
     _lib = L

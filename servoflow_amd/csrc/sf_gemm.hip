@@ -46,6 +46,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -1013,6 +1014,11 @@ hipblasStatus_t lt_matmul(hipblasLtHandle_t h, const LtShape& sh, const hipblasL
 // from sf_gemm_prepare only, never under graph capture.
 constexpr size_t kColdSetBytes = 320u << 20;
 
+// Whether sf_gemm_prepare times the candidates (1, the default) or takes
+// hipBLASLt's first heuristic candidate (0: the same algorithm in every
+// process for a given library, GPU and shape; sf_gemm_set_algo_timing).
+std::atomic<int> g_lt_timed{1};
+
 int lt_pick_fastest(hipblasLtHandle_t h, const LtShape& sh, const hipblasLtMatmulHeuristicResult_t* res, int nres,
                     int N, int K, int rows, int64_t lda, int64_t ldw) {
     void *a = nullptr, *w = nullptr, *dbuf = nullptr, *ws = nullptr, *vec = nullptr;
@@ -1135,8 +1141,8 @@ int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, const LtKind& ki
     nres = nuse;
     ok = ok && nres > 0;
     if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
-    int pick = 0;
-    if (ok && tune && nres > 1) {
+    int pick = 0;   // hipBLASLt's first heuristic candidate unless timed
+    if (ok && tune && g_lt_timed.load() && nres > 1) {
         const int best = lt_pick_fastest(*h, sh, res, nres, N, K, rows, lda, ldw);
         if (best >= 0) pick = best;
     }
@@ -1397,6 +1403,12 @@ extern "C" int sf_heads_bf16(const sf_gemm_desc* d, const void* P, int64_t ldp, 
     hipStream_t s = static_cast<hipStream_t>(stream);
     sfk::launch_reduce<1>(d, e, s);
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+}
+
+extern "C" int sf_gemm_set_algo_timing(int32_t timed) {
+    if (timed != 0 && timed != 1) return SF_EINVAL;
+    g_lt_timed.store(timed);
+    return SF_OK;
 }
 
 extern "C" int32_t sf_gemm_num_splits(const sf_gemm_desc* d) {

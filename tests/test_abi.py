@@ -309,3 +309,10 @@ def test_qk_norm_on_load_contract():
     d = abi.attn_desc_bhsd(1, 2, 67, 67)
     d.num_splits, d.k_gamma = 2, 16
     assert _fwd(d) == abi.SF_ENOTSUP
+
+
+def test_gemm_algo_timing_switch_arguments():
+    lib = abi.lib()
+    for bad in (-1, 2, 7):
+        assert lib.sf_gemm_set_algo_timing(bad) == abi.SF_EINVAL
+    assert lib.sf_gemm_set_algo_timing(1) == abi.SF_OK   # the default, restored

@@ -677,3 +677,47 @@ def test_gemm_partials_sum_to_the_fp32_product(w8):
     assert abi.lib().sf_gemm_num_splits(ctypes.byref(d2)) == 0
     d2.workspace, d2.workspace_bytes = buf.data_ptr(), buf.numel() * 4
     assert abi.lib().sf_gemm(ctypes.byref(d2), None) == abi.SF_ENOTSUP
+
+
+_HEURISTIC_PICK_SCRIPT = r"""
+import hashlib, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from servoflow_amd import abi, kernels
+assert abi.lib().sf_gemm_set_algo_timing(0) == abi.SF_OK
+dev = torch.device("cuda:0")
+g = torch.Generator(device=dev).manual_seed(11)
+a = torch.randn(536, 2048, device=dev, generator=g).to(torch.bfloat16)
+w = (torch.randn(1536, 2048, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+b = torch.randn(1536, device=dev, generator=g) * 0.02
+import ctypes
+d = kernels._desc(a, w, b, abi.SF_ACT_NONE, None)
+out = torch.empty(536, 1536, device=dev, dtype=torch.float32)
+d.epilogue, d.C, d.ldc, d.c_dtype = abi.SF_EPI_PLAIN, out.data_ptr(), 1536, abi.SF_F32
+ws = torch.empty(max(abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d)), 16), dtype=torch.uint8, device=dev)
+d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
+abi.check(abi.lib().sf_gemm_prepare(ctypes.byref(d)), "prepare")
+abi.check(abi.lib().sf_gemm(ctypes.byref(d), torch.cuda.current_stream().cuda_stream), "gemm")
+torch.cuda.synchronize()
+ref = a.float() @ w.float().t() + b
+err = float((out - ref).abs().max())
+assert err < 1e-3, err
+print(hashlib.sha256(out.cpu().numpy().tobytes()).hexdigest())
+"""
+
+
+def test_gemm_heuristic_pick_is_reproducible_across_processes():
+    """With sf_gemm_set_algo_timing(0) a library-path product (536 rows)
+    takes hipBLASLt's first heuristic candidate, so two processes produce
+    the same bits; each result also matches the fp32 product."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    digests = []
+    for _ in range(2):
+        r = subprocess.run([sys.executable, "-c", _HEURISTIC_PICK_SCRIPT, root], capture_output=True, text=True,
+                           timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        digests.append(r.stdout.strip().splitlines()[-1])
+    assert digests[0] == digests[1]
