@@ -120,6 +120,10 @@ struct sf_rdt {
     uint16_t* sincos = nullptr;    // [num_train_timesteps, freq_dim] bf16
     uint16_t* emb_h = nullptr;     // [1, D]
     float* t_emb = nullptr;        // [D]
+    // the timestep tokens of the sampler's schedule, [num_steps][D],
+    // embedded with the condition (they depend on the weights and the step
+    // index only), read by the sampled loop instead of re-embedding
+    float* t_emb_steps = nullptr;
     float* f_emb = nullptr;        // [D]
     uint16_t* state_tok = nullptr; // [B, D]
     float* vel_rows = nullptr;     // [B*S, A]
@@ -708,8 +712,17 @@ int entry_norm(sf_rdt* m, int first, hipStream_t s) {
     return sf_rmsnorm(m->x, SF_F32, D, pf(m, g), m->n, SF_BF16, D, M, D, c.eps, s);
 }
 
+// The timestep index of t (rdt1b.cpp:312-313): round(t * (T_train - 1)).
+int timestep_index(const sf_rdt_config& c, float t) {
+    const float tt = t * (float)(c.num_train_timesteps - 1);
+    return (int)std::lround(tt);
+}
+
 // RDT1BModel::denoise_step up to the final layer: velocity rows [B*S, A].
-int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s, bool widen = true) {
+// t_emb_given: t's timestep token already embedded (the sampler's schedule),
+// else it is embedded here.
+int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s, bool widen = true,
+                 const float* t_emb_given = nullptr) {
     const sf_rdt_config& c = m->cfg;
     const int D = c.hidden, T = c.horizon, A = c.action_dim, S = T + 3;
     const int BT = c.batch * T, M = c.batch * S;
@@ -721,10 +734,12 @@ int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s, bool widen
                   s));
     SF_TRY(linear(m, m->sa1, D, BT, m->sa[4], m->sa[5], SF_ACT_NONE, m->act_out, D, SF_F32, false, s));
     // timestep token (rdt1b.cpp:312-315); the frequency token is cached
-    const float tt = t * (float)(c.num_train_timesteps - 1);
-    const int t_int = (int)std::lround(tt);
-    SF_TRY(timestep_embed(m, m->te, t_int, m->t_emb, s));
-    SF_TRY(sf_assemble_tokens(m->x, m->t_emb, m->f_emb, m->state_tok, m->act_out, pf(m, m->xpos),
+    const float* t_emb = t_emb_given;
+    if (!t_emb) {
+        SF_TRY(timestep_embed(m, m->te, timestep_index(c, t), m->t_emb, s));
+        t_emb = m->t_emb;
+    }
+    SF_TRY(sf_assemble_tokens(m->x, t_emb, m->f_emb, m->state_tok, m->act_out, pf(m, m->xpos),
                               c.batch, T, D, s));
     SF_TRY(entry_norm(m, 0, s));
     if (widen) SF_TRY(widen_codes(m, 0, c.layers, s));
@@ -750,7 +765,7 @@ int sample_body(sf_rdt* m, hipStream_t s) {
     const std::vector<float> ts = schedule(c.num_steps);
     SF_TRY(widen_codes(m, 0, c.layers, s));   // once for every step of the loop
     for (int step = 0; step < c.num_steps; ++step) {
-        SF_TRY(step_forward(m, m->x_state, ts[step], s, false));
+        SF_TRY(step_forward(m, m->x_state, ts[step], s, false, m->t_emb_steps + (size_t)step * c.hidden));
         const float dt = ts[step + 1] - ts[step];
         SF_TRY(sf_euler_update(m->x_state, m->vel_rows, c.batch, c.horizon, c.action_dim,
                                c.horizon + 3, dt, s));
@@ -904,6 +919,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
         {(void**)&m->emb_h, (size_t)(D * 2)},
         {(void**)&m->t_emb, (size_t)(D * 4)},
         {(void**)&m->f_emb, (size_t)(D * 4)},
+        {(void**)&m->t_emb_steps, (size_t)c.num_steps * D * 4},
         {(void**)&m->state_tok, (size_t)(B * D * 2)},
         {(void**)&m->vel_rows, (size_t)(B * S * A * 4)},
         {(void**)&m->x_state, (size_t)(B * T * A * 4)},
@@ -1181,7 +1197,13 @@ extern "C" int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t
         ++m->cond_gen;
     }
     // the control-frequency token is constant: embed it once (rdt1b.cpp:316)
-    return timestep_embed(m, m->fe, c.ctrl_freq, m->f_emb, s);
+    SF_TRY(timestep_embed(m, m->fe, c.ctrl_freq, m->f_emb, s));
+    // and so are the sampler schedule's timestep tokens (rdt1b.cpp:312-315 at
+    // each t of Schedule::linspace, flow_matching.cpp:10-17)
+    const std::vector<float> ts = schedule(c.num_steps);
+    for (int step = 0; step < c.num_steps; ++step)
+        SF_TRY(timestep_embed(m, m->te, timestep_index(c, ts[step]), m->t_emb_steps + (size_t)step * D, s));
+    return SF_OK;
 }
 
 extern "C" int sf_rdt_set_lang_rows(sf_rdt* m, int32_t rows) {
