@@ -133,7 +133,10 @@ int32_t sf_rdt_find_param(const sf_rdt* m, const char* name);
 /* Condition for the next inferences.  lang_c bf16 [B, lang_max, D],
  * lang_len int32 [B] (device; keys >= lang_len[b] are masked), img_c bf16
  * [B, img_len, D], state_tok bf16 [B, D]: the adaptor outputs.  Adds the
- * position embeddings and projects every block's cross-attention K/V once. */
+ * position embeddings and projects every block's cross-attention K/V once,
+ * and embeds the control-frequency token and the timestep tokens of the
+ * sampler's schedule (they depend on the weights only), so set or load the
+ * weights before the condition. */
 int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t* lang_len,
                          const void* img_c, const void* state_tok, void* stream);
 /* Raw tokens: lang bf16 [B, lang_max, 4096], img bf16 [B, img_len, 1152],
