@@ -930,36 +930,41 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
 // key order matches the P^T slots the S^T accumulator provides.
 // ---------------------------------------------------------------------------
 constexpr int kShortMaxKeys = 128;
-// B*H range in which a workgroup takes all of a head's query blocks, one
-// wave each.  Same-box A/B on 1x..x32x67x67: 6.8 vs 7.9 us at B*H = 256,
-// 11.3 vs 11.5 at 512, but 20.9 vs 19.4 at 1024 (one-wave workgroups keep
-// more waves in flight per CU there), so 256 <= B*H < 1024.
+// B*H from which a workgroup takes all of a head's query blocks, one wave
+// each, sharing one LDS copy of the head's K and V (27 KB at 67 keys).
+// Same-box A/B, self-attention over the QKV rows with q/k norm on load,
+// against one-wave workgroups: B=8 7.2 vs 8.6 us (per-wave V copies),
+// B=16 12.5 vs 15.2, B=32 22.5 vs 23.3.  (With a V copy per wave, 77 KB per
+// workgroup, the grouped form had lost at B*H = 1024: 20.9 vs 19.4 us.)
 constexpr long kShortGroupMinHeads = 256;
-constexpr long kShortGroupMaxHeads = 1024;
 constexpr int kVPitch = 80;   // LDS row pitch of V (bf16): 160 B keeps the four rows of a read apart
 
 // NW query blocks per workgroup, one wave each: 1 spreads a small batch's
 // few heads over the most CUs; 5 (large batches) runs a head's 67 queries on
-// one CU, so its K and V come from L2 once and the other waves hit in L1.
+// one CU, whose waves load K and V once between them.
 template <int KB, bool kF16, int NW>   // 16-key blocks covering Sk (even, <= 8); fp16 (else bf16) Q/K/V
 __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
     using v8 = typename In16<kF16>::v8;
     constexpr int KROWS = 16 * KB;
-    __shared__ __attribute__((aligned(16))) uint16_t vls[NW][KROWS * kVPitch];
+    // NW == 1: the wave loads all of K and V and stages V in LDS.  NW > 1:
+    // the workgroup's waves share one V region and one region of K operand
+    // fragments ([KB][64 lanes][2]): wave w loads every NW-th V chunk and the
+    // K blocks kb = w, w + NW, ... (normalising them with k_gamma), all
+    // waves meet at one barrier and then read every block -- one copy of K
+    // and V per head, so more heads share a CU.  Every wave of a grouped
+    // workgroup, even one past the queries, loads its share and meets the
+    // barrier; a one-wave workgroup past the queries just ends.
+    __shared__ __attribute__((aligned(16))) uint16_t vls[KROWS * kVPitch];
+    __shared__ __attribute__((aligned(16))) u32x4 kls[NW > 1 ? KB * 64 * 2 : 1];
     const int lane = threadIdx.x & 63;
     const int w = NW > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) : 0;
-    uint16_t* vl = vls[w];
+    uint16_t* vl = vls;
     const int g = lane >> 4;
     const int r = lane & 15;
     const int q0 = 16 * ((int)blockIdx.x * NW + w);
-    // With K normalised on load (k_gamma), a grouped workgroup's waves share
-    // that work: wave w normalises K blocks w, w + NW, ... and the others
-    // read them from its LDS region, so every wave, even one past the
-    // queries, takes part in the two barriers of that exchange.  Otherwise
-    // there is no barrier and a wave past the queries just ends.
-    constexpr bool kShareK = NW > 1 && !kF16;
-    const bool share_k = kShareK && a.k_gamma != nullptr;
-    if (q0 >= a.Sq && !share_k) return;
+    if constexpr (NW == 1) {
+        if (q0 >= a.Sq) return;
+    }
     const int h = blockIdx.y;
     const int b = blockIdx.z;
 
@@ -979,20 +984,24 @@ __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
         make_rsrc(a.kv_mask ? static_cast<const void*>(a.kv_mask + b * a.kv_mask_stride) : static_cast<const void*>(a.q),
                   a.kv_mask ? (uint32_t)((a.Sk + 3) & ~3) : 0u);
 
-    // every load of the wave up front
+    // every load of the wave (its share, grouped) up front
     u32x4 vv[2 * KB];
 #pragma unroll
     for (int j = 0; j < 2 * KB; ++j) {
-        const int c = lane + 64 * j;          // 16-byte chunk: key c/8, dims 8(c%8)..
-        vv[j] = buffer_load16(vrs, (uint32_t)(((c >> 3) * a.v_ss + (c & 7) * 8) * 2));
+        if (NW == 1 || j % NW == w) {
+            const int c = lane + 64 * j;          // 16-byte chunk: key c/8, dims 8(c%8)..
+            vv[j] = buffer_load16(vrs, (uint32_t)(((c >> 3) * a.v_ss + (c & 7) * 8) * 2));
+        }
     }
     v8 kf[KB][2];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
+        if (NW == 1 || kb % NW == w) {
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-            kf[kb][hh] = __builtin_bit_cast(
-                v8, buffer_load16(krs, (uint32_t)(((16 * kb + r) * a.k_ss + 32 * hh + 8 * g) * 2)));
+            for (int hh = 0; hh < 2; ++hh)
+                kf[kb][hh] = __builtin_bit_cast(
+                    v8, buffer_load16(krs, (uint32_t)(((16 * kb + r) * a.k_ss + 32 * hh + 8 * g) * 2)));
+        }
     }
     v8 qf[2];
 #pragma unroll
@@ -1004,48 +1013,37 @@ __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
     if constexpr (!kF16) {
         load_norm_gamma(a.q_gamma, g, qgm);
         load_norm_gamma(a.k_gamma, g, kgm);
-    }
-    if constexpr (!kF16) {
         if (a.q_gamma) rms_norm_row_bf16(qf, qgm, a.q_eps);
-        if (!share_k && a.k_gamma) {
+        if (a.k_gamma) {
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) rms_norm_row_bf16(kf[kb], kgm, a.q_eps);
-        }
-    }
-    if constexpr (kShareK) {
-        if (share_k) {
-            // normalised blocks of wave w in its V region (not yet holding
-            // V): [slot kb / NW][64 lanes][2] 16-byte fragments; blocks of
-            // keys past the valid ones stay zero rows and are not exchanged
-            u32x4* own = reinterpret_cast<u32x4*>(vls[w]);
-            static_assert(((KB + NW - 1) / NW) * 64 * 2 * 16 <= KROWS * kVPitch * 2, "fits a V region");
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                if (kb % NW == w && 16 * kb < valid) {
-                    rms_norm_row_bf16(kf[kb], kgm, a.q_eps);
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh)
-                        own[((kb / NW) * 64 + lane) * 2 + hh] = __builtin_bit_cast(u32x4, kf[kb][hh]);
-                }
-            }
-            __syncthreads();
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                if (kb % NW != w && 16 * kb < valid) {
-                    const u32x4* src = reinterpret_cast<const u32x4*>(vls[kb % NW]);
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh)
-                        kf[kb][hh] = __builtin_bit_cast(v8, src[((kb / NW) * 64 + lane) * 2 + hh]);
-                }
-            }
-            __syncthreads();   // every read done before the regions take V
-            if (q0 >= a.Sq) return;
+            for (int kb = 0; kb < KB; ++kb)   // the wave's blocks; those past the valid keys stay zero
+                if ((NW == 1 || kb % NW == w) && 16 * kb < valid) rms_norm_row_bf16(kf[kb], kgm, a.q_eps);
         }
     }
 #pragma unroll
     for (int j = 0; j < 2 * KB; ++j) {
-        const int c = lane + 64 * j;
-        *reinterpret_cast<u32x4*>(vl + (c >> 3) * kVPitch + (c & 7) * 8) = vv[j];
+        if (NW == 1 || j % NW == w) {
+            const int c = lane + 64 * j;
+            *reinterpret_cast<u32x4*>(vl + (c >> 3) * kVPitch + (c & 7) * 8) = vv[j];
+        }
+    }
+    if constexpr (NW > 1) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            if (kb % NW == w) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) kls[(kb * 64 + lane) * 2 + hh] = __builtin_bit_cast(u32x4, kf[kb][hh]);
+            }
+        }
+        __syncthreads();
+        if (q0 >= a.Sq) return;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            if (kb % NW != w) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) kf[kb][hh] = __builtin_bit_cast(v8, kls[(kb * 64 + lane) * 2 + hh]);
+            }
+        }
     }
     asm volatile("" ::: "memory");
     // S^T blocks: lane holds keys 16kb + 4g + i of query q0 + r (raw scores)
@@ -1539,10 +1537,7 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         // one wave per query block while B*H*blocks leaves CUs idle; five
         // per workgroup once B*H alone fills the chip (up to the bound)
         const long bh = (long)d->B * d->H;
-        // (with K normalised on load the grouped form shares that work
-        // between a head's waves: batch 16 14.8 vs 15.5 us; at B*H = 1024
-        // the one-wave form still wins, 23.1 vs 27.1 us)
-        const bool grouped = bh >= sfk::kShortGroupMinHeads && bh < sfk::kShortGroupMaxHeads;
+        const bool grouped = bh >= sfk::kShortGroupMinHeads;
         if (grouped)
             launch_short<5>(f16, kb, dim3((qb + 4) / 5, d->H, d->B), s, a);
         else
