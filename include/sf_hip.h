@@ -140,9 +140,11 @@ typedef struct sf_attn_desc {
      * row[d] * (1 / sqrt(sum_d row[d]^2 / 64 + q_eps)) * gamma[d], rounded to
      * bf16 -- bit for bit what sf_gemm's per-head epilogue over a bf16
      * product (SF_EPI_HEADS above 160 rows) stores.  With q/k/v and their
-     * strides pointing into a projection's bf16 output (row b*S + s, column
-     * section*H*64 + h*64 + d) this takes the place of split_qkv / split_kv +
-     * apply_qk_norm.  bf16 inputs only (SF_ENOTSUP otherwise). */
+     * strides pointing into a projection's 16-bit output (row b*S + s,
+     * column section*H*64 + h*64 + d) this takes the place of split_qkv /
+     * split_kv + apply_qk_norm.  bf16 or fp16 inputs (the normalised rows
+     * are rounded to the input type; SF_ENOTSUP for fp32); k_gamma only on
+     * the short-key path (Sk <= 128, no forced split). */
     const float* q_partials;
     int32_t q_splits;
     const float* q_bias;
@@ -150,6 +152,13 @@ typedef struct sf_attn_desc {
     const float* q_gamma;
     float q_eps;
     const float* k_gamma;
+    /* q_f16 != 0 (in_dtype SF_BF16, no q_partials): Q is given in fp16
+     * while K and V are bf16 -- a projection's fp16 output rows against the
+     * bf16 cross-attention K/V cache.  Each Q row is normalised with q_gamma
+     * (when set) in fp32 and rounded to bf16 as it is loaded, so the
+     * contraction is the bf16 one.  SF_ENOTSUP with another in_dtype or
+     * with q_partials. */
+    int32_t q_f16;
 } sf_attn_desc;
 
 /* Fills a descriptor for contiguous [B,H,S,D] tensors (the layout
@@ -282,7 +291,15 @@ typedef struct sf_gemm_desc {
     int32_t round_product;   /* M > 160, SF_EPI_HEADS / SF_EPI_ADD_NORM: bf16 product (see above) */
     const void* w_codes16;   /* int8 weights, optional: their codes as bf16 [N][K] (16-byte aligned,
                                 sf_int8_codes_to_bf16); the library path reads this copy instead of
-                                widening the codes itself on every call */
+                                widening the codes itself on every call.  With w16_f16: an fp16
+                                copy [N][K] of the weights (int8 codes or bf16 values,
+                                sf_weights_to_f16) */
+    int32_t w16_f16;         /* nonzero with a_dtype SF_F16: w_codes16 is the fp16 copy, and the
+                                library path (M > 160) multiplies the fp16 activations by it in
+                                fp16 -- no rounding of the activations to bf16 -- and its 16-bit
+                                products (round_product, and a plain C written by hipBLASLt, which
+                                must then be SF_F16) are fp16.  Ignored on the other paths, which
+                                read W itself (SF_EINVAL when w_codes16 is NULL on this path) */
 } sf_gemm_desc;
 
 /* Bytes of workspace sf_gemm needs for this call (0: it always runs
@@ -376,6 +393,21 @@ typedef struct sf_codes_job {
     int32_t N, K;
 } sf_codes_job;
 int sf_int8_codes_to_bf16(const sf_codes_job* jobs, int32_t count, void* stream);
+
+/* fp16 copies of projection weights for the library path's fp16 products
+ * (sf_gemm_desc.w16_f16): job j converts w [N][ldw] -- int8 codes (exact,
+ * no scale: the row scale stays with the GEMM) or bf16 values (rounded to
+ * the nearest fp16: exact for 2^-14 <= |w| < 65520, within 2^-25 below,
+ * +-inf at or above 65520) -- into out [N][K], up to SF_CODES_MAX_JOBS
+ * matrices per launch.  K a multiple of 16, rows 16-byte aligned. */
+typedef struct sf_w16_job {
+    const void* w;
+    int32_t w_dtype;   /* SF_I8 or SF_BF16 */
+    int64_t ldw;       /* elements */
+    void* out;
+    int32_t N, K;
+} sf_w16_job;
+int sf_weights_to_f16(const sf_w16_job* jobs, int32_t count, void* stream);
 
 /* Static text for a status code. */
 const char* sf_strerror(int status);

@@ -26,13 +26,15 @@ Points: "cond" condition tokens + position embedding, "kv" cross K/V cache,
 "n1" norm1 / norm_final outputs, "qkv" per-head q/k/v (self and cross),
 "a" attention outputs, "n2" / "n3" norm2 / norm3 outputs, "h" FFN and final
 hidden, "emb" timestep-embedding inputs, "adapt" adaptor inputs / hidden,
-"state" the state token, "gemm" the block projections' outputs before the
-per-head norm or the residual add (qkv, cross q, attention / cross proj,
-fc2; the bf16 outputs of the reference's cuBLASLt epilogues,
-cuda_backend.cu:414-447), which the MI355X runtime stores in bf16 above 160
-rows (storage_points(gemm16=True)), "kvgemm" the cross K/V projection's
-output before split_kv / k_norm (dit_block.cu:291-308), rounded when the
-projection has more than 160 rows (the runtime's library path).
+"state" the state token, "gemm" the block projections' outputs before
+the residual add (attention / cross proj, fc2; the bf16 outputs of the
+reference's cuBLASLt epilogues, cuda_backend.cu:414-447), "hgemm" the
+per-head projections' outputs before the per-head norm (qkv, cross q; the
+"gemm" setting when a dict or set of points leaves it out), "cq" the
+cross-attention's per-head q (the "qkv" setting when left out), "kvgemm"
+the cross K/V projection's output before split_kv / k_norm
+(dit_block.cu:291-308), rounded when the projection has more than 160 rows
+(the runtime's library path).
 """
 from __future__ import annotations
 
@@ -64,29 +66,51 @@ class RdtConfig:
         return self.horizon + 3
 
 
-ALL_POINTS = frozenset({"cond", "kv", "kvgemm", "n1", "qkv", "a", "n2", "n3", "h", "emb", "adapt", "state"})
+ALL_POINTS = frozenset({"cond", "kv", "kvgemm", "n1", "qkv", "cq", "a", "n2", "n3", "h", "emb", "adapt",
+                        "state"})
 
 
-def storage_points(ffn16, gemm16=False):
+def storage_points(ffn16, gemm16=False, act16=False):
     """How the MI355X runtime stores each point: bf16 everywhere, except
-    (ffn16: batch * 67 <= 160 rows) the FFN inputs n3 and h in fp16; the
-    block projections' outputs ("gemm") in bf16 only with gemm16 (batch *
-    67 > 160 rows), fp32 otherwise."""
+    ffn16: the FFN inputs n3 and h in fp16;
+    gemm16: the block projections' products ("gemm", "hgemm") in bf16
+            (fp32 otherwise);
+    act16 (the runtime above 160 rows, with ffn16): every projection input
+            in fp16 (norm outputs "n1" / "n2", attention outputs "a"), the
+            products in fp16 ("gemm", "hgemm"), the self-attention's per-head
+            q / k / v in fp16 ("qkv"); the cross-attention's q ("cq") stays
+            bf16 (its K / V cache is bf16)."""
     pts = {p: "bf16" for p in ALL_POINTS}
     if ffn16:
         pts["n3"] = pts["h"] = "f16"
     if gemm16:
-        pts["gemm"] = "bf16"
+        pts["gemm"] = pts["hgemm"] = "bf16"
+    if act16:
+        for p in ("n1", "n2", "a", "qkv", "gemm", "hgemm"):
+            pts[p] = "f16"
     return pts
+
+
+def runtime_points(rows):
+    """The MI355X runtime's storage at `rows` = batch * 67 projection rows:
+    the split-K regime (<= 160) keeps bf16 inputs with fp16 FFN inputs and
+    fp32 products; the library regime (> 160) keeps fp16 inputs and fp16
+    products (storage_points)."""
+    return storage_points(True, act16=rows > 160)
 
 
 def _f16_round(x):
     return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
 
 
+_FALLBACK = {"hgemm": "gemm", "cq": "qkv"}
+
+
 def _r(x, rb, point):
     if rb is True:
         return O.bf16_round(x)
+    if isinstance(rb, (dict, set, frozenset)) and point not in rb and point in _FALLBACK:
+        point = _FALLBACK[point]
     if isinstance(rb, dict):
         mode = rb.get(point)
         if mode == "bf16":
@@ -124,7 +148,7 @@ def rdt_block(p, i, x, ck, cv, cond_len, cfg, rb=True):
     pre = f"blocks.{i}."
     # self-attention branch (dit_block.cu:198-238)
     n1 = _r(O.rms_norm(x, p[pre + "norm1.weight"], cfg.eps), rb, "n1")
-    qkv = _r(O.linear(n1, p[pre + "attn.qkv.weight"], p[pre + "attn.qkv.bias"]), rb, "gemm")
+    qkv = _r(O.linear(n1, p[pre + "attn.qkv.weight"], p[pre + "attn.qkv.bias"]), rb, "hgemm")
     Q, K, V = O.split_qkv(qkv.reshape(B, S, 3 * D), H, 64)
     Q = _r(O.rms_norm(Q, p[pre + "attn.q_norm.weight"], cfg.eps), rb, "qkv")
     K = _r(O.rms_norm(K, p[pre + "attn.k_norm.weight"], cfg.eps), rb, "qkv")
@@ -133,8 +157,8 @@ def rdt_block(p, i, x, ck, cv, cond_len, cfg, rb=True):
     x = x + _r(O.linear(a, p[pre + "attn.proj.weight"], p[pre + "attn.proj.bias"]), rb, "gemm")
     # cross-attention branch (dit_block.cu:274-326), norm2 from fused_add_rms_norm
     n2 = _r(O.rms_norm(x, p[pre + "norm2.weight"], cfg.eps), rb, "n2")
-    cq = _r(O.linear(n2, p[pre + "cross_attn.q.weight"], p[pre + "cross_attn.q.bias"]), rb, "gemm")
-    cq = _r(O.rms_norm(heads_of(cq.reshape(B, S, D), H), p[pre + "cross_attn.q_norm.weight"], cfg.eps), rb, "qkv")
+    cq = _r(O.linear(n2, p[pre + "cross_attn.q.weight"], p[pre + "cross_attn.q.bias"]), rb, "hgemm")
+    cq = _r(O.rms_norm(heads_of(cq.reshape(B, S, D), H), p[pre + "cross_attn.q_norm.weight"], cfg.eps), rb, "cq")
     ca = _r(O.head_to_seq(O.attention_f32(cq, ck, cv, valid_len=cond_len)), rb, "a")
     x = x + _r(O.linear(ca, p[pre + "cross_attn.proj.weight"], p[pre + "cross_attn.proj.bias"]), rb, "gemm")
     # FFN branch (Mlp::forward, dit_block.cu:143-163: fc1 + GELU, fc2)

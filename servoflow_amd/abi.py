@@ -57,6 +57,7 @@ class AttnDesc(ctypes.Structure):
         ("q_gamma", ctypes.c_void_p),
         ("q_eps", ctypes.c_float),
         ("k_gamma", ctypes.c_void_p),
+        ("q_f16", ctypes.c_int32),
     ]
 
 
@@ -91,6 +92,7 @@ class GemmDesc(ctypes.Structure):
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
         ("round_product", ctypes.c_int32),
         ("w_codes16", ctypes.c_void_p),
+        ("w16_f16", ctypes.c_int32),
     ]
 
 
@@ -102,6 +104,13 @@ class CodesJob(ctypes.Structure):
 
 
 SF_CODES_MAX_JOBS = 8
+
+
+class W16Job(ctypes.Structure):
+    """Mirror of `sf_w16_job`."""
+
+    _fields_ = [("w", ctypes.c_void_p), ("w_dtype", ctypes.c_int32), ("ldw", ctypes.c_int64),
+                ("out", ctypes.c_void_p), ("N", ctypes.c_int32), ("K", ctypes.c_int32)]
 
 
 class AbsmaxJob(ctypes.Structure):
@@ -160,6 +169,8 @@ def lib() -> ctypes.CDLL:
     L.sf_dequant_int8.restype = ctypes.c_int
     L.sf_int8_codes_to_bf16.argtypes = [ctypes.POINTER(CodesJob), i32, vp]
     L.sf_int8_codes_to_bf16.restype = ctypes.c_int
+    L.sf_weights_to_f16.argtypes = [ctypes.POINTER(W16Job), i32, vp]
+    L.sf_weights_to_f16.restype = ctypes.c_int
     L.sf_gemm_num_splits.argtypes = [ctypes.POINTER(GemmDesc)]
     L.sf_gemm_num_splits.restype = ctypes.c_int32
     L.sf_heads_bf16.argtypes = [ctypes.POINTER(GemmDesc), vp, i64, vp]

@@ -34,6 +34,12 @@ def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_spli
     d.B, d.H, d.Sq, d.Sk, d.D = B, H, Sq, Sk, D
     d.scale = float(scale)
     d.in_dtype = _DT[q.dtype]
+    if q.dtype == torch.float16 and k.dtype == torch.bfloat16:   # fp16 Q rows against bf16 K / V
+        d.in_dtype = abi.SF_BF16
+        d.q_f16 = 1
+    elif k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"dtypes q {q.dtype} k {k.dtype} v {v.dtype}: K and V must match Q "
+                         "(or Q fp16 with bf16 K and V)")
     d.out_dtype = _DT[out.dtype]
     d.is_causal = 1 if is_causal else 0
     d.num_splits = int(num_splits)
@@ -74,8 +80,10 @@ def attention(q, k, v, out=None, scale=0.0, is_causal=False, valid_len=None, num
     2^-25 below; a larger element makes its output column inf/NaN; see
     sf_attn_desc).
     q_gamma / k_gamma: optional float32 [D] weights of a per-head RMSNorm
-    (epsilon qk_eps) applied to each Q / K row as it is loaded (bf16 inputs;
-    K only for key sets of at most 128)."""
+    (epsilon qk_eps) applied to each Q / K row as it is loaded (bf16 or fp16
+    inputs; K only for key sets of at most 128).  An fp16 q with bf16 k and
+    v runs the bf16 contraction on Q rounded to bf16 after its norm
+    (sf_attn_desc.q_f16)."""
     if out is None:
         od = out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=od, device=q.device)

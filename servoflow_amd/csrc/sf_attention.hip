@@ -78,6 +78,7 @@ struct AttnArgs {
     const float* q_gamma;   // per-head RMSNorm weight of Q (with or without partials)
     float q_eps;
     const float* k_gamma;   // per-head RMSNorm weight of K (the short-key kernel)
+    int q_f16;              // bf16 instances: Q rows given in fp16, rounded to bf16 (after q_gamma) on load
 };
 
 enum OutKind { kOutBF16 = 0, kOutF32 = 1, kOutF16 = 2 };
@@ -227,21 +228,32 @@ __device__ __forceinline__ float sum_xor32(float x) {
 // product (heads16_kernel): each lane's eight squares in dim order, then
 // the row's eight partial sums as ((s0 + s1) + (s2 + s3)) + ((s4 + s5) +
 // (s6 + s7)), so the result is bit-identical to that epilogue's.
-__device__ __forceinline__ void rms_norm_row_bf16(bf16x8 (&f)[2], const f32x4 (&gm)[2][2], float eps) {
+//
+// norm_row16 is the general form: the row's 16-bit elements are read as
+// bf16 or fp16 (IF16), normalised when `norm` (else only converted) and
+// rounded to bf16 or fp16 (OF16).  fp16 rows are the projections' fp16
+// outputs at large batch; the fp16 result feeds the fp16 MFMAs, the bf16
+// one the bf16 MFMAs (a Q row against a bf16 K/V cache).
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <bool IF16, bool OF16>
+__device__ __forceinline__ void norm_row16(u32x4 (&f)[2], const f32x4 (&gm)[2][2], bool norm, float eps) {
     float v[2][8];
     float part[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-        const u32x4 w = __builtin_bit_cast(u32x4, f[hh]);
+        const u32x4 w = f[hh];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            v[hh][2 * e] = bf16_bits_to_f32(w[e] & 0xffffu);
-            v[hh][2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+            v[hh][2 * e] = IF16 ? half_bits_to_f32(w[e] & 0xffffu) : bf16_bits_to_f32(w[e] & 0xffffu);
+            v[hh][2 * e + 1] = IF16 ? half_bits_to_f32(w[e] >> 16) : bf16_bits_to_f32(w[e] >> 16);
         }
         float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss += v[hh][j] * v[hh][j];
-        part[hh] = sum_xor32(sum_xor16(ss));
+        part[hh] = norm ? sum_xor32(sum_xor16(ss)) : 0.f;
     }
     const float inv_rms = 1.f / sqrtf((part[0] + part[1]) / 64.f + eps);
 #pragma unroll
@@ -250,11 +262,43 @@ __device__ __forceinline__ void rms_norm_row_bf16(bf16x8 (&f)[2], const f32x4 (&
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const f32x4 g4 = gm[hh][e >> 1];
-            w[e] = pack_bf16x2(v[hh][2 * e] * inv_rms * g4[(2 * e) & 3],
-                               v[hh][2 * e + 1] * inv_rms * g4[(2 * e + 1) & 3]);
+            const float x0 = norm ? v[hh][2 * e] * inv_rms * g4[(2 * e) & 3] : v[hh][2 * e];
+            const float x1 = norm ? v[hh][2 * e + 1] * inv_rms * g4[(2 * e + 1) & 3] : v[hh][2 * e + 1];
+            w[e] = OF16 ? pack_f16x2_rn(x0, x1) : pack_bf16x2(x0, x1);
         }
-        f[hh] = u32x4_as_bf16x8(w);
+        f[hh] = w;
     }
+}
+
+__device__ __forceinline__ void rms_norm_row_bf16(bf16x8 (&f)[2], const f32x4 (&gm)[2][2], float eps) {
+    u32x4 u[2] = {__builtin_bit_cast(u32x4, f[0]), __builtin_bit_cast(u32x4, f[1])};
+    norm_row16<false, false>(u, gm, true, eps);
+    f[0] = u32x4_as_bf16x8(u[0]);
+    f[1] = u32x4_as_bf16x8(u[1]);
+}
+
+// The same on an fp16 operand row (normalised in fp32, rounded to fp16).
+__device__ __forceinline__ void rms_norm_row_f16(f16x8 (&f)[2], const f32x4 (&gm)[2][2], float eps) {
+    u32x4 u[2] = {__builtin_bit_cast(u32x4, f[0]), __builtin_bit_cast(u32x4, f[1])};
+    norm_row16<true, true>(u, gm, true, eps);
+    f[0] = u32x4_as_f16x8(u[0]);
+    f[1] = u32x4_as_f16x8(u[1]);
+}
+
+// fp16 Q rows held in a bf16 operand: optionally normalised, rounded to bf16.
+__device__ __forceinline__ void q_rows_f16_to_bf16(bf16x8 (&f)[2], const f32x4 (&gm)[2][2], bool norm, float eps) {
+    u32x4 u[2] = {__builtin_bit_cast(u32x4, f[0]), __builtin_bit_cast(u32x4, f[1])};
+    norm_row16<true, false>(u, gm, norm, eps);
+    f[0] = u32x4_as_bf16x8(u[0]);
+    f[1] = u32x4_as_bf16x8(u[1]);
+}
+
+// Either operand type: the per-head norm of a row of the kernel's own type.
+__device__ __forceinline__ void rms_norm_row(bf16x8 (&f)[2], const f32x4 (&gm)[2][2], float eps) {
+    rms_norm_row_bf16(f, gm, eps);
+}
+__device__ __forceinline__ void rms_norm_row(f16x8 (&f)[2], const f32x4 (&gm)[2][2], float eps) {
+    rms_norm_row_f16(f, gm, eps);
 }
 
 // The eight gamma values of each of a lane's two operand pieces (zeros for
@@ -510,7 +554,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     }
     // q_norm weight for Q rows normalised as they are loaded (bf16)
     f32x4 qgm[2][2];
-    if constexpr (!kQP && !kF16) load_norm_gamma(a.q_gamma, g, qgm);
+    if constexpr (!kQP) load_norm_gamma(a.q_gamma, g, qgm);
 
     // DMA of one tile into a stage: wave w, op j fills LDS chunks
     // (4w + j) * 64 + lane = key * 8 + slot of K (and of V), loading global
@@ -603,10 +647,18 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) asm volatile("" ::"v"(qf[qb][hh]));
-    if constexpr (!kQP && !kF16) {
-        if (a.q_gamma) {
+    if constexpr (!kQP) {
+        if constexpr (!kF16) {
+            if (a.q_f16) {   // fp16 rows: normalised (with q_gamma) and rounded to bf16
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) rms_norm_row_bf16(qf[qb], qgm, a.q_eps);
+                for (int qb = 0; qb < QB; ++qb) q_rows_f16_to_bf16(qf[qb], qgm, a.q_gamma != nullptr, a.q_eps);
+            } else if (a.q_gamma) {
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) rms_norm_row_bf16(qf[qb], qgm, a.q_eps);
+            }
+        } else if (a.q_gamma) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) rms_norm_row_f16(qf[qb], qgm, a.q_eps);
         }
     }
 
@@ -1008,17 +1060,21 @@ __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
     for (int hh = 0; hh < 2; ++hh)
         qf[hh] = __builtin_bit_cast(
             v8, buffer_load16(qrs, (uint32_t)(((q0 + r) * a.q_ss + 32 * hh + 8 * g) * 2)));
-    // q_norm / k_norm weights for rows normalised as they are loaded (bf16)
+    // q_norm / k_norm weights for rows normalised as they are loaded (in the
+    // kernel's element type; fp16 Q rows of a bf16 call are rounded to bf16)
     f32x4 qgm[2][2], kgm[2][2];
+    load_norm_gamma(a.q_gamma, g, qgm);
+    load_norm_gamma(a.k_gamma, g, kgm);
     if constexpr (!kF16) {
-        load_norm_gamma(a.q_gamma, g, qgm);
-        load_norm_gamma(a.k_gamma, g, kgm);
-        if (a.q_gamma) rms_norm_row_bf16(qf, qgm, a.q_eps);
-        if (a.k_gamma) {
+        if (a.q_f16) q_rows_f16_to_bf16(qf, qgm, a.q_gamma != nullptr, a.q_eps);
+        else if (a.q_gamma) rms_norm_row(qf, qgm, a.q_eps);
+    } else {
+        if (a.q_gamma) rms_norm_row(qf, qgm, a.q_eps);
+    }
+    if (a.k_gamma) {
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb)   // the wave's blocks; those past the valid keys stay zero
-                if ((NW == 1 || kb % NW == w) && 16 * kb < valid) rms_norm_row_bf16(kf[kb], kgm, a.q_eps);
-        }
+        for (int kb = 0; kb < KB; ++kb)   // the wave's blocks; those past the valid keys stay zero
+            if ((NW == 1 || kb % NW == w) && 16 * kb < valid) rms_norm_row(kf[kb], kgm, a.q_eps);
     }
 #pragma unroll
     for (int j = 0; j < 2 * KB; ++j) {
@@ -1369,8 +1425,11 @@ int validate(const sf_attn_desc* d) {
             if (reinterpret_cast<uintptr_t>(p) & 15) return SF_EINVAL;
         if ((int64_t)d->q_splits * d->B * d->Sq * d->H * 64 * 4 > 0x7fffffffLL) return SF_ENOTSUP;
     }
+    if (d->q_f16) {   // fp16 Q rows against bf16 K / V
+        if (d->in_dtype != SF_BF16 || d->q_partials) return SF_ENOTSUP;
+    }
     if (d->q_gamma || d->k_gamma) {   // per-head Q / K RMSNorm on load
-        if (d->in_dtype != SF_BF16) return SF_ENOTSUP;
+        if (d->in_dtype == SF_F32) return SF_ENOTSUP;
         if ((reinterpret_cast<uintptr_t>(d->q_gamma) & 15) || (reinterpret_cast<uintptr_t>(d->k_gamma) & 15))
             return SF_EINVAL;
         // K rows are normalised by the short-key kernel only (the key-split
@@ -1500,6 +1559,7 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     a.q_gamma = d->q_gamma;
     a.q_eps = d->q_eps;
     a.k_gamma = d->k_gamma;
+    a.q_f16 = d->q_f16 != 0;
     a.k = static_cast<const uint16_t*>(k);
     a.v = static_cast<const uint16_t*>(v);
     a.o = out;

@@ -487,8 +487,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
 
 struct EpiArgs {
     const float* part;     // [splits][M][N]
-    const uint16_t* part16;  // or the library path's bf16 product [M][ld16], bias and scale already in
+    const uint16_t* part16;  // or the library path's 16-bit product [M][ld16], bias and scale already in
     int64_t ld16;            // row stride of part16 (elements)
+    int part16_f16;          // part16 holds fp16 (else bf16)
     int heads16;             // heads outputs take 16-byte stores (8-aligned head_out, strides)
     int splits;
     int M, N;
@@ -518,6 +519,11 @@ struct EpiArgs {
 // `splits` re-read the last slice and are masked -- plus the bias and scale
 // quads) is issued before the first add, so the epilogue costs one memory
 // round trip.
+// A 16-bit element (bf16, or fp16 when f16) as fp32.
+__device__ __forceinline__ float bits16_to_f32(uint32_t h, int f16) {
+    return f16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)h) : bf16_bits_to_f32(h);
+}
+
 template <int NS>
 struct Quad {
     f32x4 part[NS];
@@ -528,8 +534,8 @@ template <int NS>
 __device__ __forceinline__ void load_quad(const EpiArgs& e, int m, int n, Quad<NS>& q) {
     if (e.part16) {   // one "slice": the rounded product, bias and scale applied
         const uint2 h = *reinterpret_cast<const uint2*>(e.part16 + (int64_t)m * e.ld16 + n);
-        q.part[0] = f32x4{bf16_bits_to_f32(h.x & 0xffffu), bf16_bits_to_f32(h.x >> 16),
-                          bf16_bits_to_f32(h.y & 0xffffu), bf16_bits_to_f32(h.y >> 16)};
+        q.part[0] = f32x4{bits16_to_f32(h.x & 0xffffu, e.part16_f16), bits16_to_f32(h.x >> 16, e.part16_f16),
+                          bits16_to_f32(h.y & 0xffffu, e.part16_f16), bits16_to_f32(h.y >> 16, e.part16_f16)};
 #pragma unroll
         for (int s = 1; s < NS; ++s) q.part[s] = q.part[0];
         q.bias = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -646,8 +652,8 @@ __global__ __launch_bounds__(256) void heads16_kernel(const EpiArgs e) {
     float v[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        v[2 * j] = bf16_bits_to_f32(raw[j] & 0xffffu);
-        v[2 * j + 1] = bf16_bits_to_f32(raw[j] >> 16);
+        v[2 * j] = bits16_to_f32(raw[j] & 0xffffu, e.part16_f16);
+        v[2 * j + 1] = bits16_to_f32(raw[j] >> 16, e.part16_f16);
     }
     const int cols = e.H * 64;
     const int sec = n / cols;
@@ -770,6 +776,43 @@ struct CodesJobs {
     uint32_t start[SF_CODES_MAX_JOBS + 1];
     int32_t count;
 };
+
+// Weight copies in fp16 for the library path's fp16 products: job j holds
+// int8 codes (widened exactly) or bf16 weights (rounded to the nearest
+// fp16: exact for 2^-14 <= |w| < 65520, to within 2^-25 below, +-inf
+// beyond), 16 elements per thread; rows of K elements out of [N][ldq].
+struct W16Jobs {
+    const void* q[SF_CODES_MAX_JOBS];
+    uint16_t* out[SF_CODES_MAX_JOBS];
+    int64_t ldq[SF_CODES_MAX_JOBS];
+    int32_t K[SF_CODES_MAX_JOBS];
+    int32_t bf16[SF_CODES_MAX_JOBS];   // source bf16 (else int8)
+    uint32_t start[SF_CODES_MAX_JOBS + 1];
+    int32_t count;
+};
+
+__global__ __launch_bounds__(256) void weights_f16_kernel(const W16Jobs J) {
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= J.start[J.count]) return;
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < SF_CODES_MAX_JOBS; ++i)
+        if (i < J.count && idx >= J.start[i]) j = i;
+    const uint32_t local = idx - J.start[j];
+    const uint32_t kc = (uint32_t)J.K[j] / 16u;
+    const uint32_t n = local / kc;
+    const uint32_t k = 16u * (local - n * kc);
+    uint16_t* dst = J.out[j] + (int64_t)n * J.K[j] + k;
+    if (J.bf16[j]) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(J.q[j]) + (int64_t)n * J.ldq[j] + k);
+        *reinterpret_cast<f16x8*>(dst) = bf16x8_to_f16x8(src[0]);
+        *reinterpret_cast<f16x8*>(dst + 8) = bf16x8_to_f16x8(src[1]);
+    } else {
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(J.q[j]) + (int64_t)n * J.ldq[j] + k);
+        *reinterpret_cast<f16x8*>(dst) = i8x8_to_f16x8(uint2{raw[0], raw[1]});
+        *reinterpret_cast<f16x8*>(dst + 8) = i8x8_to_f16x8(uint2{raw[2], raw[3]});
+    }
+}
 
 __global__ __launch_bounds__(256) void widen_jobs_kernel(const CodesJobs J) {
     const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
@@ -967,10 +1010,14 @@ LibPlan plan_library(int M, int N, int K, bool w8, bool a_conv) {
 // a bf16 D with the bias epilogue (BIAS, or GELU_BIAS with gelu) and, for
 // int8 weights, the per-row scale as a device alpha vector (one alpha per
 // row of D, i.e. per output column n).  ldd: D's leading dimension.
+// f16: fp16 operands (the activation and an fp16 weight copy) and, with
+// out16, an fp16 D; otherwise bf16 operands and D.
 struct LtKind {
-    bool out16 = false, bias = false, gelu = false, alpha = false;
+    bool out16 = false, bias = false, gelu = false, alpha = false, f16 = false;
     int64_t ldd = 0;
-    int bits() const { return (out16 ? 1 : 0) | (bias ? 2 : 0) | (gelu ? 4 : 0) | (alpha ? 8 : 0); }
+    int bits() const {
+        return (out16 ? 1 : 0) | (bias ? 2 : 0) | (gelu ? 4 : 0) | (alpha ? 8 : 0) | (f16 ? 16 : 0);
+    }
 };
 
 // One hipBLASLt handle per device and one (descriptor, layouts, algorithm)
@@ -1120,9 +1167,10 @@ int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, const LtKind& ki
         ok = ok && hipblasLtMatmulDescSetAttribute(sh.desc, HIPBLASLT_MATMUL_DESC_POINTER_MODE, &pm, sizeof pm) ==
                        HIPBLAS_STATUS_SUCCESS;
     }
-    ok = ok && hipblasLtMatrixLayoutCreate(&sh.a, HIP_R_16BF, K, N, ldw) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatrixLayoutCreate(&sh.b, HIP_R_16BF, K, rows, lda) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatrixLayoutCreate(&sh.d, kind.out16 ? HIP_R_16BF : HIP_R_32F, N, rows, kind.ldd) ==
+    const hipDataType t16 = kind.f16 ? HIP_R_16F : HIP_R_16BF;
+    ok = ok && hipblasLtMatrixLayoutCreate(&sh.a, t16, K, N, ldw) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&sh.b, t16, K, rows, lda) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&sh.d, kind.out16 ? t16 : HIP_R_32F, N, rows, kind.ldd) ==
                    HIPBLAS_STATUS_SUCCESS;
     hipblasLtMatmulPreference_t pref = nullptr;
     ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
@@ -1318,8 +1366,11 @@ int gemm_single_pass(const sf_gemm_desc* d, const sfk::EpiArgs& e, hipStream_t s
 
 // Leading dimensions hipBLASLt sees on the library path: int8 weights are
 // widened into a [N][K] copy, fp32 activations rounded into [chunk][K].
-int64_t lib_ldw(const sf_gemm_desc* d) { return d->w_dtype == SF_I8 ? d->K : d->ldw; }
-int64_t lib_lda(const sf_gemm_desc* d) { return d->a_dtype != SF_BF16 ? d->K : d->lda; }
+// fp16 library path: fp16 activations with the caller's fp16 weight copy
+// (w16_f16), multiplied by hipBLASLt in fp16 as they are.
+bool lib_f16(const sf_gemm_desc* d) { return d->a_dtype == SF_F16 && d->w16_f16 != 0; }
+int64_t lib_ldw(const sf_gemm_desc* d) { return (d->w_dtype == SF_I8 || lib_f16(d)) ? d->K : d->ldw; }
+int64_t lib_lda(const sf_gemm_desc* d) { return (d->a_dtype != SF_BF16 && !lib_f16(d)) ? d->K : d->lda; }
 
 // What the library path stores for this call.  A plain bf16 C (no
 // accumulate, act NONE or GELU) is written by hipBLASLt itself with the bias
@@ -1331,8 +1382,9 @@ int64_t lib_lda(const sf_gemm_desc* d) { return d->a_dtype != SF_BF16 ? d->K : d
 LtKind lib_kind(const sf_gemm_desc* d) {
     LtKind k;
     k.ldd = d->N;
+    k.f16 = lib_f16(d);
     const bool act_ok = d->act == SF_ACT_NONE || d->act == SF_ACT_GELU_TANH;
-    const bool plain16 = d->epilogue == SF_EPI_PLAIN && !d->accumulate && d->c_dtype == SF_BF16;
+    const bool plain16 = d->epilogue == SF_EPI_PLAIN && !d->accumulate && d->c_dtype == (k.f16 ? SF_F16 : SF_BF16);
     const bool rounded = (d->epilogue == SF_EPI_HEADS || d->epilogue == SF_EPI_ADD_NORM) && d->round_product;
     if (!act_ok || !(plain16 || rounded)) return k;
     k.out16 = true;
@@ -1377,6 +1429,7 @@ extern "C" int sf_gemm_prepare(const sf_gemm_desc* d) {
     // single-pass kernel: not an error
     LtKind k;
     k.ldd = d->N;
+    k.f16 = lib_f16(d);
     (void)lib_available(d, lp, k, true);
     k.out16 = k.bias = true;
     k.alpha = d->w_dtype == SF_I8;
@@ -1425,7 +1478,9 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     SF_CHECK_OK(validate(d, e));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool a32 = d->a_dtype == SF_F32;
-    const bool a_conv = d->a_dtype != SF_BF16;   // library path: activations rounded to bf16 first
+    const bool f16lib = lib_f16(d);   // library path in fp16 (the caller's fp16 weight copy)
+    const bool a_conv = d->a_dtype != SF_BF16 && !f16lib;   // library path: activations rounded to bf16 first
+    if (f16lib && (!d->w_codes16 || !al16(d->w_codes16))) return SF_EINVAL;
     if (a32 && ((d->lda & 3) || !al16(d->A))) return SF_EINVAL;
     const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K, a32);
     if (d->epilogue == SF_EPI_PARTIALS) {   // the K-slice sums only, for a consumer to finish
@@ -1458,7 +1513,10 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
             void* ltws = ws + c_bytes + lp.w_bytes + lp.a_bytes;
             const void* W = d->W;
             int64_t ldw = d->ldw;
-            if (w8 && d->w_codes16) {   // the caller's widened copy
+            if (f16lib) {   // the caller's fp16 copy (int8 codes or bf16 weights)
+                W = d->w_codes16;
+                ldw = d->K;
+            } else if (w8 && d->w_codes16) {   // the caller's widened copy
                 if (!al16(d->w_codes16)) return SF_EINVAL;
                 W = d->w_codes16;
                 ldw = d->K;
@@ -1503,8 +1561,9 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
                 ec.splits = 1;
                 ec.M = rows;
                 ec.m_off = m0;
-                if (kind.out16) {   // bias, GELU and the int8 scale are in the bf16 product
+                if (kind.out16) {   // bias, GELU and the int8 scale are in the 16-bit product
                     ec.part = nullptr;
+                    ec.part16_f16 = kind.f16 ? 1 : 0;
                     ec.part16 = reinterpret_cast<const uint16_t*>(cbuf);
                     ec.ld16 = d->N;
                     ec.bias = nullptr;
@@ -1537,6 +1596,36 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     else if (p.splits <= 4) sfk::launch_reduce<4>(d, e, s);
     else if (p.splits <= 8) sfk::launch_reduce<8>(d, e, s);
     else sfk::launch_reduce<16>(d, e, s);
+    return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+}
+
+extern "C" int sf_weights_to_f16(const sf_w16_job* jobs, int32_t count, void* stream) {
+    if (count == 0) return SF_OK;
+    if (!jobs || count < 0 || count > SF_CODES_MAX_JOBS) return SF_EINVAL;
+    sfk::W16Jobs J{};
+    J.count = count;
+    uint64_t total = 0;
+    for (int j = 0; j < count; ++j) {
+        const sf_w16_job& b = jobs[j];
+        if (b.N < 0 || b.K < 0) return SF_EINVAL;
+        if (b.w_dtype != SF_I8 && b.w_dtype != SF_BF16) return SF_EINVAL;
+        J.start[j] = (uint32_t)total;
+        if ((int64_t)b.N * b.K == 0) continue;
+        const int64_t ldbytes = b.ldw * (b.w_dtype == SF_BF16 ? 2 : 1);
+        if (!b.w || !b.out || !al16(b.w) || !al16(b.out) || (b.K & 15) || (ldbytes & 15) || b.ldw < b.K)
+            return SF_EINVAL;
+        J.q[j] = b.w;
+        J.out[j] = static_cast<uint16_t*>(b.out);
+        J.ldq[j] = b.ldw;
+        J.K[j] = b.K;
+        J.bf16[j] = b.w_dtype == SF_BF16;
+        total += (uint64_t)b.N * (uint64_t)(b.K / 16);
+        if (total >= 0x7fffff00ull) return SF_ENOTSUP;   // 32-bit thread indices
+    }
+    J.start[count] = (uint32_t)total;
+    if (total == 0) return SF_OK;
+    hipLaunchKernelGGL(sfk::weights_f16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), J);
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
 }
 

@@ -105,13 +105,25 @@ struct sf_rdt {
     // the per-head epilogue pass.
     bool rows_qkv = false;
     uint16_t* qkv_rows = nullptr;
-    uint16_t* a = nullptr;         // [B*S, D] bf16 attention output
-    // The FFN's inputs (norm3 output, GELU hidden) in ffn_dtype: fp16 while
-    // B*S rows fit the split-K regime (3 more significant bits than bf16 at
-    // the same bytes; the fc1 / fc2 weight fragments are converted to fp16
-    // in registers), bf16 above it.  Of the block's bf16 storage points these
-    // two move the block output furthest from fp32 arithmetic.
-    int32_t ffn_dtype = SF_BF16;
+    uint16_t* a = nullptr;         // [B*S, D] attention output (act16)
+    // Element type of the projections' 16-bit inputs.  The FFN's inputs
+    // (norm3 output, GELU hidden; ffn_dtype) are fp16 at every batch size
+    // (3 more significant bits than bf16 at the same bytes; of the block's
+    // 16-bit storage points these two move the block output furthest from
+    // fp32 arithmetic); on the split-K path the fc1 / fc2 weight fragments
+    // are converted to fp16 in registers.  The other inputs -- norm1 /
+    // norm2 / final-norm outputs and attention outputs (act16) -- are bf16
+    // while B*S rows fit the split-K regime (<= 160) and fp16 above it,
+    // where the library path multiplies fp16 activations by fp16 copies of
+    // the weights (w16) and keeps its 16-bit products in fp16: with bf16
+    // inputs and bf16 products a block sat at 1.6-1.8e-3 from fp32
+    // arithmetic, with fp16 ones at 0.6-0.8e-3.  fp16 holds magnitudes below
+    // 65504: norm outputs stay below sqrt(hidden) * max|gamma|, attention
+    // outputs below max|V| (the cross K/V cache's range is checked when the
+    // condition is set), products and GELU outputs of the block below it as
+    // long as the model's activations do.
+    int32_t ffn_dtype = SF_F16;
+    int32_t act16 = SF_BF16;
     void* n3 = nullptr;            // [B*S, D] norm3 output
     void* h = nullptr;             // [B*S, F] FFN hidden
     uint16_t* act_in = nullptr;    // [B*T, 2A]
@@ -159,13 +171,14 @@ struct sf_rdt {
     size_t attn_ws_bytes = 0;
     void* gemm_ws = nullptr;       // split-K partial sums, shared by the stream's GEMMs
     size_t gemm_ws_bytes = 0;
-    // int8 models above 160 rows (the library path): every block's six
-    // projection weights widened to bf16 codes (sf_int8_codes_to_bf16, up to
-    // eight matrices per launch) once at the start of each entry point's
-    // pass -- once per sampled loop, not once per block and step -- instead
-    // of one widening pass per GEMM.  codes16_of[param] is a weight's copy
-    // (fixed at creation).  The widening runs inside the captured loop, so
-    // a replay after the int8 weights change widens the new codes.
+    // Above 160 rows (the library path): fp16 copies of every block's six
+    // projection weights and of the final layer's two (int8 codes widened
+    // exactly, bf16 weights rounded to fp16; sf_weights_to_f16, up to eight
+    // matrices per launch), refreshed at the start of each entry point's
+    // pass -- once per sampled loop, not once per block and step.
+    // codes16_of[param] is a weight's copy (fixed at creation).  The refresh
+    // runs inside the captured loop, so a replay after the weights change
+    // (they may be written through sf_rdt_param_data) uses the new values.
     char* codes16 = nullptr;
     size_t codes16_bytes = 0;
     std::vector<const void*> codes16_of;
@@ -364,6 +377,7 @@ int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, i
     d.w_dtype = W.dtype;
     d.w_scale = W.scale;
     d.w_codes16 = m->codes16_of[w_idx];
+    d.w16_f16 = d.w_codes16 ? 1 : 0;
     d.bias = b_idx >= 0 ? pf(m, b_idx) : nullptr;
     d.act = act;
     d.epilogue = SF_EPI_PLAIN;
@@ -396,6 +410,7 @@ int linear_add_norm(sf_rdt* m, const void* A, int a_dtype, int M, int w_idx, int
     d.w_dtype = W.dtype;
     d.w_scale = W.scale;
     d.w_codes16 = m->codes16_of[w_idx];
+    d.w16_f16 = d.w_codes16 ? 1 : 0;
     d.bias = pf(m, b_idx);
     d.epilogue = SF_EPI_ADD_NORM;
     d.C = m->x;
@@ -433,6 +448,7 @@ int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
     d.w_dtype = W.dtype;
     d.w_scale = W.scale;
     d.w_codes16 = m->codes16_of[w_idx];
+    d.w16_f16 = d.w_codes16 ? 1 : 0;
     d.bias = pf(m, b_idx);
     d.epilogue = SF_EPI_HEADS;
     d.H = H;
@@ -470,6 +486,7 @@ struct RowsIn {
     int64_t kv_ld = 0;   // 0: K, V in [B, H, Sc, 64]
     const float* q_gamma = nullptr;
     const float* k_gamma = nullptr;
+    bool f16 = false;    // rows in fp16: with kv_ld, Q, K and V (an fp16 attention); else Q only
 };
 
 // Sc: the rows per head of the K/V buffer (its capacity), Sk <= Sc the keys
@@ -480,7 +497,9 @@ int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v
     const sf_rdt_config& c = m->cfg;
     const int S = c.horizon + 3;
     sf_attn_desc d;
-    sf_attn_desc_init_bhsd(&d, c.batch, c.heads, S, Sk, 64, SF_BF16, SF_BF16);
+    const bool all16 = rows && rows->f16 && rows->kv_ld;
+    sf_attn_desc_init_bhsd(&d, c.batch, c.heads, S, Sk, 64, all16 ? SF_F16 : SF_BF16, m->act16);
+    if (rows && rows->f16 && !rows->kv_ld) d.q_f16 = 1;
     if (rows) {
         d.q_stride[0] = (int64_t)S * rows->q_ld;
         d.q_stride[1] = 64;
@@ -555,6 +574,20 @@ int cross_q_partials(sf_rdt* m, const LayerIdx& L, int M, hipStream_t s, QPartia
     return SF_OK;
 }
 
+// The projection weights that get fp16 copies above 160 rows: every
+// block's six and the final layer's two (their K a multiple of 16).
+std::vector<int> w16_params(const sf_rdt* m) {
+    std::vector<int> ws;
+    for (const LayerIdx& L : m->layers)
+        for (int w : block_weights(L)) ws.push_back(w);
+    ws.push_back(m->f1w);
+    ws.push_back(m->f2w);
+    std::vector<int> out;
+    for (int w : ws)
+        if (m->params[w].shape[1] % 16 == 0) out.push_back(w);
+    return out;
+}
+
 // Every GEMM the runtime issues: each matrix at each row count it is used
 // with (step rows B*S, B*T, B, 1; condition rows B*lang_max, B*img_len).
 // Returns the largest workspace; with prepare, also selects the library
@@ -565,11 +598,16 @@ size_t gemm_ws_for(const sf_rdt* m, bool prepare, int* status) {
                          c.batch * c.lang_max, c.batch * c.img_len,
                          std::min(160, c.lang_max)};   // largest split-K M (language rows at batch 1)
     size_t best = 0;
-    for (const Param& p : m->params) {
+    // weights with an fp16 copy (above 160 rows) multiply fp16 activations
+    // in fp16 on the library path
+    std::vector<char> w16(m->params.size(), 0);
+    if (c.batch * (c.horizon + 3) > 160)
+        for (int w : w16_params(m)) w16[w] = 1;
+    for (size_t pi = 0; pi < m->params.size(); ++pi) {
+        const Param& p = m->params[pi];
         if (p.shape.size() != 2 || p.dtype == SF_F32) continue;
         for (int M : rows) {
             for (int ad : {SF_BF16, SF_F16}) {
-                if (ad == SF_F16 && ad != m->ffn_dtype) continue;
                 sf_gemm_desc d{};
                 d.M = M;
                 d.N = (int32_t)p.shape[0];
@@ -578,6 +616,7 @@ size_t gemm_ws_for(const sf_rdt* m, bool prepare, int* status) {
                 d.a_dtype = ad;
                 d.ldw = d.K;
                 d.w_dtype = p.dtype;
+                d.w16_f16 = ad == SF_F16 && w16[pi];
                 best = std::max(best, sf_gemm_workspace_bytes(&d));
                 if (prepare && status && *status == SF_OK) *status = sf_gemm_prepare(&d);
             }
@@ -620,28 +659,35 @@ int next_norm(const sf_rdt* m, int i) {
     return i + 1 < m->cfg.layers ? m->layers[i + 1].norm1 : m->fnorm;
 }
 
-// Refreshes the bf16 code copies of blocks [first, first + count)'s int8
-// weights (no-op without them), up to SF_CODES_MAX_JOBS matrices per launch.
-int widen_codes(sf_rdt* m, int first, int count, hipStream_t s) {
+// Refreshes the fp16 weight copies of blocks [first, first + count) and,
+// with final_layer, of the final layer (no-op without copies), up to
+// SF_CODES_MAX_JOBS matrices per launch.
+int widen_codes(sf_rdt* m, int first, int count, hipStream_t s, bool final_layer = false) {
     if (!m->codes16) return SF_OK;
-    sf_codes_job jobs[SF_CODES_MAX_JOBS];
+    sf_w16_job jobs[SF_CODES_MAX_JOBS];
     int n = 0;
-    for (int i = first; i < first + count; ++i) {
-        for (int w : block_weights(m->layers[i])) {
-            const Param& P = m->params[w];
-            if (!m->codes16_of[w]) continue;
-            jobs[n].q = static_cast<const int8_t*>(P.data);
-            jobs[n].ldq = P.shape[1];
-            jobs[n].out = const_cast<void*>(m->codes16_of[w]);
-            jobs[n].N = (int32_t)P.shape[0];
-            jobs[n].K = (int32_t)P.shape[1];
-            if (++n == SF_CODES_MAX_JOBS) {
-                SF_TRY(sf_int8_codes_to_bf16(jobs, n, s));
-                n = 0;
-            }
+    std::vector<int> ws;
+    for (int i = first; i < first + count; ++i)
+        for (int w : block_weights(m->layers[i])) ws.push_back(w);
+    if (final_layer) {
+        ws.push_back(m->f1w);
+        ws.push_back(m->f2w);
+    }
+    for (int w : ws) {
+        const Param& P = m->params[w];
+        if (!m->codes16_of[w]) continue;
+        jobs[n].w = P.data;
+        jobs[n].w_dtype = P.dtype;
+        jobs[n].ldw = P.shape[1];
+        jobs[n].out = const_cast<void*>(m->codes16_of[w]);
+        jobs[n].N = (int32_t)P.shape[0];
+        jobs[n].K = (int32_t)P.shape[1];
+        if (++n == SF_CODES_MAX_JOBS) {
+            SF_TRY(sf_weights_to_f16(jobs, n, s));
+            n = 0;
         }
     }
-    return n ? sf_int8_codes_to_bf16(jobs, n, s) : SF_OK;
+    return n ? sf_weights_to_f16(jobs, n, s) : SF_OK;
 }
 
 // RDTBlock::forward (dit_block.cu:349-387) on the fp32 residual m->x, with
@@ -651,16 +697,17 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const LayerIdx& L = m->layers[i];
     const int D = c.hidden, S = c.horizon + 3, M = c.batch * S;
-    const int fd = m->ffn_dtype;
+    const int fd = m->ffn_dtype, ad = m->act16;
     // self-attention branch
     if (m->rows_qkv) {
-        // qkv = x W^T + b in bf16 (dit_block.cu:206-207); split_qkv and
+        // qkv = x W^T + b in fp16 (dit_block.cu:206-207); split_qkv and
         // apply_qk_norm (:209-220) happen as the attention loads the rows
-        SF_TRY(linear(m, m->n, D, M, L.qkv_w, L.qkv_b, SF_ACT_NONE, m->qkv_rows, 3 * D, SF_BF16, false, s));
+        SF_TRY(linear(m, m->n, D, M, L.qkv_w, L.qkv_b, SF_ACT_NONE, m->qkv_rows, 3 * D, ad, false, s, ad));
         RowsIn r;
         r.q_ld = r.kv_ld = 3 * D;
         r.q_gamma = pf(m, L.q_norm);
         r.k_gamma = pf(m, L.k_norm);
+        r.f16 = ad == SF_F16;
         SF_TRY(attention(m, m->qkv_rows, m->qkv_rows + D, m->qkv_rows + 2 * D, S, nullptr, m->a, false, s, 0,
                          nullptr, &r));
     } else {
@@ -669,7 +716,7 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
         SF_TRY(linear_heads(m, m->n, M, S, L.qkv_w, L.qkv_b, qkv, qk_g, 3, s, SF_BF16, true));
         SF_TRY(attention(m, m->q, m->k, m->v, S, nullptr, m->a, false, s));
     }
-    SF_TRY(linear_add_norm(m, m->a, SF_BF16, M, L.proj_w, L.proj_b, L.norm2, m->n, SF_BF16, s));
+    SF_TRY(linear_add_norm(m, m->a, ad, M, L.proj_w, L.proj_b, L.norm2, m->n, ad, s));
     // cross-attention branch: even blocks attend to language, odd to image
     // (dit_block.cu:369)
     const bool lang = (i % 2) == 0;
@@ -679,12 +726,14 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
         SF_TRY(attention(m, nullptr, m->ck[i], m->cv[i], m->cond_lang_rows, m->lang_len, m->a,
                          m->exact_pv[i] != 0, s, c.lang_max, &qp));
     } else if (m->rows_qkv) {
-        // q = x W^T + b in bf16 rows (dit_block.cu:282-284); seq_to_head and
-        // q_norm (:298-307) happen as the attention loads them
-        SF_TRY(linear(m, m->n, D, M, L.cq_w, L.cq_b, SF_ACT_NONE, m->q, D, SF_BF16, false, s));
+        // q = x W^T + b in fp16 rows (dit_block.cu:282-284); seq_to_head and
+        // q_norm (:298-307) happen as the attention loads them (rounding Q to
+        // bf16 for the bf16 K/V cache)
+        SF_TRY(linear(m, m->n, D, M, L.cq_w, L.cq_b, SF_ACT_NONE, m->q, D, ad, false, s, ad));
         RowsIn r;
         r.q_ld = D;
         r.q_gamma = pf(m, L.cq_norm);
+        r.f16 = ad == SF_F16;
         SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? m->cond_lang_rows : c.img_len,
                          lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,
                          lang ? c.lang_max : c.img_len, nullptr, &r));
@@ -696,12 +745,12 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
                          lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,
                          lang ? c.lang_max : c.img_len));
     }
-    SF_TRY(linear_add_norm(m, m->a, SF_BF16, M, L.cproj_w, L.cproj_b, L.norm3, m->n3, fd, s));
+    SF_TRY(linear_add_norm(m, m->a, ad, M, L.cproj_w, L.cproj_b, L.norm3, m->n3, fd, s));
     // FFN branch (Mlp::forward, dit_block.cu:143-163); fc2's add + norm
-    // writes the next block's norm1 (bf16, the QKV input)
+    // writes the next block's norm1 (act16, the QKV input)
     const int F = (int)ffn_dim(c);
     SF_TRY(linear(m, m->n3, D, M, L.fc1_w, L.fc1_b, SF_ACT_GELU_TANH, m->h, F, fd, false, s, fd));
-    return linear_add_norm(m, m->h, fd, M, L.fc2_w, L.fc2_b, next_norm(m, i), m->n, SF_BF16, s);
+    return linear_add_norm(m, m->h, fd, M, L.fc2_w, L.fc2_b, next_norm(m, i), m->n, ad, s);
 }
 
 // m->n = first norm applied to the residual m->x before block `first`.
@@ -709,7 +758,7 @@ int entry_norm(sf_rdt* m, int first, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const int D = c.hidden, M = c.batch * (c.horizon + 3);
     const int g = first < c.layers ? m->layers[first].norm1 : m->fnorm;
-    return sf_rmsnorm(m->x, SF_F32, D, pf(m, g), m->n, SF_BF16, D, M, D, c.eps, s);
+    return sf_rmsnorm(m->x, SF_F32, D, pf(m, g), m->n, m->act16, D, M, D, c.eps, s);
 }
 
 // The timestep index of t (rdt1b.cpp:312-313): round(t * (T_train - 1)).
@@ -742,10 +791,10 @@ int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s, bool widen
     SF_TRY(sf_assemble_tokens(m->x, t_emb, m->f_emb, m->state_tok, m->act_out, pf(m, m->xpos),
                               c.batch, T, D, s));
     SF_TRY(entry_norm(m, 0, s));
-    if (widen) SF_TRY(widen_codes(m, 0, c.layers, s));
+    if (widen) SF_TRY(widen_codes(m, 0, c.layers, s, true));
     for (int i = 0; i < c.layers; ++i) SF_TRY(block_forward(m, i, s));
     // FinalLayer (dit_block.cu:407-412); m->n = norm_final(x) from the last block
-    SF_TRY(linear(m, m->n, D, M, m->f1w, m->f1b, SF_ACT_GELU_TANH, m->h, D, m->ffn_dtype, false, s));
+    SF_TRY(linear(m, m->n, D, M, m->f1w, m->f1b, SF_ACT_GELU_TANH, m->h, D, m->ffn_dtype, false, s, m->act16));
     return linear(m, m->h, D, M, m->f2w, m->f2b, SF_ACT_NONE, m->vel_rows, A, SF_F32, false, s,
                   m->ffn_dtype);
 }
@@ -763,7 +812,7 @@ std::vector<float> schedule(int num_steps) {
 int sample_body(sf_rdt* m, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const std::vector<float> ts = schedule(c.num_steps);
-    SF_TRY(widen_codes(m, 0, c.layers, s));   // once for every step of the loop
+    SF_TRY(widen_codes(m, 0, c.layers, s, true));   // once for every step of the loop
     for (int step = 0; step < c.num_steps; ++step) {
         SF_TRY(step_forward(m, m->x_state, ts[step], s, false, m->t_emb_steps + (size_t)step * c.hidden));
         const float dt = ts[step + 1] - ts[step];
@@ -842,8 +891,10 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
         return SF_ENOTSUP;   // GEMM K dims are multiples of 32
     sf_rdt* m = new sf_rdt();
     m->cfg = c;
-    // fp16 FFN inputs while the block GEMMs run split-K (M <= 160 rows)
-    m->ffn_dtype = c.batch * (c.horizon + 3) <= 160 ? SF_F16 : SF_BF16;
+    // fp16 FFN inputs at every batch size; the other projection inputs in
+    // fp16 once the block GEMMs leave the split-K regime (M > 160 rows)
+    m->ffn_dtype = SF_F16;
+    m->act16 = c.batch * (c.horizon + 3) <= 160 ? SF_BF16 : SF_F16;
     build_param_table(m);
 
     const int64_t B = c.batch, D = c.hidden, T = c.horizon, S = T + 3, A = c.action_dim;
@@ -943,11 +994,9 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     bufs.push_back({&m->gemm_ws, std::max<size_t>(m->gemm_ws_bytes, 256)});
     m->rows_qkv = S * B > 160;
     if (m->rows_qkv) bufs.push_back({(void**)&m->qkv_rows, (size_t)(B * S * 3 * D * 2)});
-    if (S * B > 160) {   // every block's int8 weights as bf16 codes
-        for (const LayerIdx& L : m->layers)
-            for (int w : block_weights(L))
-                if (m->params[w].dtype == SF_I8)
-                    m->codes16_bytes += align256((size_t)m->params[w].shape[0] * m->params[w].shape[1] * 2);
+    if (S * B > 160) {   // fp16 copies of the block and final-layer projection weights
+        for (int w : w16_params(m))
+            m->codes16_bytes += align256((size_t)m->params[w].shape[0] * m->params[w].shape[1] * 2);
         if (m->codes16_bytes) bufs.push_back({(void**)&m->codes16, m->codes16_bytes});
     }
     std::vector<size_t> boff(bufs.size());
@@ -975,13 +1024,11 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     m->codes16_of.assign(m->params.size(), nullptr);
     if (m->codes16) {
         char* dst = m->codes16;
-        for (const LayerIdx& L : m->layers)
-            for (int w : block_weights(L)) {
-                const Param& P = m->params[w];
-                if (P.dtype != SF_I8) continue;
-                m->codes16_of[w] = dst;
-                dst += align256((size_t)P.shape[0] * P.shape[1] * 2);
-            }
+        for (int w : w16_params(m)) {
+            const Param& P = m->params[w];
+            m->codes16_of[w] = dst;
+            dst += align256((size_t)P.shape[0] * P.shape[1] * 2);
+        }
     }
     m->exact_pv.assign(c.layers, 0);
     m->lang_rows = m->cond_lang_rows = c.lang_max;
@@ -1277,7 +1324,7 @@ extern "C" int sf_rdt_run_blocks(sf_rdt* m, float* x, int32_t first, int32_t cou
     const size_t nbytes = (size_t)c.batch * (c.horizon + 3) * c.hidden * 4;
     SF_HIP(hipMemcpyAsync(m->x, x, nbytes, hipMemcpyDeviceToDevice, s));
     SF_TRY(entry_norm(m, first, s));
-    SF_TRY(widen_codes(m, first, count, s));
+    SF_TRY(widen_codes(m, first, count, s, false));
     for (int i = first; i < first + count; ++i) SF_TRY(block_forward(m, i, s));
     SF_HIP(hipMemcpyAsync(x, m->x, nbytes, hipMemcpyDeviceToDevice, s));
     return SF_OK;

@@ -48,18 +48,26 @@ def workspace_bytes(a, w):
     return abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d))
 
 
+def _w16(d, w16):
+    """An fp16 copy of the weights (weights_to_f16) for the library path."""
+    if w16 is not None:
+        d.w_codes16, d.w16_f16 = w16.data_ptr(), 1
+
+
 def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat16,
-         accumulate=False, w_scale=None, workspace="auto", w_codes16=None):
+         accumulate=False, w_scale=None, workspace="auto", w_codes16=None, w16=None):
     """out[M,N] = act(a[M,K] w[N,K]^T + bias) (bf16 a; bf16 or int8 w with
     per-row fp32 w_scale).  accumulate adds into an fp32 `out`.  w_codes16:
     int8 w's codes as bf16 (int8_codes_to_bf16), read by the library path
-    instead of widening them."""
+    instead of widening them.  w16: an fp16 copy of w (weights_to_f16) for
+    fp16 `a`: the library path then multiplies in fp16."""
     M, K = a.shape
     N = w.shape[0]
     if out is None:
         out = torch.empty(M, N, dtype=out_dtype, device=a.device)
     d = _desc(a, w, bias, act, w_scale)
     d.w_codes16 = _p(w_codes16)
+    _w16(d, w16)
     d.epilogue = abi.SF_EPI_PLAIN
     d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), _DT[out.dtype]
     d.accumulate = 1 if accumulate else 0
@@ -68,14 +76,16 @@ def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat1
 
 
 def gemm_add_norm(a, w, bias, residual, gamma, eps=1e-6, act=abi.SF_ACT_NONE, w_scale=None,
-                  norm_dtype=torch.bfloat16, workspace="auto", round_product=False):
+                  norm_dtype=torch.bfloat16, workspace="auto", round_product=False, w16=None):
     """residual (fp32 [M,N]) += act(a w^T + bias); returns
     rmsnorm(residual) * gamma in norm_dtype.  round_product: above 160 rows
-    the branch output is stored in bf16 before the add."""
+    the branch output is stored in 16 bits before the add (bf16, or fp16
+    with w16)."""
     M = a.shape[0]
     N = w.shape[0]
     out = torch.empty(M, N, dtype=norm_dtype, device=a.device)
     d = _desc(a, w, bias, act, w_scale)
+    _w16(d, w16)
     d.epilogue = abi.SF_EPI_ADD_NORM
     d.C, d.ldc, d.c_dtype = residual.data_ptr(), residual.stride(0), abi.SF_F32
     d.eps = eps
@@ -87,12 +97,13 @@ def gemm_add_norm(a, w, bias, residual, gamma, eps=1e-6, act=abi.SF_ACT_NONE, w_
 
 
 def gemm_heads(a, w, bias, S, H, outs, gammas=(None, None, None), eps=1e-6, w_scale=None,
-               workspace="auto", round_product=False):
+               workspace="auto", round_product=False, w16=None):
     """Projection whose N columns are sections of H*64, written per head to
     outs[j] ([B,H,S,64] bf16 views) with optional per-head RMSNorm.
-    round_product: above 160 rows the projection is stored in bf16 before
-    the norm."""
+    round_product: above 160 rows the projection is stored in 16 bits
+    before the norm (bf16, or fp16 with w16)."""
     d = _desc(a, w, bias, abi.SF_ACT_NONE, w_scale)
+    _w16(d, w16)
     d.epilogue = abi.SF_EPI_HEADS
     d.H, d.S, d.eps = H, S, eps
     d.round_product = 1 if round_product else 0
@@ -114,6 +125,18 @@ def int8_codes_to_bf16(qs):
         jobs[j].N, jobs[j].K = q.shape[0], q.shape[1]
     st = abi.lib().sf_int8_codes_to_bf16(jobs, len(qs), _stream(qs[0]) if qs else None)
     abi.check(st, "sf_int8_codes_to_bf16")
+    return outs
+
+
+def weights_to_f16(ws):
+    """fp16 copies [N][K] of bf16 or int8 (codes) matrices, one launch (at
+    most abi.SF_CODES_MAX_JOBS)."""
+    outs = [torch.empty(w.shape[0], w.shape[1], dtype=torch.float16, device=w.device) for w in ws]
+    jobs = (abi.W16Job * max(1, len(ws)))()
+    for j, (w, o) in enumerate(zip(ws, outs)):
+        jobs[j].w, jobs[j].w_dtype, jobs[j].ldw = w.data_ptr(), _DT[w.dtype], w.stride(0)
+        jobs[j].out, jobs[j].N, jobs[j].K = o.data_ptr(), w.shape[0], w.shape[1]
+    abi.check(abi.lib().sf_weights_to_f16(jobs, len(ws), _stream(ws[0]) if ws else None), "sf_weights_to_f16")
     return outs
 
 

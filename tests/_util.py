@@ -25,3 +25,11 @@ def assert_close_bf16(got, ref, what=""):
     mr = mean_rel(got, ref) if got.size else 0.0
     assert mx <= MAX_ABS and mr <= MEAN_REL, f"{what}: max-abs {mx:.3e}, mean-rel {mr:.3e}"
     return mx, mr
+
+
+def cosine(got, ref):
+    """Cosine similarity of the flattened arrays (the reference's alignment
+    metric, tests/alignment/test_rdt1b_alignment.py:287-299, 426)."""
+    g = np.asarray(got, dtype=np.float64).ravel()
+    r = np.asarray(ref, dtype=np.float64).ravel()
+    return float(g @ r / max(np.linalg.norm(g) * np.linalg.norm(r), 1e-300))

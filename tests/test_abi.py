@@ -216,6 +216,27 @@ def test_int8_codes_to_bf16_rejects_bad_jobs():
         assert lib.sf_int8_codes_to_bf16(one, 1, None) == abi.SF_EINVAL, (field, bad)
 
 
+def test_weights_to_f16_rejects_bad_jobs():
+    """Argument checks of the fp16 weight copies, before any launch: too
+    many jobs, a source type other than int8 / bf16, K or the row stride
+    (in bytes) not a multiple of 16, misaligned pointers, stride below K."""
+    lib = abi.lib()
+    jobs = (abi.W16Job * (abi.SF_CODES_MAX_JOBS + 1))()
+    for j in jobs:
+        j.w, j.w_dtype, j.ldw, j.out, j.N, j.K = 256, abi.SF_BF16, 64, 512, 4, 64
+    assert lib.sf_weights_to_f16(jobs, 0, None) == abi.SF_OK
+    assert lib.sf_weights_to_f16(jobs, abi.SF_CODES_MAX_JOBS + 1, None) == abi.SF_EINVAL
+    assert lib.sf_weights_to_f16(jobs, -1, None) == abi.SF_EINVAL
+    cases = [("K", 40, abi.SF_BF16), ("ldw", 48, abi.SF_BF16), ("w", 264, abi.SF_BF16), ("out", 520, abi.SF_BF16),
+             ("N", -1, abi.SF_BF16), ("w_dtype", abi.SF_F32, abi.SF_F32), ("w_dtype", abi.SF_F16, abi.SF_F16),
+             ("ldw", 72, abi.SF_I8), ("ldw", 68, abi.SF_BF16)]
+    for field, bad, wd in cases:
+        one = (abi.W16Job * 1)()
+        one[0].w, one[0].w_dtype, one[0].ldw, one[0].out, one[0].N, one[0].K = 256, wd, 64, 512, 4, 64
+        setattr(one[0], field, bad)
+        assert lib.sf_weights_to_f16(one, 1, None) == abi.SF_EINVAL, (field, bad)
+
+
 def test_absmax_batched_rejects_bad_jobs():
     """Argument checks of the batched max-|x| scan, before any launch: job
     count outside 0..SF_ABSMAX_MAX_JOBS, a missing output, a negative
@@ -267,7 +288,7 @@ def test_ctypes_mirrors_match_the_c_layout(tmp_path):
     cc = shutil.which("gcc") or shutil.which("cc")
     if cc is None:
         pytest.skip("no C compiler")
-    mirrors = {"sf_attn_desc": abi.AttnDesc, "sf_gemm_desc": abi.GemmDesc, "sf_codes_job": abi.CodesJob,
+    mirrors = {"sf_attn_desc": abi.AttnDesc, "sf_gemm_desc": abi.GemmDesc, "sf_codes_job": abi.CodesJob, "sf_w16_job": abi.W16Job,
                "sf_absmax_job": abi.AbsmaxJob, "sf_rdt_config": rdt.RdtConfig, "sf_st_entry": rdt.StEntry}
     lines = ['#include <stdio.h>', '#include "sf_rdt.h"', 'int main(void) {']
     for cname, py in mirrors.items():
@@ -298,6 +319,9 @@ def test_qk_norm_on_load_contract():
     d.q_gamma, d.k_gamma = 16, 40
     assert _fwd(d) == abi.SF_EINVAL
     d = abi.attn_desc_bhsd(1, 2, 67, 67, in_dtype=abi.SF_F16)
+    d.q_gamma = 24
+    assert _fwd(d) == abi.SF_EINVAL   # fp16 rows take the norm too (alignment still checked)
+    d = abi.attn_desc_bhsd(1, 2, 67, 67, in_dtype=abi.SF_F32)
     d.q_gamma = 16
     assert _fwd(d) == abi.SF_ENOTSUP
     d = abi.attn_desc_bhsd(1, 2, 67, 67, in_dtype=abi.SF_F32)
@@ -308,6 +332,18 @@ def test_qk_norm_on_load_contract():
     assert _fwd(d) == abi.SF_ENOTSUP
     d = abi.attn_desc_bhsd(1, 2, 67, 67)
     d.num_splits, d.k_gamma = 2, 16
+    assert _fwd(d) == abi.SF_ENOTSUP
+
+
+def test_q_f16_contract():
+    """q_f16 (fp16 Q rows against bf16 K / V): bf16 in_dtype only, and not
+    with Q given as projection partials."""
+    for dt in (abi.SF_F16, abi.SF_F32):
+        d = abi.attn_desc_bhsd(1, 2, 67, 4374, in_dtype=dt)
+        d.q_f16 = 1
+        assert _fwd(d) == abi.SF_ENOTSUP, dt
+    d = abi.attn_desc_bhsd(1, 2, 67, 512)
+    d.q_f16, d.q_partials, d.q_splits = 1, 256, 2
     assert _fwd(d) == abi.SF_ENOTSUP
 
 

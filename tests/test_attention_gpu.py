@@ -666,3 +666,65 @@ def test_qk_norm_on_load_grouped_waves(B, S, lens):
     torch.cuda.synchronize()
     assert torch.isfinite(ref).all()
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("B", [3, 16, 32])
+def test_qk_norm_on_load_fp16_self_attention(B):
+    """The runtime's self-attention above 160 rows: Q, K and V read from the
+    QKV projection's fp16 rows, q_norm / k_norm applied on load in fp32 and
+    rounded to fp16, the fp16 contraction.  Against the fp32 oracle on the
+    same normalisation (fp64, rounded to fp16) at the bf16 bar; every
+    grouping of the short-key kernel (B*H = 96: one wave per workgroup;
+    512, 1024: five)."""
+    H, S = 32, 67
+    dev = torch.device(DEV)
+    g = torch.Generator(device=dev).manual_seed(700 + B)
+    P = (torch.randn(B * S, 3 * H * 64, device=dev, generator=g) * 3.0).to(torch.float16)
+    gq = torch.rand(64, device=dev, generator=g) + 0.5
+    gk = torch.rand(64, device=dev, generator=g) + 0.5
+    got = attention(*(_rows_as_heads(P, S, H, j) for j in range(3)), out_dtype=torch.float32,
+                    q_gamma=gq, k_gamma=gk)
+    Ph = P.float().cpu().numpy().astype(np.float64).reshape(B, S, 3, H, 64).transpose(2, 0, 3, 1, 4)
+
+    def norm16(x, gm):
+        inv = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6)
+        return (x * inv * gm.cpu().numpy().astype(np.float64)).astype(np.float16).astype(np.float32)
+
+    q, k, v = norm16(Ph[0], gq), norm16(Ph[1], gk), Ph[2].astype(np.float32)
+    ref = O.attention_f32(q, k, v)
+    mx, mr = assert_close_bf16(got.cpu().numpy(), ref, f"fp16 rows self-attention B={B}")
+    assert mr < 2e-4, mr
+
+
+@pytest.mark.parametrize("B,Sk,lang,exact", [(16, 4374, False, False), (3, 4374, False, True),
+                                             (3, 1024, True, False), (16, 1024, True, False)])
+def test_q_f16_rows_cross_attention(B, Sk, lang, exact):
+    """The runtime's cross-attention above 160 rows: Q from the cross-q
+    projection's fp16 rows (q_f16), normalised on load and rounded to bf16,
+    against the bf16 K/V cache.  For fp16 rows whose values are bf16
+    numbers the result equals, bit for bit, the same rows given in bf16
+    (both normalise the same floats in the same order); on general fp16
+    rows it meets the bf16 bar against the oracle.  Every grid of the
+    runtime: (batch, head) workgroups, key splits + merge, query blocks."""
+    H, S = 32, 67
+    dev = torch.device(DEV)
+    g = torch.Generator(device=dev).manual_seed(800 + B + Sk)
+    P16 = (torch.randn(B * S, H * 64, device=dev, generator=g) * 3.0).to(torch.bfloat16)
+    gq = torch.rand(64, device=dev, generator=g) + 0.5
+    k = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    vl = torch.from_numpy(lang_valid_lengths(B, B)).to(dev) if lang else None
+    kw = dict(out_dtype=torch.float32, valid_len=vl, exact_pv=exact, q_gamma=gq)
+    ref_b = attention(_rows_as_heads(P16, S, H, 0), k, v, **kw)
+    got_b = attention(_rows_as_heads(P16.to(torch.float16), S, H, 0), k, v, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(ref_b).all()
+    assert torch.equal(got_b, ref_b)
+    Pf = (torch.randn(B * S, H * 64, device=dev, generator=g) * 3.0).to(torch.float16)
+    got = attention(_rows_as_heads(Pf, S, H, 0), k, v, **kw)
+    x = Pf.float().cpu().numpy().astype(np.float64).reshape(B, S, H, 64).transpose(0, 2, 1, 3)
+    q = O.bf16_round((x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) *
+                      gq.cpu().numpy().astype(np.float64)).astype(np.float32))
+    ref = O.attention_f32(q, k.float().cpu().numpy(), v.float().cpu().numpy(),
+                          valid_len=None if vl is None else vl.cpu().numpy())
+    assert_close_bf16(got.cpu().numpy(), ref, f"fp16 Q rows cross-attention B={B} Sk={Sk}")

@@ -566,6 +566,106 @@ def test_gemm_fp16_activations_library_path():
     close(got, O.linear(O.bf16_round(a), w, b), "fp16-activation library gemm")
 
 
+def test_weights_to_f16_exact():
+    """sf_weights_to_f16: int8 codes widen to fp16 exactly (all 256 codes);
+    bf16 weights round to the nearest fp16, bit for bit torch's conversion --
+    fp16 subnormals, 65504, the first value that rounds to inf (65520) and
+    beyond included; a row-strided source view; three jobs in one launch."""
+    d = torch.device(DEV)
+    codes = torch.arange(-128, 128, dtype=torch.int32).to(torch.int8).repeat(16, 1).contiguous().to(d)
+    g = torch.Generator(device=d).manual_seed(5)
+    wb = (torch.randn(96, 512, device=d, generator=g) * 0.02).to(torch.bfloat16)
+    wb[0, :10] = torch.tensor([1e-6, -3e-7, 6e-5, 65504.0, 65520.0, -70000.0, 1e-9, 0.0, 2.0 ** -24, -2.0 ** -25],
+                              dtype=torch.bfloat16)
+    big = torch.randn(32, 1024, device=d, generator=g).to(torch.bfloat16)
+    view = big[:, :512]
+    c16, b16, v16 = K.weights_to_f16([codes, wb, view])
+    torch.cuda.synchronize()
+    assert torch.equal(c16, codes.to(torch.float16))
+    assert torch.equal(b16.view(torch.int16), wb.to(torch.float16).view(torch.int16))
+    assert torch.equal(v16, view.to(torch.float16))
+
+
+@pytest.mark.parametrize("w8", [False, True])
+def test_gemm_fp16_library_path_with_f16_copy(w8):
+    """M > 160 with fp16 activations and an fp16 copy of the weights
+    (w16_f16; int8 codes widened exactly, bf16 weights rounded): hipBLASLt
+    multiplies in fp16 and nothing is rounded to bf16 --
+      * fp32 C against the oracle on the same fp16 values (exact products,
+        only the summation order differs);
+      * a plain fp16 C that hipBLASLt writes with its GELU + bias epilogue:
+        the fp32 result rounded to fp16, within one fp16 ulp;
+      * the per-head norm and the residual add + norm over the fp16 product
+        (round_product): the oracle's fp16-rounded product, normed."""
+    B, S, H = 16, 67, 32
+    M, Kd = B * S, 2048
+    a = f16r(O.randn(171, (M, Kd)))
+    ad = dev(a, torch.float16)
+    w, wdev, sdev = _library_weights(172, 2048, Kd, w8)
+    (w16,) = K.weights_to_f16([wdev])
+    b = O.randn(173, (2048,), 0.02)
+    bd = dev(b, torch.float32)
+    ref = O.linear(a, w, b)
+    close(host(K.gemm(ad, wdev, bd, out_dtype=torch.float32, w_scale=sdev, w16=w16)), ref, "fp16 library fp32 C")
+    got16 = host(K.gemm(ad, wdev, bd, abi.SF_ACT_GELU_TANH, out_dtype=torch.float16, w_scale=sdev, w16=w16))
+    rg = O.linear(a, w, b, act=abi.SF_ACT_GELU_TANH)
+    # one fp16 rounding of the fp32 result, plus the difference between
+    # hipBLASLt's GELU and the tanh form in the negative tail, where
+    # 1 + tanh cancels (an absolute term)
+    excess = np.abs(got16 - rg) - np.abs(rg) * 2.0 ** -10
+    print(f"fp16 GELU C: worst excess over one ulp {excess.max():.3e} at ref {rg.flat[excess.argmax()]:.4e}; "
+          f"equal to the nearest fp16 {np.mean(got16 == f16r(rg)):.4f}", flush=True)
+    assert excess.max() <= 3e-5, "fp16 C one rounding"
+    assert np.mean(got16 == f16r(rg)) >= 0.99
+    assert mean_rel(got16, rg) < 5e-4
+    # per-head epilogue over the fp16 product (the QKV shape)
+    w3, w3dev, s3dev = _library_weights(174, 3 * H * 64, Kd, w8)
+    (w316,) = K.weights_to_f16([w3dev])
+    b3 = O.randn(175, (3 * H * 64,), 0.02)
+    gq, gk = 1.0 + O.randn(176, (64,), 0.1), 1.0 + O.randn(177, (64,), 0.1)
+    outs = [torch.empty(B, H, S, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3)]
+    K.gemm_heads(ad, w3dev, dev(b3, torch.float32), S, H, outs, (dev(gq, torch.float32), dev(gk, torch.float32), None),
+                 w_scale=s3dev, round_product=True, w16=w316)
+    Q, Kh, V = O.split_qkv(f16r(O.linear(a, w3, b3)).reshape(B, S, 3 * H * 64), H, 64)
+    for got, r, what in zip(outs, (O.rms_norm(Q, gq), O.rms_norm(Kh, gk), V), "QKV"):
+        gh = host(got)
+        assert np.all(np.abs(gh - r) <= np.abs(r) * 2.0 ** -7 + 1e-3), what
+        assert mean_rel(gh, r) < 2e-3, what
+    # residual add + norm over the fp16 product, fp16 norm output
+    g2 = 1.0 + O.randn(178, (2048,), 0.1)
+    x = O.randn(179, (M, 2048))
+    xd = dev(x, torch.float32)
+    n = K.gemm_add_norm(ad, wdev, bd, xd, dev(g2, torch.float32), w_scale=sdev, norm_dtype=torch.float16,
+                        round_product=True, w16=w16)
+    x_ref = x + f16r(ref)
+    close(host(xd), x_ref, "residual (fp16 product)", rel=1e-5)
+    # where the two fp32 sums straddle an fp16 midpoint the products round
+    # to neighbours, moving the residual (and its normalised value) by one
+    # product ulp: a bf16-bar check on the fp16 output, and nearly all of it
+    # the oracle's own rounding
+    nr = O.rms_norm(x_ref, g2)
+    gn = host(n)
+    close(gn, nr, "norm (fp16 product, fp16 out)", rel=5e-4)
+    assert np.mean(gn == f16r(nr)) >= 0.99
+
+
+def test_gemm_fp16_library_path_needs_the_copy():
+    """w16_f16 set without the copy itself is an argument error on the
+    library path (the copy is what hipBLASLt reads)."""
+    import ctypes
+    M, Kd = 1072, 256
+    a = torch.zeros(M, Kd, dtype=torch.float16, device=DEV)
+    w = torch.zeros(64, Kd, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty(M, 64, dtype=torch.float32, device=DEV)
+    d = K._desc(a, w, None, abi.SF_ACT_NONE, None)
+    d.w16_f16 = 1
+    d.epilogue = abi.SF_EPI_PLAIN
+    d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), abi.SF_F32
+    ws = torch.empty(max(abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d)), 16), dtype=torch.uint8, device=DEV)
+    d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
+    assert abi.lib().sf_gemm(ctypes.byref(d), torch.cuda.current_stream().cuda_stream) == abi.SF_EINVAL
+
+
 def test_absmax_bf16_batched_matches_torch():
     """One launch over buffers of different lengths (a ragged tail, an
     empty one, a NaN, an inf) gives each its own max |x|, merged into an

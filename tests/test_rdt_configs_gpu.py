@@ -71,6 +71,53 @@ def test_block_vs_fp32_oracle(blk):
 
 # ---- batch 16 and int8 batch 32: the library-path regime ----------------------
 
+@pytest.mark.parametrize("batch,int8,blk", [(16, 0, 0), (16, 0, 1), (32, 1, 0), (32, 1, 1)],
+                         ids=["b16-language", "b16-image", "int8_b32-language", "int8_b32-image"])
+def test_block_vs_fp32_oracle_large_batch(batch, int8, blk):
+    """RDTBlock::forward (dit_block.cu:349-387) at batch 16 (bf16 weights)
+    and batch 32 (int8 weights): 1072 / 2144 rows per projection, the
+    library-path GEMMs.  The fp32 residual after one full-width block is
+    held to the north-star bar against the pure-fp32 oracle (rb=False):
+    max-abs <= 2e-2 and mean-rel <= 1e-3.  Block 0 attends to language keys
+    with ragged valid lengths, block 1 to image keys (reduced condition
+    lengths: the precision question sits in the storage points of the
+    1072 / 2144-row projections, not in the key count).
+
+    Above 160 rows the runtime multiplies fp16 activations by fp16 copies
+    of the weights and keeps the products in fp16 (the oracle's CPU model
+    of that storage put the block at 5.6-7.9e-4 from fp32; with the bf16
+    inputs and bf16 products used before, 1.6-1.8e-3).  The GPU is also held
+    to the oracle with the same storage points (rb_of) at the same bar."""
+    print(f"block {blk} batch {batch} int8 {int8} vs fp32 oracle", flush=True)
+    c = small_cfg(layers=2, batch=batch, int8_weights=int8)
+    m = build(c)
+    lang_len = np.random.default_rng(batch + blk).integers(8, c.lang_max + 1, size=batch).astype(np.int32)
+    lang, ll, img, state = make_condition(c, lang_len=lang_len)
+    set_cond(m, lang, ll, img, state)
+    S = c.horizon + 3
+    x = O.randn(177 + blk, (batch, S, c.hidden))
+    xd = torch.from_numpy(x).to(DEV)
+    m.run_blocks(xd, first=blk, count=1)
+    got = xd.cpu().numpy()
+    p = m.state_dict()
+    m.close()
+    oc = oracle_cfg(c)
+    cond32 = OR.condition_tokens(p, lang, img, oc, rb=False)[blk]
+    ck, cv = OR.cross_kv(p, blk, cond32, oc, rb=False)
+    ref32 = OR.rdt_block(p, blk, x, ck, cv, ll if blk == 0 else None, oc, rb=False)
+    condb = OR.condition_tokens(p, lang, img, oc, rb=rb_of(c))[blk]
+    ckb, cvb = OR.cross_kv(p, blk, condb, oc, rb=rb_of(c))
+    refb = OR.rdt_block(p, blk, x, ckb, cvb, ll if blk == 0 else None, oc, rb=rb_of(c))
+    mx, mr = float(np.abs(got - ref32).max()), mean_rel(got, ref32)
+    mr_model, mr_b = mean_rel(refb, ref32), mean_rel(got, refb)
+    print(f"block {blk} B={batch} int8={int8}: vs fp32 max-abs {mx:.3e} mean-rel {mr:.3e}; "
+          f"storage model vs fp32 {mr_model:.3e}; GPU vs storage model {mr_b:.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert mx <= 2e-2
+    assert mr <= 1e-3
+    assert mr_b <= 1e-3
+
+
 @pytest.mark.parametrize("batch,int8", [(16, 0), (32, 1)], ids=["b16", "int8_b32"])
 def test_denoise_step_large_batch(batch, int8):
     """Config 4 at batch 16 and config 5 (int8 weights) at batch 32: every
@@ -149,11 +196,11 @@ def test_run_blocks_int8_large_batch_block_range():
     ref, floor = oracle_noise_floor(stack)
     mx, mr, scale = float(np.abs(got - ref).max()), mean_rel(got, ref), max(1.0, float(np.abs(ref).max()))
     print(f"int8 b32 blocks 1..2: max-abs {mx:.3e} (|ref| <= {scale:.2f}) mean-rel {mr:.3e} floor {floor:.3e}")
-    # 4.4M residual elements of magnitude up to ~5: the largest difference
-    # is a bf16 rounding flip on a large value, so the bound scales with it;
-    # another block's weights would put mean-rel near 1
+    # measured max-abs 2.8e-3 on 4.4M residual elements up to ~6.5 in
+    # magnitude, mean-rel 1.09x the floor: 2x margins (another block's
+    # weights would put mean-rel near 1)
     assert np.isfinite(got).all()
-    assert mx <= 2e-2 * scale and mr <= 4 * floor
+    assert mx <= 6e-3 and mr <= 2 * floor
 
 
 @pytest.mark.parametrize("int8", [0, 1])
@@ -222,9 +269,9 @@ def test_full_depth_batch16_slots_match_batch1():
     """28 layers, full condition lengths, 5-step graph loop at batch 16:
     slots 0, 7 and 15 against batch-1 models given the same slot's
     condition and noise.  The two runs take different GEMM paths (hipBLASLt
-    at M = 1072 vs split-K at M = 67) and attention split counts, so they
-    differ by summation order only: mean-rel <= 2e-2 on the final action
-    after 28 x 5 block applications (measured value printed)."""
+    in fp16 at M = 1072 vs split-K at M = 67) and storage types, so they
+    differ by rounding: measured 1.4-1.6e-3 mean-rel on the action update
+    after 28 x 5 block applications, bound 3e-3 (about 2x)."""
     print("full depth batch 16 vs batch 1", flush=True)
     c16 = R.default_config(batch=16)
     c1 = R.default_config(batch=1)
@@ -247,7 +294,34 @@ def test_full_depth_batch16_slots_match_batch1():
         mr = mean_rel(a16[b:b + 1] - x0[b:b + 1], a1 - x0[b:b + 1])
         print(f"slot {b}: mean-rel of the action update {mr:.3e}, max-abs {np.abs(a16[b:b + 1] - a1).max():.3e}")
         assert np.isfinite(a1).all()
-        assert mr <= 2e-2, (b, mr)
+        assert mr <= 3e-3, (b, mr)
+
+
+def test_full_size_int8_batch32_graph_loop():
+    """Config 5 at full size: 28 layers, hidden 2048, int8 weights, batch
+    32, full condition lengths (ragged language rows, 4374 image keys), the
+    5-step loop.  Properties that do not need the oracle at this size: the
+    graph replays equal the eager loop bit for bit (twice), every action
+    stays finite, and each batch slot moved from its noise."""
+    print("full-size int8 batch 32 loop", flush=True)
+    c = R.default_config(batch=32, int8_weights=1)
+    m = build(c)
+    lang_len = np.random.default_rng(32).integers(32, c.lang_max + 1, size=32).astype(np.int32)
+    lang, ll, img, state = make_condition(c, lang_len=lang_len)
+    set_cond(m, lang, ll, img, state)
+    del lang, img
+    x0 = O.randn(23, (32, c.horizon, c.action_dim))
+    xe = torch.from_numpy(x0).to(DEV)
+    m.sample(xe, use_graph=False)
+    eager = xe.cpu().numpy()
+    assert np.isfinite(eager).all()
+    moved = np.abs(eager - x0).reshape(32, -1).max(axis=1)
+    assert (moved > 0).all(), moved
+    for rep in range(2):
+        xg = torch.from_numpy(x0).to(DEV)
+        m.sample(xg, use_graph=True)
+        assert np.array_equal(xg.cpu().numpy(), eager), rep
+    print(f"int8 b32 full size: finite, graph == eager, min per-slot move {moved.min():.3e}", flush=True)
 
 
 # ---- V beyond the fp16 range: the layer switches to the exact P.V form --------

@@ -26,7 +26,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import assert_close_bf16, mean_rel
+from _util import assert_close_bf16, cosine, mean_rel
 from oracle import oracle as O
 from oracle import rdt as OR
 from servoflow_amd import abi
@@ -55,12 +55,13 @@ def bf(x):
 
 
 def rb_of(c):
-    """The oracle's storage model of the runtime at config c: bf16
-    everywhere, except at batch * 67 <= 160 rows the FFN inputs (norm3
-    output, GELU hidden), which the runtime stores in fp16; above 160 rows
-    also the block projections' outputs (the library path's bf16 product)."""
-    rows = c.batch * (c.horizon + 3)
-    return OR.storage_points(rows <= 160, gemm16=rows > 160)
+    """The oracle's storage model of the runtime at config c
+    (OR.runtime_points): at batch * 67 <= 160 rows bf16 everywhere except
+    the FFN inputs (norm3 output, GELU hidden) in fp16, products in fp32;
+    above 160 rows every projection input, the products and the
+    self-attention's q / k / v in fp16, the cross-attention's q and the K/V
+    cache in bf16."""
+    return OR.runtime_points(c.batch * (c.horizon + 3))
 
 
 def make_condition(c, seed=5, lang_len=None):
@@ -172,7 +173,11 @@ def test_denoise_step_matches_oracle(int8):
     assert_within_floor(got, ref, floor, f"denoise step int8={int8}")
     ref32 = OR.denoise_step(p, x_t, 1.0, state, OR.encode_caches(p, lang, img, oc, rb=False), ll, oc,
                             rb=False)
-    assert mean_rel(got, ref32) < 2e-2
+    mr32 = mean_rel(got, ref32)
+    print(f"denoise step int8={int8} vs fp32: mean-rel {mr32:.3e}", flush=True)
+    # measured 3.37e-3 (bf16) / 3.35e-3 (int8): two blocks of 16-bit storage
+    # at batch 2, velocity after the final layer; 1.5x margin
+    assert mr32 < 5e-3
 
 
 def test_sample_graph_equals_eager_and_oracle():
@@ -432,8 +437,12 @@ def test_full_rdt1b_denoise_step_matches_oracle():
     assert_within_floor(got, ref, floor, "full-size denoise step")
     del caches
     ref32 = OR.denoise_step(p, x_t, 0.8, state, OR.encode_caches(p, lang, img, oc, rb=False), ll, oc, rb=False)
-    print(f"full-size step vs fp32: mean-rel {mean_rel(got, ref32):.3e}", flush=True)
-    assert mean_rel(got, ref32) < 2e-2
+    mr32, mx32, cos32 = mean_rel(got, ref32), float(np.abs(got - ref32).max()), cosine(got, ref32)
+    print(f"full-size step vs fp32: mean-rel {mr32:.3e} max-abs {mx32:.3e} cos {cos32:.7f}", flush=True)
+    # the reference's end-to-end check on this output: max-abs < 0.05 and
+    # cos > 0.9999 (tests/alignment/test_rdt1b_alignment.py:426)
+    assert mx32 < 0.05 and cos32 > 0.9999
+    assert mr32 < 5e-3   # measured 3.31e-3 (28 blocks of 16-bit storage): 1.5x margin
 
 
 def _hf_checkpoint(model, path, int8_as_fp32=False):
