@@ -232,16 +232,17 @@ GEMM_SHAPES = (
 )
 
 
-def make_model(B, int8=False, seed=1234):
+def make_model(B, int8=False, seed=1234, mlp_ratio=1, lens_out=None):
     """RDT-1B (28 layers) with random weights and a synthetic condition:
     language N(0,1) with valid lengths ~ U{32..1024}, image N(0,1) 4374 tokens,
-    state token N(0,1).  Returns (model, encode_ms)."""
+    state token N(0,1).  Returns (model, encode_ms); lens_out (a list)
+    receives the drawn language lengths."""
     import numpy as np
     import torch
 
     from servoflow_amd import rdt as R
 
-    cfg = R.default_config(batch=B, int8_weights=1 if int8 else 0)
+    cfg = R.default_config(batch=B, int8_weights=1 if int8 else 0, mlp_ratio=mlp_ratio)
     m = R.RdtModel(cfg)
     m.init_random(seed, 0.02)
     dev = torch.device("cuda:0")
@@ -252,6 +253,8 @@ def make_model(B, int8=False, seed=1234):
     state = torch.randn(B, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
     rng = np.random.default_rng(seed + B)
     lens = rng.integers(32, 1025, size=B).astype(np.int32)
+    if lens_out is not None:
+        lens_out.extend(int(x) for x in lens)
     ll = torch.from_numpy(lens).to(dev)
     if B == 1:   # the caller's language tensor holds L = lens[0] rows (the reference's [1, L, 4096])
         m.set_lang_rows(int(lens[0]))
@@ -359,9 +362,39 @@ def bench_blocks(m, steps):
     return start.elapsed_time(stop) / steps
 
 
-def cpu_baseline(budget_s=25.0):
+def gemm_picks(B, int8):
+    """Which hipBLASLt algorithm the model's block projections run at batch
+    B (sf_gemm_algo_pick; call after make_model, which prepares every
+    shape): the QKV product (fp16 rows + bias), a 2048-wide projection into
+    the residual add + norm (fp16 product) and fc1 (fp16 C with GELU +
+    bias).  Each: index in hipBLASLt's heuristic list / candidates, and
+    whether it was timed."""
+    import ctypes
+
+    from servoflow_amd import abi
+
+    M = 67 * B
+    res = {}
+    for name, N, addnorm, act in (("qkv", 6144, False, abi.SF_ACT_NONE), ("proj", 2048, True, abi.SF_ACT_NONE),
+                                  ("fc1", 2048, False, abi.SF_ACT_GELU_TANH)):
+        d = abi.GemmDesc()
+        d.M, d.N, d.K, d.lda, d.ldw = M, N, 2048, 2048, 2048
+        d.a_dtype, d.w_dtype, d.w16_f16 = abi.SF_F16, abi.SF_I8 if int8 else abi.SF_BF16, 1
+        d.bias, d.act = 256, act   # any non-null bias: the kind, not the data, is looked up
+        if addnorm:
+            d.epilogue, d.round_product, d.c_dtype, d.ldc = abi.SF_EPI_ADD_NORM, 1, abi.SF_F32, N
+        else:
+            d.epilogue, d.c_dtype, d.ldc = abi.SF_EPI_PLAIN, abi.SF_F16, N
+        pick, ncand, timed = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        st = abi.lib().sf_gemm_algo_pick(ctypes.byref(d), ctypes.byref(pick), ctypes.byref(ncand), ctypes.byref(timed))
+        res[name] = f"{pick.value}/{ncand.value} {'timed' if timed.value else 'heuristic'}" if st == 0 else "n/a"
+    return res
+
+
+def cpu_baseline(budget_s=25.0, lang_len=517):
     """The oracle's fp32 RDT-1B denoise step (28 layers, batch 1, image keys
-    4374, language 1024 padded keys with a valid length) on the host cores.
+    4374, language 1024 padded keys with valid length lang_len -- the
+    headline's drawn L) on the host cores.
     Weights are N(0, 0.02); one layer's weights are shared by all 28 layers
     (the timing does not depend on the values) and the condition caches are
     random.  One step is timed and scaled by 5 to the loop."""
@@ -412,7 +445,7 @@ def cpu_baseline(budget_s=25.0):
     caches = [(lang_k, lang_k) if i % 2 == 0 else (img_k, img_k) for i in range(c.layers)]
     state = O.randn(903, (1, D))
     x_t = O.randn(904, (1, c.horizon, c.action_dim))
-    ll = np.array([517], np.int32)
+    ll = np.array([lang_len], np.int32)
     times = []
     t_end = time.perf_counter() + budget_s
     while not times or (time.perf_counter() < t_end and len(times) < 3):
@@ -429,7 +462,7 @@ def cpu_baseline(budget_s=25.0):
         "host_cpus": os.cpu_count(),
         "kind": "port",
         "sample": f"{len(times)} timed fp32 oracle denoise step(s) (28 layers, batch 1, lang 1024 "
-                  f"keys with valid length 517, image 4374 keys), median {step_s * 1e3:.0f} ms, x5 steps",
+                  f"keys with valid length {lang_len}, image 4374 keys), median {step_s * 1e3:.0f} ms, x5 steps",
     }
 
 
@@ -534,7 +567,9 @@ def main():
         return
     extra = {}
     # ---- headline: batch-1 loop (config 4)
-    m1, enc1 = make_model(1)
+    lens1 = []
+    m1, enc1 = make_model(1, lens_out=lens1)
+    L1 = lens1[0]
     loop1 = bench_loop(m1, args.steps, args.warmup)
     extra["encode_condition_b1_ms"] = round(enc1, 3)
     if not args.quick:
@@ -594,14 +629,22 @@ def main():
             if M <= 160:   # weight streaming: the HBM rate is the bound that matters
                 extra[f"gemm_{name}_GBps"] = round(r["GBps"], 1)
                 extra[f"gemm_{name}_hbm_frac"] = round(r["hbm_frac"], 4)
-        for B, int8, key in ((16, False, "loop_b16_ms"), (32, True, "loop_int8_b32_ms")):
+        for B, int8, key in ((16, False, "loop_b16_ms"), (32, True, "loop_int8_b32_ms"),
+                             (32, False, "loop_b32_bf16_ms")):
             m, enc = make_model(B, int8=int8)
             extra[key] = round(bench_loop(m, max(3, args.steps // 10), 2), 3)
             extra[key.replace("loop", "encode")] = round(enc, 3)
+            extra[key.replace("loop", "gemm_picks").replace("_ms", "")] = gemm_picks(B, int8)
             m.close()
             del m
             torch.cuda.empty_cache()
-    cpu = None if args.no_cpu else cpu_baseline()
+        # config 3 as written: the 28-block stack with MLP 4x (2048 -> 8192 -> 2048)
+        m4, _ = make_model(1, mlp_ratio=4)
+        extra["block_stack_mlp4x_b1_ms"] = round(bench_blocks(m4, 5), 3)
+        m4.close()
+        del m4
+        torch.cuda.empty_cache()
+    cpu = None if args.no_cpu else cpu_baseline(lang_len=L1)
     if cpu is not None:
         extra.update(cpu_attention_ops())
     line = {
@@ -618,13 +661,14 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "config 4: RDT-1B denoise loop, 5 Euler steps, batch 1, 28 layers, "
-                               "hidden 2048, 32 heads, 67 tokens, language condition of L ~ "
-                               "U{32..1024} token rows (padded to 1024, only the L rows encoded "
-                               "and read) / image 4374 keys cached once, one hipGraph replay "
+                               "hidden 2048, 32 heads, 67 tokens, language condition of "
+                               f"L = {L1} token rows (drawn from U{{32..1024}} with a fixed seed; "
+                               "padded to 1024, only the L rows encoded and read) / image 4374 "
+                               "keys cached once, one hipGraph replay "
                                "per step, random-init weights; the once-per-inference condition "
                                "encode is not in value (extra.encode_condition_b1_ms; a whole "
                                "control step with a new camera frame, encode + loop + host copy: "
-                               "extra.infer_b1_new_frame_ms)"},
+                               "extra.infer_b1_new_frame_ms)", "lang_rows": L1},
         "roofline": {
             "bound": "hbm",
             "achieved": round(img1["GBps"], 1),

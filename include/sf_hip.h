@@ -349,6 +349,16 @@ int sf_gemm_prepare(const sf_gemm_desc* desc);
  * (cuda_backend.cu:414-447).  SF_EINVAL for other values. */
 int sf_gemm_set_algo_timing(int32_t timed);
 
+/* Which hipBLASLt algorithm the library path runs for this call's shape and
+ * kind (M > 160; the first chunk of <= 8192 rows): *pick = its index in
+ * hipBLASLt's heuristic list (0 = the heuristic's first choice),
+ * *candidates = the usable candidates, *timed = 1 when the pick came from
+ * timing them (sf_gemm_prepare with timing on), 0 otherwise.  SF_ENOTSUP
+ * (pick -1) for a shape that is not on the library path or has not been
+ * set up yet (sf_gemm_prepare or a first call).  No counterpart in the
+ * reference: a record of what ran, for reproducibility reports. */
+int sf_gemm_algo_pick(const sf_gemm_desc* desc, int32_t* pick, int32_t* candidates, int32_t* timed);
+
 /* ---------------------------------------------------------------------------
  * Normalisation and dequant.
  * ------------------------------------------------------------------------- */

@@ -160,6 +160,9 @@ def lib() -> ctypes.CDLL:
     L.sf_gemm_workspace_bytes.restype = ctypes.c_size_t
     L.sf_gemm_prepare.argtypes = [ctypes.POINTER(GemmDesc)]
     L.sf_gemm_prepare.restype = ctypes.c_int
+    L.sf_gemm_algo_pick.argtypes = [ctypes.POINTER(GemmDesc), ctypes.POINTER(ctypes.c_int32),
+                                    ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]
+    L.sf_gemm_algo_pick.restype = ctypes.c_int
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     L.sf_rmsnorm.argtypes = [vp, i32, i64, vp, vp, i32, i64, i32, i32, ctypes.c_float, vp]
     L.sf_rmsnorm.restype = ctypes.c_int

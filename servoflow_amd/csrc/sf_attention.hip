@@ -1594,8 +1594,9 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     } else if (short_keys) {
         const int qb = (d->Sq + 15) / 16;
         const int kb = ((d->Sk + 31) / 32) * 2;
-        // one wave per query block while B*H*blocks leaves CUs idle; five
-        // per workgroup once B*H alone fills the chip (up to the bound)
+        // one wave per query block while B*H < 256 leaves CUs idle; from
+        // B*H >= 256 (every batch size) a head's query blocks are the five
+        // waves of one workgroup sharing K and V in LDS
         const long bh = (long)d->B * d->H;
         const bool grouped = bh >= sfk::kShortGroupMinHeads;
         if (grouped)

@@ -32,11 +32,17 @@
 //   a fixed order (deterministic) and applies the epilogue, including the
 //   residual add + RMSNorm that follows a block branch.
 //   library path (M > 160, caller workspace): at those sizes the product is
-//   MFMA-bound, a plain library GEMM: hipBLASLt computes the fp32 product
-//   chunk by chunk (<= 8192 rows) into the workspace and the same reduce
-//   kernels apply the epilogue.  int8 weights are first widened to bf16
-//   (exactly, without the scale) in the workspace, so the row scale is
-//   applied in the epilogue as in the other paths.
+//   MFMA-bound, a plain library GEMM: hipBLASLt computes it chunk by chunk
+//   (<= 8192 rows) and the same epilogue kernels finish it.  What hipBLASLt
+//   stores depends on the call: a 16-bit C with its BIAS / GELU_BIAS
+//   epilogue written directly; a 16-bit product (bias and int8 row scale
+//   applied by hipBLASLt, the scale as its alpha vector) that the per-head
+//   norm or the residual add + RMSNorm reads (round_product); otherwise the
+//   fp32 product.  Operands are bf16, or -- with fp16 activations and the
+//   caller's fp16 copy of the weights (w16_f16; int8 codes widened exactly,
+//   bf16 weights rounded, sf_weights_to_f16, once per model pass) -- fp16,
+//   and then the 16-bit outputs are fp16.  int8 weights without a copy are
+//   widened to bf16 codes in the workspace on every call.
 //   single-pass path (no workspace): one workgroup of 8 waves per 16 or 64
 //   weight rows over all of K, reduced in LDS, epilogue in place.
 #include <hip/hip_runtime.h>
@@ -1028,6 +1034,9 @@ struct LtShape {
     hipblasLtMatmulAlgo_t algo{};
     LtKind kind;
     bool ok = false;
+    int pick = -1;    // index of the algorithm in hipBLASLt's heuristic list (0: its first choice)
+    int ncand = 0;    // usable candidates the heuristic returned
+    bool timed = false;   // chosen by timing the candidates
 };
 
 std::mutex g_lt_mu;
@@ -1193,8 +1202,13 @@ int lt_lookup(int N, int K, int rows, int64_t lda, int64_t ldw, const LtKind& ki
     if (ok && tune && g_lt_timed.load() && nres > 1) {
         const int best = lt_pick_fastest(*h, sh, res, nres, N, K, rows, lda, ldw);
         if (best >= 0) pick = best;
+        sh.timed = true;
     }
-    if (ok) sh.algo = res[pick].algo;
+    if (ok) {
+        sh.algo = res[pick].algo;
+        sh.pick = pick;
+        sh.ncand = nres;
+    }
     sh.ok = ok;
     std::lock_guard<std::mutex> lock(g_lt_mu);
     // a shape another thread created meanwhile wins; this one is dropped
@@ -1456,6 +1470,26 @@ extern "C" int sf_heads_bf16(const sf_gemm_desc* d, const void* P, int64_t ldp, 
     hipStream_t s = static_cast<hipStream_t>(stream);
     sfk::launch_reduce<1>(d, e, s);
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+}
+
+extern "C" int sf_gemm_algo_pick(const sf_gemm_desc* d, int32_t* pick, int32_t* candidates, int32_t* timed) {
+    if (!d || !pick) return SF_EINVAL;
+    *pick = -1;
+    if (candidates) *candidates = 0;
+    if (timed) *timed = 0;
+    const LibPlan lp = plan_library(d->M, d->N, d->K, d->w_dtype == SF_I8, d->a_dtype != SF_BF16 && !lib_f16(d));
+    if (!lp.ok) return SF_ENOTSUP;   // not a library-path shape
+    const LtKind kind = lib_kind(d);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return SF_EDEVICE;
+    const int64_t ldw = (d->w_dtype == SF_I8 || lib_f16(d)) ? d->K : d->ldw;
+    std::lock_guard<std::mutex> lock(g_lt_mu);
+    auto it = g_lt_shapes.find(std::make_tuple(dev, d->N, d->K, lp.chunk, lib_lda(d), ldw, kind.ldd, kind.bits()));
+    if (it == g_lt_shapes.end() || !it->second.ok) return SF_ENOTSUP;   // not prepared (or no algorithm)
+    *pick = it->second.pick;
+    if (candidates) *candidates = it->second.ncand;
+    if (timed) *timed = it->second.timed ? 1 : 0;
+    return SF_OK;
 }
 
 extern "C" int sf_gemm_set_algo_timing(int32_t timed) {

@@ -9,6 +9,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 
@@ -84,7 +87,114 @@ void check_status(int st) {
     throw std::runtime_error(msg);
 }
 
-// Fills the mask fields of the descriptor from the reference's mask forms.
+float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const int e = (h >> 10) & 31;
+    uint32_t m = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {   // subnormal: normalise
+            int ee = -1;
+            do {
+                ++ee;
+                m <<= 1;
+            } while (!(m & 0x400u));
+            bits = sign | ((uint32_t)(127 - 15 - ee) << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else {
+        bits = sign | ((uint32_t)(e - 15 + 127) << 23) | (m << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+}  // namespace
+
+// An additive mask [B,1,1,Sk] or [B,1,Sq,Sk] as the key-padding form the
+// kernels apply.  softmax(s + m) over a row equals softmax(s) over the keys
+// whose m equals the row's maximum M whenever every other key has
+// m <= M - 5000: those keys' weights exp(s_k + m_k - max) underflow to
+// exactly 0 in fp32 (while the raw scores of the row span less than ~4800;
+// -1e4 -- -9984 in bf16 --, -1e9 and -inf all qualify), and the common
+// offset M of the kept keys cancels.  So per batch element every row must
+// be the same and hold only M and values <= M - 5000; a row that is all
+// one value keeps every key, as the additive form does.  Anything else (a
+// bias between -5000 and the maximum, NaN,
+// rows that differ per query) has no key-padding equivalent:
+// std::invalid_argument.  The mask is read on the host: not allowed while
+// the stream is being captured.
+std::vector<uint8_t> RocmBackend::additive_to_keep(const TensorRef& m, int64_t B, int64_t Sq, int64_t Sk,
+                                                   StreamHandle stream) {
+    const bool key_only = m.ndim() == 4 && m.shape[0] == B && m.shape[1] == 1 && m.shape[2] == 1 && m.shape[3] == Sk;
+    const bool per_query = m.ndim() == 4 && m.shape[0] == B && m.shape[1] == 1 && m.shape[2] == Sq && m.shape[3] == Sk;
+    if (!key_only && !per_query) bad("an additive mask must be [B,1,1,Sk] or [B,1,S,Sk]");
+    const int64_t es = (int64_t)dtype_size(m.dtype);
+    if (m.strides.size() != 4 || m.strides[3] != es) bad("an additive mask must be contiguous along Sk");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess)
+        throw std::runtime_error("RocmBackend::attention: hipStreamIsCapturing failed");
+    if (cs != hipStreamCaptureStatusNone)
+        bad("an additive float mask is read on the host and cannot be used inside graph capture; "
+            "pass its Bool key-padding form instead");
+    const int64_t rows = key_only ? 1 : Sq;
+    std::vector<char> host((size_t)(Sk * es));
+    std::vector<float> row((size_t)Sk);
+    std::vector<uint8_t> keep((size_t)(B * ((Sk + 3) & ~int64_t(3))), 0);
+    const int64_t ld = (Sk + 3) & ~int64_t(3);
+    for (int64_t b = 0; b < B; ++b) {
+        std::vector<float> first;
+        for (int64_t r = 0; r < rows; ++r) {
+            const char* src = static_cast<const char*>(m.data) + b * m.strides[0] + r * m.strides[2];
+            if (hipMemcpyAsync(host.data(), src, host.size(), hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess)
+                throw std::runtime_error("RocmBackend::attention: reading the mask failed");
+            for (int64_t k = 0; k < Sk; ++k) {
+                float v;
+                if (m.dtype == DType::Float32) {
+                    std::memcpy(&v, host.data() + 4 * k, 4);
+                } else {
+                    uint16_t h;
+                    std::memcpy(&h, host.data() + 2 * k, 2);
+                    if (m.dtype == DType::BFloat16) {
+                        const uint32_t bits = (uint32_t)h << 16;
+                        std::memcpy(&v, &bits, 4);
+                    } else {
+                        v = half_to_float(h);
+                    }
+                }
+                if (std::isnan(v) || v == INFINITY) bad("an additive mask holds NaN or +inf");
+                row[(size_t)k] = v;
+            }
+            if (r == 0) {
+                first = row;
+            } else if (row != first) {
+                bad("an additive mask that differs between query rows has no key-padding form");
+            }
+        }
+        float mx = -INFINITY;
+        for (float v : first) mx = std::max(mx, v);
+        for (int64_t k = 0; k < Sk; ++k) {
+            const float v = first[(size_t)k];
+            if (v == mx) {
+                keep[(size_t)(b * ld + k)] = 1;
+            } else if (!(v <= mx - 5000.f)) {
+                bad("an additive mask entry is neither the row's maximum nor 5000 or more below it");
+            }
+        }
+    }
+    return keep;
+}
+
+namespace {
+
+// Fills the mask fields of the descriptor from the reference's mask forms
+// (an additive float mask arrives here already as its key-padding form).
 void apply_mask(const TensorRef& m, int64_t B, int64_t Sk, sf_attn_desc& d) {
     if (!m.on_device) bad("mask must be on the device");
     if (m.dtype == DType::Int32) {
@@ -105,22 +215,26 @@ void apply_mask(const TensorRef& m, int64_t B, int64_t Sk, sf_attn_desc& d) {
         d.kv_mask_stride = m.strides[0];
         return;
     }
-    bad("unsupported mask: additive float masks are not implemented (use a Bool key-padding mask)");
+    bad("unsupported mask dtype (Int32 lengths, Bool / Int8 key padding, or an additive float mask)");
 }
 
 }  // namespace
 
 RocmBackend::~RocmBackend() {
-    for (auto& kv : ws_)
+    for (auto& kv : ws_) {
         if (kv.second.ptr) (void)hipFree(kv.second.ptr);
+        if (kv.second.mask) (void)hipFree(kv.second.mask);
+    }
 }
 
 size_t RocmBackend::attention_workspace_bytes(const TensorRef& Q, const TensorRef& K) {
-    if (Q.ndim() != 4 || K.ndim() != 4) return 0;
+    if (Q.ndim() != 4 || K.ndim() != 4 || sf_type(Q.dtype) < 0) return 0;
     sf_attn_desc d;
-    // the partials' size does not depend on the element type
+    // the split count (and with it the partials' size) depends on the
+    // element type: Float32 takes key splits where 16-bit types run one
+    // workgroup per query block
     sf_attn_desc_init_bhsd(&d, (int32_t)Q.shape[0], (int32_t)Q.shape[1], (int32_t)Q.shape[2],
-                           (int32_t)K.shape[2], (int32_t)Q.shape[3], SF_BF16, SF_BF16);
+                           (int32_t)K.shape[2], (int32_t)Q.shape[3], sf_type(Q.dtype), sf_type(Q.dtype));
     return sf_attn_workspace_bytes(&d);
 }
 
@@ -178,10 +292,40 @@ void RocmBackend::attention(const TensorRef& Q, const TensorRef& K, const Tensor
     d.scale = scale;
     d.is_causal = is_causal ? 1 : 0;
     d.exact_pv = precision_ == AttentionPrecision::Exact ? 1 : 0;
-    if (mask) apply_mask(*mask, B, Sk, d);
+    const bool additive = mask && (mask->dtype == DType::Float32 || mask->dtype == DType::Float16 ||
+                                   mask->dtype == DType::BFloat16);
+    std::vector<uint8_t> keep;
+    if (additive) {
+        if (!mask->on_device) bad("mask must be on the device");
+        keep = additive_to_keep(*mask, B, S, Sk, stream);
+    } else if (mask) {
+        apply_mask(*mask, B, Sk, d);
+    }
 
     std::lock_guard<std::mutex> lock(mu_);
     Workspace& ws = ws_[stream];
+    if (additive) {   // the key-padding form goes to this stream's mask buffer
+        if (keep.size() > ws.mask_bytes) {
+            if (hipStreamSynchronize(static_cast<hipStream_t>(stream)) != hipSuccess)
+                throw std::runtime_error("RocmBackend: hipStreamSynchronize failed");
+            if (ws.mask) (void)hipFree(ws.mask);
+            ws.mask = nullptr;
+            ws.mask_bytes = 0;
+            if (hipMalloc(&ws.mask, keep.size()) != hipSuccess) {
+                ws.mask = nullptr;
+                throw std::runtime_error("RocmBackend: mask buffer allocation failed");
+            }
+            ws.mask_bytes = keep.size();
+        }
+        // synchronous: the host vector is gone when this call returns, and
+        // an earlier call on the stream may still read the buffer
+        if (hipMemcpyAsync(ws.mask, keep.data(), keep.size(), hipMemcpyHostToDevice,
+                           static_cast<hipStream_t>(stream)) != hipSuccess ||
+            hipStreamSynchronize(static_cast<hipStream_t>(stream)) != hipSuccess)
+            throw std::runtime_error("RocmBackend: uploading the key-padding mask failed");
+        d.kv_mask = static_cast<const uint8_t*>(ws.mask);
+        d.kv_mask_stride = (Sk + 3) & ~int64_t(3);
+    }
     grow(ws, sf_attn_workspace_bytes(&d), stream);
     check_status(sf_attn_fwd(&d, Q.data, K.data, V.data, out.data, ws.ptr, ws.bytes, stream));
 }

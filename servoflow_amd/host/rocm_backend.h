@@ -19,6 +19,16 @@
 //   Bool / Int8 [B, Sk] or [B,1,1,Sk] key-padding mask (nonzero = attend),
 //                                    contiguous along Sk, rows readable for
 //                                    Sk rounded up to 4 bytes
+//   Float32 / Float16 / BFloat16     the additive mask of backend.h:104,
+//     [B,1,1,Sk] or [B,1,S,Sk]       softmax(Q K^T * scale + mask): read on
+//                                    the host (synchronously; not inside a
+//                                    graph capture) and applied as its
+//                                    key-padding form -- per batch element
+//                                    every row the same, each entry either
+//                                    the row's maximum (kept) or at least
+//                                    5000 below it (-1e4, -inf: dropped,
+//                                    its weight underflows to 0); a row of
+//                                    one value keeps every key
 //   anything else                    std::invalid_argument
 //
 // Thread-compatible like the reference (backend.h:35-42): a stream must not
@@ -106,9 +116,15 @@ private:
     struct Workspace {
         void* ptr = nullptr;
         size_t bytes = 0;
+        void* mask = nullptr;   // key-padding form of an additive mask
+        size_t mask_bytes = 0;
     };
     // Grows ws to `bytes` outside capture; mu_ held.
     void grow(Workspace& ws, size_t bytes, StreamHandle stream);
+    // The key-padding form ([B][Sk rounded up to 4] bytes) of an additive
+    // mask; std::invalid_argument for one that has none.
+    static std::vector<uint8_t> additive_to_keep(const TensorRef& m, int64_t B, int64_t Sq, int64_t Sk,
+                                                 StreamHandle stream);
 
     AttentionPrecision precision_;
     std::mutex mu_;

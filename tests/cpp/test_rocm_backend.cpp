@@ -255,9 +255,9 @@ void test_errors_use_reference_exception_types() {
     qh.on_device = false;        // host tensor (cuda_backend.cu:156-161)
     expect_throw<std::invalid_argument>([&] { be.attention(qh, k.ref(), k.ref(), out); }, "host tensor");
     DevBuf fm((size_t)8 * 300 * 4);
-    TensorRef additive = TensorRef::contiguous(fm.p, DType::Float32, {1, 1, 8, 300});
+    TensorRef additive = TensorRef::contiguous(fm.p, DType::Float32, {1, 1, 8, 299});
     expect_throw<std::invalid_argument>([&] { be.attention(q.ref(), k.ref(), k.ref(), out, &additive); },
-                                        "additive float mask");
+                                        "additive float mask of the wrong shape");
     DevBuf bm((size_t)8 * 300);
     TensorRef per_query = TensorRef::contiguous(bm.p, DType::Bool, {1, 1, 8, 300});
     expect_throw<std::invalid_argument>([&] { be.attention(q.ref(), k.ref(), k.ref(), out, &per_query); },
@@ -481,6 +481,145 @@ void test_precision_option_and_large_v() {
         if (i % 64 != 5) CHECK(std::isfinite(gf[i]), "fast precision: other columns finite");
 }
 
+// Uploads a float host mask [rows][Sk] (rows = B or B*S) to the device.
+struct FloatMask {
+    DevBuf dev;
+    std::vector<int64_t> shape;
+    FloatMask(const std::vector<float>& h, std::vector<int64_t> shp) : dev(h.size() * 4), shape(shp) {
+        if (hipMemcpy(dev.p, h.data(), h.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            throw std::runtime_error("hipMemcpy");
+    }
+    TensorRef ref() const { return TensorRef::contiguous(dev.p, DType::Float32, shape); }
+};
+
+void test_additive_mask_forms() {
+    // the additive mask of backend.h:104 (softmax(Q K^T scale + mask)):
+    // 0 / -1e4 / -inf per key, a row offset by a constant, and a row that is
+    // all -1e4 (the additive form then keeps every key: the offset cancels)
+    const int B = 3, H = 4, S = 20, Sk = 300;
+    Bf16Tensor q(301, {B, H, S, 64}), k(302, {B, H, Sk, 64}), v(303, {B, H, Sk, 64});
+    std::vector<float> m((size_t)B * Sk);
+    std::vector<std::vector<uint8_t>> keep(B, std::vector<uint8_t>(Sk));
+    for (int j = 0; j < Sk; ++j) {
+        const bool k0 = (j * 7) % 5 != 0;
+        m[j] = k0 ? 0.f : (j % 2 ? -1e4f : -INFINITY);
+        keep[0][j] = k0;
+        const bool k1 = j < 123;
+        m[Sk + j] = k1 ? 2.5f : -2e4f;   // kept keys share an offset of 2.5
+        keep[1][j] = k1;
+        m[2 * Sk + j] = -1e4f;
+        keep[2][j] = 1;
+    }
+    const std::vector<float> ref = oracle_kept(q, k, v, keep);
+    RocmBackend be;
+    DevBuf ob((size_t)B * H * S * 64 * 4), ob2((size_t)B * H * S * 64 * 4);
+    TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {B, H, S, 64});
+    TensorRef out2 = TensorRef::contiguous(ob2.p, DType::Float32, {B, H, S, 64});
+    FloatMask key_only(m, {B, 1, 1, Sk});
+    TensorRef km = key_only.ref();
+    be.attention(q.ref(), k.ref(), v.ref(), out, &km);
+    HIP_OK(hipDeviceSynchronize());
+    const std::vector<float> got = download_f32(ob, ref.size());
+    expect_close(got, ref, "additive [B,1,1,Sk] vs oracle on the kept keys");
+    // the per-query form with identical rows: the same result bit for bit
+    std::vector<float> mq((size_t)B * S * Sk);
+    for (int b = 0; b < B; ++b)
+        for (int r = 0; r < S; ++r) std::memcpy(&mq[((size_t)b * S + r) * Sk], &m[(size_t)b * Sk], Sk * 4);
+    FloatMask per_query(mq, {B, 1, S, Sk});
+    TensorRef pq = per_query.ref();
+    be.attention(q.ref(), k.ref(), v.ref(), out2, &pq);
+    HIP_OK(hipDeviceSynchronize());
+    CHECK(std::memcmp(download_f32(ob2, ref.size()).data(), got.data(), got.size() * 4) == 0,
+          "additive [B,1,S,Sk] with equal rows == [B,1,1,Sk]");
+    // a bfloat16 mask of the same values
+    std::vector<uint16_t> mb(m.size());
+    for (size_t i = 0; i < m.size(); ++i) {
+        uint32_t u;
+        std::memcpy(&u, &m[i], 4);
+        mb[i] = (uint16_t)(u >> 16);   // 0, -9984 (-1e4 truncated), -2e4, 2.5, -inf: kept / >= 5000 below
+    }
+    DevBuf bm(mb.size() * 2);
+    HIP_OK(hipMemcpy(bm.p, mb.data(), mb.size() * 2, hipMemcpyHostToDevice));
+    TensorRef bmask = TensorRef::contiguous(bm.p, DType::BFloat16, {B, 1, 1, Sk});
+    be.attention(q.ref(), k.ref(), v.ref(), out2, &bmask);
+    HIP_OK(hipDeviceSynchronize());
+    CHECK(std::memcmp(download_f32(ob2, ref.size()).data(), got.data(), got.size() * 4) == 0,
+          "BFloat16 additive mask == Float32");
+    // no key-padding form: a bias between -5000 and the maximum, rows that
+    // differ per query, NaN
+    std::vector<float> bias = m;
+    bias[5] = -0.5f;
+    FloatMask fb(bias, {B, 1, 1, Sk});
+    TensorRef fbr = fb.ref();
+    expect_throw<std::invalid_argument>([&] { be.attention(q.ref(), k.ref(), v.ref(), out, &fbr); }, "-0.5 bias");
+    std::vector<float> mq2 = mq;
+    mq2[(size_t)(1 * S + 3) * Sk + 7] = -1e4f;
+    FloatMask fq(mq2, {B, 1, S, Sk});
+    TensorRef fqr = fq.ref();
+    expect_throw<std::invalid_argument>([&] { be.attention(q.ref(), k.ref(), v.ref(), out, &fqr); },
+                                        "rows differing per query");
+    std::vector<float> nan = m;
+    nan[9] = NAN;
+    FloatMask fn(nan, {B, 1, 1, Sk});
+    TensorRef fnr = fn.ref();
+    expect_throw<std::invalid_argument>([&] { be.attention(q.ref(), k.ref(), v.ref(), out, &fnr); }, "NaN entry");
+    // read on the host: refused inside a graph capture
+    hipStream_t st;
+    HIP_OK(hipStreamCreate(&st));
+    be.reserve_attention_workspace(RocmBackend::attention_workspace_bytes(q.ref(), k.ref()), st);
+    HIP_OK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    bool threw = false;
+    try {
+        be.attention(q.ref(), k.ref(), v.ref(), out, &km, 0.f, false, st);
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    hipGraph_t g0 = nullptr;
+    (void)hipStreamEndCapture(st, &g0);
+    if (g0) (void)hipGraphDestroy(g0);
+    (void)hipStreamDestroy(st);
+    CHECK(threw, "additive mask under capture must throw std::invalid_argument");
+}
+
+void test_fp32_reserve_then_capture() {
+    // the documented flow with no eager call first: reserve the size
+    // attention_workspace_bytes() gives for Float32 inputs whose 729 keys
+    // take key splits (16-bit inputs would run unsplit), then capture
+    const int B = 1, H = 32, S = 67, Sk = 729;
+    AnyTensor q(311, {B, H, S, 64}, DType::Float32), k(312, {B, H, Sk, 64}, DType::Float32),
+        v(313, {B, H, Sk, 64}, DType::Float32);
+    CHECK(RocmBackend::attention_workspace_bytes(q.ref(), k.ref()) > 0, "Float32 729 keys need partials");
+    DevBuf ob((size_t)B * H * S * 64 * 4), eb((size_t)B * H * S * 64 * 4);
+    TensorRef out = TensorRef::contiguous(ob.p, DType::Float32, {B, H, S, 64});
+    TensorRef eager = TensorRef::contiguous(eb.p, DType::Float32, {B, H, S, 64});
+    hipStream_t st;
+    HIP_OK(hipStreamCreate(&st));
+    RocmBackend be;
+    be.reserve_attention_workspace(RocmBackend::attention_workspace_bytes(q.ref(), k.ref()), st);
+    hipGraph_t g;
+    hipGraphExec_t ge;
+    HIP_OK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    be.attention(q.ref(), k.ref(), v.ref(), out, nullptr, 0.f, false, st);
+    HIP_OK(hipStreamEndCapture(st, &g));
+    HIP_OK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    be.attention(q.ref(), k.ref(), v.ref(), eager, nullptr, 0.f, false, st);
+    HIP_OK(hipStreamSynchronize(st));
+    const std::vector<float> ref = download_f32(eb, (size_t)B * H * S * 64);
+    for (int rep = 0; rep < 2; ++rep) {
+        HIP_OK(hipMemsetAsync(ob.p, 0xff, ob.n, st));   // NaN fill, outside the graph
+        HIP_OK(hipGraphLaunch(ge, st));
+        HIP_OK(hipStreamSynchronize(st));
+        CHECK(std::memcmp(download_f32(ob, ref.size()).data(), ref.data(), ref.size() * 4) == 0,
+              "Float32 graph replay == eager");
+    }
+    std::vector<float> oref(ref.size());
+    sfo_attention_f32(q.host.data(), k.host.data(), v.host.data(), oref.data(), B, H, S, Sk, 64, 0.f, 0, nullptr);
+    expect_close(ref, oref, "Float32 729 keys vs oracle");
+    (void)hipGraphExecDestroy(ge);
+    (void)hipGraphDestroy(g);
+    (void)hipStreamDestroy(st);
+}
+
 }  // namespace
 
 int main() {
@@ -501,6 +640,8 @@ int main() {
     run_case("float16_output", test_float16_output);
     run_case("streams_have_separate_workspaces", test_streams_have_separate_workspaces);
     run_case("precision_option_and_large_v", test_precision_option_and_large_v);
+    run_case("additive_mask_forms", test_additive_mask_forms);
+    run_case("fp32_reserve_then_capture", test_fp32_reserve_then_capture);
     if (g_failed) {
         std::printf("%d case(s) failed\n", g_failed);
         return 1;

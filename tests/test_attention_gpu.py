@@ -408,10 +408,10 @@ def test_long_keys_and_many_query_chunks(B, H, Sq, Sk):
                                                     (8, 32, 81, 100, True, "rand", torch.bfloat16),
                                                     (4, 64, 67, 67, False, "rand", torch.float16)])
 def test_short_keys_grouped_waves(B, H, Sq, Sk, causal, vl, dt):
-    """Short key sets at 256 <= B*H < 1024 run a head's query blocks as the
-    waves of one workgroup (B*H = 1024 one wave per workgroup again):
+    """Short key sets at B*H >= 256 (every batch size) run a head's query
+    blocks as the five waves of one workgroup sharing K and V in LDS:
     against the oracle, and bit-identical to the same heads run one batch
-    element at a time (one wave per workgroup)."""
+    element at a time (B*H < 256: one wave per workgroup)."""
     q, k, v = rounded(241, (B, H, Sq, 64)), rounded(242, (B, H, Sk, 64)), rounded(243, (B, H, Sk, 64))
     lens = None if vl is None else np.random.default_rng(244).integers(1, Sk + 1, size=B).astype(np.int32)
     kw = {"is_causal": causal}
@@ -427,6 +427,44 @@ def test_short_keys_grouped_waves(B, H, Sq, Sk, causal, vl, dt):
                         valid_len=None if lens is None else to_dev(lens[b:b + 1], torch.int32), **kw)
         torch.cuda.synchronize()
         assert np.array_equal(one.float().cpu().numpy()[0], got[b]), b
+
+
+def test_short_keys_grouped_large_bh_causal_ragged_mask():
+    """B*H = 1024 on the grouped five-wave workgroups with causal rows,
+    random valid lengths (zeros included) and a key-padding mask at once:
+    against an fp64 closed form (softmax over the allowed keys k <=
+    valid_len, mask[k], k <= q; zeros for a row with none), and
+    bit-identical to the same heads run one batch element at a time (one
+    wave per workgroup)."""
+    B, H, Sq, Sk = 32, 32, 67, 67
+    q, k, v = rounded(641, (B, H, Sq, 64)), rounded(642, (B, H, Sk, 64)), rounded(643, (B, H, Sk, 64))
+    rng = np.random.default_rng(644)
+    lens = rng.integers(0, Sk + 1, size=B).astype(np.int32)
+    lens[[3, 17]] = 0
+    mask = rng.random((B, Sk)) < 0.7
+    stride = (Sk + 3) // 4 * 4
+    md = torch.zeros(B, stride, dtype=torch.uint8, device=DEV)
+    md[:, :Sk] = torch.from_numpy(mask.astype(np.uint8)).to(DEV)
+    dq, dk, dv = (to_dev(x, torch.bfloat16) for x in (q, k, v))
+    full = attention(dq, dk, dv, out_dtype=torch.float32, is_causal=True, valid_len=to_dev(lens, torch.int32),
+                     kv_mask=md[:, :Sk])
+    torch.cuda.synchronize()
+    got = full.cpu().numpy()
+    allowed = mask[:, None, None, :] & (np.arange(Sk)[None, None, None, :] < lens[:, None, None, None]) & \
+        (np.arange(Sk)[None, None, None, :] <= np.arange(Sq)[None, None, :, None])
+    sc = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), k.astype(np.float64)) / 8.0
+    sc = np.where(allowed, sc, -np.inf)
+    mx = np.max(sc, axis=-1, keepdims=True)
+    p = np.where(allowed, np.exp(sc - np.where(np.isfinite(mx), mx, 0.0)), 0.0)
+    den = p.sum(-1, keepdims=True)
+    ref = np.einsum("bhqk,bhkd->bhqd", p / np.where(den > 0, den, 1.0), v.astype(np.float64))
+    assert_close_bf16(got, ref, "grouped B*H=1024 causal + valid lengths + key mask")
+    assert not got[3].any() and not got[17].any()
+    for b in range(B):
+        one = attention(dq[b:b + 1], dk[b:b + 1], dv[b:b + 1], out_dtype=torch.float32, is_causal=True,
+                        valid_len=to_dev(lens[b:b + 1], torch.int32), kv_mask=md[b:b + 1, :Sk])
+        torch.cuda.synchronize()
+        assert np.array_equal(one.cpu().numpy()[0], got[b]), b
 
 
 @pytest.mark.parametrize("B,H,Sq,Sk,causal,vl,dt,exact", [

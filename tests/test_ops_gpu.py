@@ -797,19 +797,36 @@ d.epilogue, d.C, d.ldc, d.c_dtype = abi.SF_EPI_PLAIN, out.data_ptr(), 1536, abi.
 ws = torch.empty(max(abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d)), 16), dtype=torch.uint8, device=dev)
 d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
 abi.check(abi.lib().sf_gemm_prepare(ctypes.byref(d)), "prepare")
+pick, ncand, timed = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+abi.check(abi.lib().sf_gemm_algo_pick(ctypes.byref(d), ctypes.byref(pick), ctypes.byref(ncand), ctypes.byref(timed)),
+          "pick")
+assert pick.value == 0 and timed.value == 0 and ncand.value >= 1, (pick.value, ncand.value, timed.value)
 abi.check(abi.lib().sf_gemm(ctypes.byref(d), torch.cuda.current_stream().cuda_stream), "gemm")
 torch.cuda.synchronize()
 ref = a.float() @ w.float().t() + b
 err = float((out - ref).abs().max())
 assert err < 1e-3, err
-print(hashlib.sha256(out.cpu().numpy().tobytes()).hexdigest())
+digest = hashlib.sha256(out.cpu().numpy().tobytes()).hexdigest()
+# with timing switched back on, a shape prepared afterwards is timed
+assert abi.lib().sf_gemm_set_algo_timing(1) == abi.SF_OK
+d2 = kernels._desc(a[:400], w, b, abi.SF_ACT_NONE, None)
+d2.epilogue, d2.C, d2.ldc, d2.c_dtype = abi.SF_EPI_PLAIN, out.data_ptr(), 1536, abi.SF_F32
+d2.workspace, d2.workspace_bytes = ws.data_ptr(), ws.numel()
+assert abi.lib().sf_gemm_algo_pick(ctypes.byref(d2), ctypes.byref(pick), None, None) == abi.SF_ENOTSUP
+abi.check(abi.lib().sf_gemm_prepare(ctypes.byref(d2)), "prepare 400")
+abi.check(abi.lib().sf_gemm_algo_pick(ctypes.byref(d2), ctypes.byref(pick), ctypes.byref(ncand), ctypes.byref(timed)),
+          "pick 400")
+assert timed.value == (1 if ncand.value > 1 else 0) and 0 <= pick.value < ncand.value, (pick.value, ncand.value)
+print(digest)
 """
 
 
 def test_gemm_heuristic_pick_is_reproducible_across_processes():
     """With sf_gemm_set_algo_timing(0) a library-path product (536 rows)
-    takes hipBLASLt's first heuristic candidate, so two processes produce
-    the same bits; each result also matches the fp32 product."""
+    takes hipBLASLt's first heuristic candidate (sf_gemm_algo_pick reports
+    index 0, not timed), so two processes produce the same bits; each
+    result also matches the fp32 product.  A shape prepared after timing is
+    switched back on reports a timed pick."""
     import os
     import subprocess
     import sys
