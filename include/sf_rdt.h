@@ -126,7 +126,18 @@ int sf_rdt_init_random(sf_rdt* m, uint64_t seed, float std, void* stream);
 int32_t sf_rdt_num_params(const sf_rdt* m);
 int sf_rdt_param_info(const sf_rdt* m, int32_t idx, const char** name, int32_t* dtype,
                       int32_t* ndim, int64_t shape[4]);
-void* sf_rdt_param_data(sf_rdt* m, int32_t idx);        /* device pointer */
+/* Device pointer to parameter idx.  Above 160 projection rows (batch * 67)
+ * the runtime multiplies fp16 copies of the block and final-layer weights;
+ * they are rebuilt before the first pass after this call, after
+ * sf_rdt_init_random / sf_rdt_load_safetensors, and after
+ * sf_rdt_params_changed -- a caller that writes through a pointer it
+ * obtained before a pass must call sf_rdt_params_changed before the next
+ * one. */
+void* sf_rdt_param_data(sf_rdt* m, int32_t idx);
+/* Parameters were written through pointers from sf_rdt_param_data: the
+ * weight copies are rebuilt (and sf_rdt_infer's cached condition
+ * re-encoded) before the next pass. */
+int sf_rdt_params_changed(sf_rdt* m);
 float* sf_rdt_param_scale(sf_rdt* m, int32_t idx);      /* int8 row scales or NULL */
 int32_t sf_rdt_find_param(const sf_rdt* m, const char* name);
 

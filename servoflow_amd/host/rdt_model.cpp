@@ -174,14 +174,19 @@ struct sf_rdt {
     // Above 160 rows (the library path): fp16 copies of every block's six
     // projection weights and of the final layer's two (int8 codes widened
     // exactly, bf16 weights rounded to fp16; sf_weights_to_f16, up to eight
-    // matrices per launch), refreshed at the start of each entry point's
-    // pass -- once per sampled loop, not once per block and step.
-    // codes16_of[param] is a weight's copy (fixed at creation).  The refresh
-    // runs inside the captured loop, so a replay after the weights change
-    // (they may be written through sf_rdt_param_data) uses the new values.
+    // matrices per launch), made before the first pass and again before
+    // the first pass after the parameters may have changed (w16_stale), on
+    // the pass's stream and outside any graph capture -- not once per loop:
+    // a batch-16 loop refreshing them in its graph took 0.8 ms more.
+    // codes16_of[param] is a weight's copy (fixed at creation).
     char* codes16 = nullptr;
     size_t codes16_bytes = 0;
     std::vector<const void*> codes16_of;
+    // The copies may no longer match the weights: set by every call that
+    // writes parameters or hands out a pointer to them (and by
+    // sf_rdt_params_changed), cleared by the refresh at the start of the
+    // next pass.
+    bool w16_stale = true;
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -221,7 +226,9 @@ void sf_rdt_set_error(sf_rdt* m, const std::string& msg) {
 }
 
 void sf_rdt_weights_changed(sf_rdt* m) {
-    if (m) m->infer_cond_valid = false;
+    if (!m) return;
+    m->infer_cond_valid = false;
+    m->w16_stale = true;
 }
 
 extern "C" const char* sf_rdt_last_error(const sf_rdt* m) { return m ? m->last_error.c_str() : ""; }
@@ -692,7 +699,8 @@ int widen_codes(sf_rdt* m, int first, int count, hipStream_t s, bool final_layer
 
 // RDTBlock::forward (dit_block.cu:349-387) on the fp32 residual m->x, with
 // m->n holding norm1(x) on entry; on exit m->n holds the next norm of x.
-// The block's int8 code copies (if any) are current (widen_codes).
+// The fp16 weight copies of the library path (if any) are current
+// (refresh_w16).
 int block_forward(sf_rdt* m, int i, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const LayerIdx& L = m->layers[i];
@@ -770,7 +778,7 @@ int timestep_index(const sf_rdt_config& c, float t) {
 // RDT1BModel::denoise_step up to the final layer: velocity rows [B*S, A].
 // t_emb_given: t's timestep token already embedded (the sampler's schedule),
 // else it is embedded here.
-int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s, bool widen = true,
+int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s,
                  const float* t_emb_given = nullptr) {
     const sf_rdt_config& c = m->cfg;
     const int D = c.hidden, T = c.horizon, A = c.action_dim, S = T + 3;
@@ -791,7 +799,6 @@ int step_forward(sf_rdt* m, const float* x_t, float t, hipStream_t s, bool widen
     SF_TRY(sf_assemble_tokens(m->x, t_emb, m->f_emb, m->state_tok, m->act_out, pf(m, m->xpos),
                               c.batch, T, D, s));
     SF_TRY(entry_norm(m, 0, s));
-    if (widen) SF_TRY(widen_codes(m, 0, c.layers, s, true));
     for (int i = 0; i < c.layers; ++i) SF_TRY(block_forward(m, i, s));
     // FinalLayer (dit_block.cu:407-412); m->n = norm_final(x) from the last block
     SF_TRY(linear(m, m->n, D, M, m->f1w, m->f1b, SF_ACT_GELU_TANH, m->h, D, m->ffn_dtype, false, s, m->act16));
@@ -812,9 +819,8 @@ std::vector<float> schedule(int num_steps) {
 int sample_body(sf_rdt* m, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const std::vector<float> ts = schedule(c.num_steps);
-    SF_TRY(widen_codes(m, 0, c.layers, s, true));   // once for every step of the loop
     for (int step = 0; step < c.num_steps; ++step) {
-        SF_TRY(step_forward(m, m->x_state, ts[step], s, false, m->t_emb_steps + (size_t)step * c.hidden));
+        SF_TRY(step_forward(m, m->x_state, ts[step], s, m->t_emb_steps + (size_t)step * c.hidden));
         const float dt = ts[step + 1] - ts[step];
         SF_TRY(sf_euler_update(m->x_state, m->vel_rows, c.batch, c.horizon, c.action_dim,
                                c.horizon + 3, dt, s));
@@ -849,6 +855,15 @@ int resolve_pv_forms(sf_rdt* m) {
 
 hipStream_t pick_stream(sf_rdt* m, void* stream) {
     return stream ? static_cast<hipStream_t>(stream) : m->own_stream;
+}
+
+// The fp16 weight copies of the library path, brought up to date before a
+// pass (never under capture: every entry point calls this first).
+int refresh_w16(sf_rdt* m, hipStream_t s) {
+    if (!m->codes16 || !m->w16_stale) return SF_OK;
+    SF_TRY(widen_codes(m, 0, m->cfg.layers, s, true));
+    m->w16_stale = false;
+    return SF_OK;
 }
 
 }  // namespace
@@ -1124,7 +1139,7 @@ extern "C" int sf_rdt_init_random(sf_rdt* m, uint64_t seed, float std, void* str
         }
     }
     release_graph(m);   // weights changed: a captured graph stays valid, but be explicit
-    m->infer_cond_valid = false;
+    sf_rdt_weights_changed(m);
     return SF_OK;
 }
 
@@ -1144,7 +1159,14 @@ extern "C" int sf_rdt_param_info(const sf_rdt* m, int32_t idx, const char** name
 
 extern "C" void* sf_rdt_param_data(sf_rdt* m, int32_t idx) {
     if (!m || idx < 0 || idx >= (int32_t)m->params.size()) return nullptr;
+    m->w16_stale = true;   // the caller may write through it before the next pass
     return m->params[idx].data;
+}
+
+extern "C" int sf_rdt_params_changed(sf_rdt* m) {
+    if (!m) return SF_EINVAL;
+    sf_rdt_weights_changed(m);
+    return SF_OK;
 }
 
 extern "C" float* sf_rdt_param_scale(sf_rdt* m, int32_t idx) {
@@ -1322,9 +1344,9 @@ extern "C" int sf_rdt_run_blocks(sf_rdt* m, float* x, int32_t first, int32_t cou
     hipStream_t s = pick_stream(m, stream);
     SF_TRY(resolve_pv_forms(m));
     const size_t nbytes = (size_t)c.batch * (c.horizon + 3) * c.hidden * 4;
+    SF_TRY(refresh_w16(m, s));
     SF_HIP(hipMemcpyAsync(m->x, x, nbytes, hipMemcpyDeviceToDevice, s));
     SF_TRY(entry_norm(m, first, s));
-    SF_TRY(widen_codes(m, first, count, s, false));
     for (int i = first; i < first + count; ++i) SF_TRY(block_forward(m, i, s));
     SF_HIP(hipMemcpyAsync(x, m->x, nbytes, hipMemcpyDeviceToDevice, s));
     return SF_OK;
@@ -1336,6 +1358,7 @@ extern "C" int sf_rdt_denoise_step(sf_rdt* m, const float* x_t, float t, float* 
     const sf_rdt_config& c = m->cfg;
     hipStream_t s = pick_stream(m, stream);
     SF_TRY(resolve_pv_forms(m));
+    SF_TRY(refresh_w16(m, s));
     SF_TRY(step_forward(m, x_t, t, s));
     // last T token rows of each batch element (rdt1b.cpp:362-368)
     SF_HIP(hipMemcpy2DAsync(velocity, (size_t)c.horizon * c.action_dim * 4,
@@ -1349,6 +1372,7 @@ extern "C" int sf_rdt_sample(sf_rdt* m, float* x, int32_t use_graph, void* strea
     const sf_rdt_config& c = m->cfg;
     hipStream_t s = pick_stream(m, stream);
     SF_TRY(resolve_pv_forms(m));
+    SF_TRY(refresh_w16(m, s));
     const size_t nbytes = (size_t)c.batch * c.horizon * c.action_dim * 4;
     // the initial noise is copied in outside the graph (flow_matching.cpp:49-51)
     SF_HIP(hipMemcpyAsync(m->x_state, x, nbytes, hipMemcpyDeviceToDevice, s));

@@ -57,6 +57,7 @@ def lib():
                                     ctypes.POINTER(i32), ctypes.c_int64 * 4]
     L.sf_rdt_param_data.argtypes = [vp, i32]
     L.sf_rdt_param_data.restype = vp
+    L.sf_rdt_params_changed.argtypes = [vp]
     L.sf_rdt_param_scale.argtypes = [vp, i32]
     L.sf_rdt_param_scale.restype = vp
     L.sf_rdt_find_param.argtypes = [vp, ctypes.c_char_p]
@@ -196,6 +197,11 @@ class RdtModel:
         v = np.ascontiguousarray(values)
         assert v.itemsize == esize and offset + v.size <= int(np.prod(shape))
         _hipmemcpy(lib().sf_rdt_param_data(self.h, idx) + offset * esize, v.ctypes.data, v.nbytes, 1)
+
+    def params_changed(self):
+        """sf_rdt_params_changed: parameters were written through pointers
+        obtained earlier; the weight copies are rebuilt before the next pass."""
+        abi.check(lib().sf_rdt_params_changed(self.h), "sf_rdt_params_changed")
 
     def set_lang_rows(self, rows):
         """The language condition's token count L (sf_rdt_set_lang_rows): the

@@ -169,6 +169,60 @@ def test_loop_large_batch_graph_and_oracle(batch, int8):
         assert_within_floor(eager[b:b + 1], ref, floor, f"loop B={batch} slot {b}")
 
 
+@pytest.mark.parametrize("int8", [0, 1])
+def test_weight_writes_reach_the_large_batch_copies(int8):
+    """Above 160 rows the projections multiply fp16 copies of the weights,
+    rebuilt before a pass only when the parameters may have changed.  A
+    write through sf_rdt_param_data after a pass (param_write), and a write
+    through a pointer taken before a pass followed by sf_rdt_params_changed,
+    both reach the next graph replay: its velocity matches the oracle on
+    the new weights (a stale copy would give the old weights' result)."""
+    import ctypes
+    c = small_cfg(layers=2, batch=3, int8_weights=int8)
+    m = build(c)
+    lang, ll, img, state = make_condition(c)
+    set_cond(m, lang, ll, img, state)
+    x0 = O.randn(41, (c.batch, c.horizon, c.action_dim))
+
+    def loop():
+        x = torch.from_numpy(x0).to(DEV)
+        m.sample(x, use_graph=True)
+        return x.cpu().numpy()
+
+    base = loop()
+    oc = oracle_cfg(c)
+    for how in ("param_write", "raw_pointer"):
+        name = "blocks.1.ffn.fc2.weight"
+        idx = R.lib().sf_rdt_find_param(m.h, name.encode())
+        p0 = m.state_dict()
+        if int8:
+            # new codes, same row scales: negate every code of the matrix
+            q = np.empty(p0[name].shape, np.int8)
+            ptr = R.lib().sf_rdt_param_data(m.h, idx)
+            R._memcpy_d2h(q, ptr)
+            newv = (-q.astype(np.int16)).clip(-127, 127).astype(np.int8)
+        else:
+            newv = O.bf16_round(-p0[name])
+            newv = (newv.view(np.uint32) >> 16).astype(np.uint16)
+        if how == "param_write":
+            loop()                     # a pass first: the copies are current
+            m.param_write(idx, newv.reshape(-1))
+        else:
+            ptr = R.lib().sf_rdt_param_data(m.h, idx)   # pointer taken before the pass
+            loop()
+            R._hipmemcpy(ptr, np.ascontiguousarray(newv).ctypes.data, newv.nbytes, 1)
+            m.params_changed()
+        got = loop()
+        p = m.state_dict()
+        assert not np.array_equal(p[name], p0[name])
+        caches = OR.encode_caches(p, lang, img, oc, rb=rb_of(c))
+        ref, floor = oracle_noise_floor(lambda: OR.sample(p, x0, state, caches, ll, oc, rb=rb_of(c)))
+        print(f"{how} int8={int8}: mean-rel {mean_rel(got, ref):.3e} floor {floor:.3e}", flush=True)
+        assert_within_floor(got, ref, floor, f"loop after {how}")
+        assert not np.array_equal(got, base)
+        base = got
+
+
 def test_run_blocks_int8_large_batch_block_range():
     """sf_rdt_run_blocks on an int8 model at batch 32 (2144 rows, the
     library path) over blocks 1..2 of 3: the runtime widens the int8 codes
