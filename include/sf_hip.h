@@ -159,6 +159,16 @@ typedef struct sf_attn_desc {
      * contraction is the bf16 one.  SF_ENOTSUP with another in_dtype or
      * with q_partials. */
     int32_t q_f16;
+    /* With q_partials: q_row_ss != NULL says the projection's input rows
+     * held x * gamma of a deferred RMSNorm (sf_gemm_desc.norm_ss); Q's row
+     * b*Sq + s is then scaled by rsqrt(sum_t q_row_ss[t * B*Sq + b*Sq + s]
+     * / q_row_n + q_row_eps) (q_row_tiles <= 64 tiles) after q_scale and
+     * before q_bias -- as sf_gemm's a_row_ss does, bit for bit.
+     * SF_EINVAL without q_partials. */
+    const float* q_row_ss;
+    int32_t q_row_tiles;
+    int32_t q_row_n;
+    float q_row_eps;
 } sf_attn_desc;
 
 /* Fills a descriptor for contiguous [B,H,S,D] tensors (the layout
@@ -300,6 +310,22 @@ typedef struct sf_gemm_desc {
                                 products (round_product, and a plain C written by hipBLASLt, which
                                 must then be SF_F16) are fp16.  Ignored on the other paths, which
                                 read W itself (SF_EINVAL when w_codes16 is NULL on this path) */
+    /* Deferred RMSNorm (split-K path, M <= 160 with a workspace; SF_ENOTSUP
+     * elsewhere; N a multiple of 64).  norm_ss (SF_EPI_ADD_NORM): instead of
+     * the normalised row, norm_out[m] = C[m] * norm_gamma after the residual
+     * add, and norm_ss[t * M + m] = the sum of C[m][n]^2 over the 64 columns
+     * n of tile t (N / 64 tiles, fp32, 16-byte aligned) -- the row-wide
+     * reduction is left to the consumer, so no workgroup waits for a whole
+     * row.  a_row_ss (SF_EPI_PLAIN / SF_EPI_HEADS): A holds such rows; output
+     * row m is scaled by rsqrt(sum_t a_row_ss[t * M + m] / a_row_n +
+     * a_row_eps) (a_row_tiles tiles, <= 64) after the int8 scale and before
+     * the bias: (s a) W^T = s (a W^T), the normalisation of
+     * fused_add_rms_norm (norm.cuh:130-171) applied after the product. */
+    float* norm_ss;
+    const float* a_row_ss;
+    int32_t a_row_tiles;
+    int32_t a_row_n;
+    float a_row_eps;
 } sf_gemm_desc;
 
 /* Bytes of workspace sf_gemm needs for this call (0: it always runs
@@ -369,6 +395,15 @@ int sf_gemm_algo_pick(const sf_gemm_desc* desc, int32_t* pick, int32_t* candidat
 int sf_rmsnorm(const void* x, int32_t x_dtype, int64_t ldx, const float* gamma,
                void* out, int32_t out_dtype, int64_t ldo, int32_t rows,
                int32_t cols, float eps, void* stream);
+
+/* Deferred RMSNorm of fp32 rows x (cols a multiple of 64, rows 16-byte
+ * aligned): out[r] = x[r] * gamma (not yet normalised) and ss[t * rows + r]
+ * = the sum of x[r][c]^2 over the 64 columns c of tile t, for a consumer
+ * that applies rsqrt(sum_t ss / cols + eps) after its contraction
+ * (sf_gemm_desc.a_row_ss, sf_attn_desc.q_row_ss) -- rms_norm_kernel_impl
+ * (norm.cuh:89-122) with its row-wide step moved into the consumer. */
+int sf_rmsnorm_deferred(const float* x, int64_t ldx, const float* gamma, void* out, int32_t out_dtype,
+                        int64_t ldo, float* ss, int32_t rows, int32_t cols, void* stream);
 
 /* residual[r] += delta[r]; out[r] = rmsnorm(residual[r]) * gamma
  * (fused_add_rms_norm_kernel, norm.cuh:130-171; IBackend::fused_add_rms_norm,

@@ -94,9 +94,14 @@ def storage_points(ffn16, gemm16=False, act16=False):
 def runtime_points(rows):
     """The MI355X runtime's storage at `rows` = batch * 67 projection rows:
     the split-K regime (<= 160) keeps bf16 inputs with fp16 FFN inputs and
-    fp32 products; the library regime (> 160) keeps fp16 inputs and fp16
-    products (storage_points)."""
-    return storage_points(True, act16=rows > 160)
+    fp32 products, and norm1 / norm2 in their deferred form ("defer": the
+    rows x * gamma are stored, the projection's output rows scaled by
+    1/rms after the product); the library regime (> 160) keeps fp16 inputs
+    and fp16 products (storage_points)."""
+    pts = storage_points(True, act16=rows > 160)
+    if rows <= 160:
+        pts["defer"] = True
+    return pts
 
 
 def _f16_round(x):
@@ -140,15 +145,31 @@ def cross_kv(p, i, cond, cfg, rb=True):
     return _r(K, rb, "kv"), _r(V, rb, "kv")
 
 
+def _deferred_linear(x, gamma, W, b, eps, rb, point):
+    """RMSNorm(x) W^T + b in the runtime's deferred form: the stored input
+    rows are x * gamma (rounded at `point`), the row's 1/rms multiplies the
+    product before the bias -- equal in exact arithmetic, (s a) W^T =
+    s (a W^T)."""
+    x = np.asarray(x, np.float32)
+    a = _r(x * np.asarray(gamma, np.float32), rb, point)
+    s = (1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(-1, keepdims=True) + eps)).astype(np.float32)
+    return O.linear(a, W) * s + np.asarray(b, np.float32)
+
+
 def rdt_block(p, i, x, ck, cv, cond_len, cfg, rb=True):
     """RDTBlock::forward, src/models/rdt1b/dit_block.cu:349-387, with the
     cross-attention K/V precomputed (cross_kv).  x [B,S,D] fp32, updated."""
     B, S, D = x.shape
     H = cfg.heads
     pre = f"blocks.{i}."
+    defer = isinstance(rb, dict) and rb.get("defer", False)
     # self-attention branch (dit_block.cu:198-238)
-    n1 = _r(O.rms_norm(x, p[pre + "norm1.weight"], cfg.eps), rb, "n1")
-    qkv = _r(O.linear(n1, p[pre + "attn.qkv.weight"], p[pre + "attn.qkv.bias"]), rb, "hgemm")
+    if defer:
+        qkv = _r(_deferred_linear(x, p[pre + "norm1.weight"], p[pre + "attn.qkv.weight"],
+                                  p[pre + "attn.qkv.bias"], cfg.eps, rb, "n1"), rb, "hgemm")
+    else:
+        n1 = _r(O.rms_norm(x, p[pre + "norm1.weight"], cfg.eps), rb, "n1")
+        qkv = _r(O.linear(n1, p[pre + "attn.qkv.weight"], p[pre + "attn.qkv.bias"]), rb, "hgemm")
     Q, K, V = O.split_qkv(qkv.reshape(B, S, 3 * D), H, 64)
     Q = _r(O.rms_norm(Q, p[pre + "attn.q_norm.weight"], cfg.eps), rb, "qkv")
     K = _r(O.rms_norm(K, p[pre + "attn.k_norm.weight"], cfg.eps), rb, "qkv")
@@ -156,8 +177,12 @@ def rdt_block(p, i, x, ck, cv, cond_len, cfg, rb=True):
     a = _r(O.head_to_seq(O.attention_f32(Q, K, V)), rb, "a")
     x = x + _r(O.linear(a, p[pre + "attn.proj.weight"], p[pre + "attn.proj.bias"]), rb, "gemm")
     # cross-attention branch (dit_block.cu:274-326), norm2 from fused_add_rms_norm
-    n2 = _r(O.rms_norm(x, p[pre + "norm2.weight"], cfg.eps), rb, "n2")
-    cq = _r(O.linear(n2, p[pre + "cross_attn.q.weight"], p[pre + "cross_attn.q.bias"]), rb, "hgemm")
+    if defer:
+        cq = _r(_deferred_linear(x, p[pre + "norm2.weight"], p[pre + "cross_attn.q.weight"],
+                                 p[pre + "cross_attn.q.bias"], cfg.eps, rb, "n2"), rb, "hgemm")
+    else:
+        n2 = _r(O.rms_norm(x, p[pre + "norm2.weight"], cfg.eps), rb, "n2")
+        cq = _r(O.linear(n2, p[pre + "cross_attn.q.weight"], p[pre + "cross_attn.q.bias"]), rb, "hgemm")
     cq = _r(O.rms_norm(heads_of(cq.reshape(B, S, D), H), p[pre + "cross_attn.q_norm.weight"], cfg.eps), rb, "cq")
     ca = _r(O.head_to_seq(O.attention_f32(cq, ck, cv, valid_len=cond_len)), rb, "a")
     x = x + _r(O.linear(ca, p[pre + "cross_attn.proj.weight"], p[pre + "cross_attn.proj.bias"]), rb, "gemm")

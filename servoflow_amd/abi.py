@@ -58,6 +58,10 @@ class AttnDesc(ctypes.Structure):
         ("q_eps", ctypes.c_float),
         ("k_gamma", ctypes.c_void_p),
         ("q_f16", ctypes.c_int32),
+        ("q_row_ss", ctypes.c_void_p),
+        ("q_row_tiles", ctypes.c_int32),
+        ("q_row_n", ctypes.c_int32),
+        ("q_row_eps", ctypes.c_float),
     ]
 
 
@@ -93,6 +97,11 @@ class GemmDesc(ctypes.Structure):
         ("round_product", ctypes.c_int32),
         ("w_codes16", ctypes.c_void_p),
         ("w16_f16", ctypes.c_int32),
+        ("norm_ss", ctypes.c_void_p),
+        ("a_row_ss", ctypes.c_void_p),
+        ("a_row_tiles", ctypes.c_int32),
+        ("a_row_n", ctypes.c_int32),
+        ("a_row_eps", ctypes.c_float),
     ]
 
 
@@ -166,6 +175,8 @@ def lib() -> ctypes.CDLL:
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     L.sf_rmsnorm.argtypes = [vp, i32, i64, vp, vp, i32, i64, i32, i32, ctypes.c_float, vp]
     L.sf_rmsnorm.restype = ctypes.c_int
+    L.sf_rmsnorm_deferred.argtypes = [vp, i64, vp, vp, i32, i64, vp, i32, i32, vp]
+    L.sf_rmsnorm_deferred.restype = ctypes.c_int
     L.sf_add_rmsnorm.argtypes = [vp, i32, vp, vp, vp, i32, i32, i32, ctypes.c_float, vp]
     L.sf_add_rmsnorm.restype = ctypes.c_int
     L.sf_dequant_int8.argtypes = [vp, vp, i32, vp, i32, i64, i64, vp]

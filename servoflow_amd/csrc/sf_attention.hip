@@ -79,6 +79,11 @@ struct AttnArgs {
     float q_eps;
     const float* k_gamma;   // per-head RMSNorm weight of K (the short-key kernel)
     int q_f16;              // bf16 instances: Q rows given in fp16, rounded to bf16 (after q_gamma) on load
+    // Q from partials of x * gamma rows (a deferred RMSNorm): row scale from
+    // q_row_ss[t][b * Sq + s], t < q_row_tiles
+    const float* q_row_ss;
+    int q_row_tiles;
+    float q_row_inv_n, q_row_eps;
 };
 
 enum OutKind { kOutBF16 = 0, kOutF32 = 1, kOutF16 = 2 };
@@ -523,6 +528,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
     constexpr int kQPMax = 8;
     f32x4 qpv[kQP ? kQPMax : 1];
     f32x4 qbias, qscale, qgam;
+    float qrss[4] = {0.f, 0.f, 0.f, 0.f};
     if constexpr (kQP) {
         static_assert(QB == 1 && !kF16, "Q from partials: the bf16 query-block instance");
         const int row = q0 + 4 * w + (lane >> 4);
@@ -544,6 +550,15 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
         qbias = __builtin_bit_cast(f32x4, buffer_load16(brs, (uint32_t)(nb * 4)));
         qscale = __builtin_bit_cast(f32x4, buffer_load16(srs, (uint32_t)(nb * 4)));
         qgam = __builtin_bit_cast(f32x4, buffer_load16(grs, (uint32_t)(c4 * 4)));
+        if (a.q_row_ss) {   // the deferred norm's tile sums of this lane's row
+            const int64_t prow = (int64_t)b * a.Sq + (rlive ? row : 0);
+            const int64_t M = (int64_t)a.B * a.Sq;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int t = (lane & 15) + 16 * k;
+                qrss[k] = t < a.q_row_tiles ? a.q_row_ss[t * M + prow] : 0.f;
+            }
+        }
     } else {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
@@ -618,8 +633,18 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 #pragma unroll
         for (int j = 1; j < kQPMax; ++j)
             if (j < a.q_splits) v += qpv[j];
+        if (a.q_row_ss) {   // as reduce_heads_kernel over x * gamma rows (deferred_row_scale)
+            float tsum = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = v[i] * (a.q_scale ? qscale[i] : 1.f) + qbias[i];
+            for (int k = 0; k < 4; ++k)
+                if ((lane & 15) + 16 * k < a.q_row_tiles) tsum += qrss[k];
+            const float rs = deferred_rsqrt(row16_sum(tsum), a.q_row_inv_n, a.q_row_eps);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = deferred_affine(v[i], a.q_scale ? qscale[i] : 1.f, rs, qbias[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = v[i] * (a.q_scale ? qscale[i] : 1.f) + qbias[i];
+        }
         if (a.q_gamma) {
             float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
             ss = row16_sum(ss);
@@ -1424,6 +1449,10 @@ int validate(const sf_attn_desc* d) {
         for (const void* p : ptrs)
             if (reinterpret_cast<uintptr_t>(p) & 15) return SF_EINVAL;
         if ((int64_t)d->q_splits * d->B * d->Sq * d->H * 64 * 4 > 0x7fffffffLL) return SF_ENOTSUP;
+        if (d->q_row_ss && (d->q_row_tiles < 1 || d->q_row_tiles > 64 || d->q_row_n <= 0 || !(d->q_row_eps >= 0.f)))
+            return SF_EINVAL;
+    } else if (d->q_row_ss) {
+        return SF_EINVAL;   // a row scale applies to Q given as partials only
     }
     if (d->q_f16) {   // fp16 Q rows against bf16 K / V
         if (d->in_dtype != SF_BF16 || d->q_partials) return SF_ENOTSUP;
@@ -1560,6 +1589,10 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
     a.q_eps = d->q_eps;
     a.k_gamma = d->k_gamma;
     a.q_f16 = d->q_f16 != 0;
+    a.q_row_ss = d->q_row_ss;
+    a.q_row_tiles = d->q_row_tiles;
+    a.q_row_inv_n = d->q_row_n > 0 ? 1.f / (float)d->q_row_n : 0.f;
+    a.q_row_eps = d->q_row_eps;
     a.k = static_cast<const uint16_t*>(k);
     a.v = static_cast<const uint16_t*>(v);
     a.o = out;

@@ -90,6 +90,18 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
+// Deferred RMSNorm: the row scale rsqrt(ss / n + eps) from a row's sum of
+// squares, and the affine step a consumer applies to its contraction v of
+// x * gamma rows: (v * weight scale) * row scale + bias, one rounding for
+// the product and one fused multiply-add, the same in every kernel that
+// finishes such a projection (so their results agree bit for bit).
+__device__ __forceinline__ float deferred_rsqrt(float ss, float inv_n, float eps) {
+    return 1.f / sqrtf(ss * inv_n + eps);
+}
+__device__ __forceinline__ float deferred_affine(float v, float wscale, float rs, float bias) {
+    return __builtin_fmaf(v * wscale, rs, bias);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);
 }

@@ -518,6 +518,15 @@ struct EpiArgs {
     void* norm_out;
     int64_t norm_ldo;
     int norm_f32, norm_f16;
+    // deferred RMSNorm, producer side (SF_EPI_ADD_NORM with norm_ss): x * gamma
+    // to norm_out and, per 64-column tile t, norm_ss[t][m] = sum of x^2
+    float* norm_ss;
+    // consumer side: the activation rows hold x * gamma of a deferred norm;
+    // each output row m is scaled by rsqrt(sum_t row_ss[t][m] * row_inv_n +
+    // row_eps) after the weight scale and before the bias
+    const float* row_ss;
+    int row_tiles;
+    float row_inv_n, row_eps;
 };
 
 // Sum of the K-slice partials for C[m][n..n+3], slices in ascending order,
@@ -557,22 +566,39 @@ __device__ __forceinline__ void load_quad(const EpiArgs& e, int m, int n, Quad<N
     q.scale = e.w_scale ? *reinterpret_cast<const f32x4*>(e.w_scale + n) : f32x4{1.f, 1.f, 1.f, 1.f};
 }
 
+// rs: the row's deferred-norm scale (row_ss set), else unused.
 template <int NS>
-__device__ __forceinline__ f32x4 finish_quad(const EpiArgs& e, const Quad<NS>& q) {
+__device__ __forceinline__ f32x4 finish_quad(const EpiArgs& e, const Quad<NS>& q, float rs = 1.f) {
     f32x4 v = q.part[0];
 #pragma unroll
     for (int s = 1; s < NS; ++s)
         if (s < e.splits) v += q.part[s];
+    if (e.row_ss) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = apply_act(e.act, v[j] * q.scale[j] + q.bias[j]);
+        for (int j = 0; j < 4; ++j) v[j] = apply_act(e.act, deferred_affine(v[j], q.scale[j], rs, q.bias[j]));
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = apply_act(e.act, v[j] * q.scale[j] + q.bias[j]);
+    }
     return v;
+}
+
+// The deferred-norm scale of row m for the 16 lanes that share it (lanes
+// 16k .. 16k + 15, the reduce tiles' layout): lane j adds tiles j, j + 16,
+// ... in ascending order, then the 16 lanes' sums are combined in a fixed
+// butterfly (deterministic).  1 without row_ss.
+__device__ __forceinline__ float deferred_row_scale(const EpiArgs& e, int m) {
+    if (!e.row_ss) return 1.f;
+    float t = 0.f;
+    for (int k = (int)(threadIdx.x & 15); k < e.row_tiles; k += 16) t += e.row_ss[(int64_t)k * e.M + m];
+    return deferred_rsqrt(row16_sum(t), e.row_inv_n, e.row_eps);
 }
 
 template <int NS>
 __device__ __forceinline__ f32x4 finish4(const EpiArgs& e, int m, int n) {
     Quad<NS> q;
     load_quad<NS>(e, m, n, q);
-    return finish_quad<NS>(e, q);
+    return finish_quad<NS>(e, q, deferred_row_scale(e, m));
 }
 
 __device__ __forceinline__ uint2 pack_bf16x4(f32x4 v) {
@@ -749,6 +775,35 @@ __global__ __launch_bounds__(kAddNormThreads) void reduce_addnorm_kernel(const E
     }
 }
 
+// Deferred form of the residual add + RMSNorm, one workgroup per 16-row x
+// 64-column tile (the reduce tiles' layout and XCD placement): x[m] +=
+// result[m]; norm_out[m] = x[m] * gamma (not yet normalised); norm_ss[t][m]
+// = the tile's sum of x^2 over its 64 columns (4 per lane in column order,
+// then the 16 lanes of the row in a fixed butterfly).  The consumer of
+// norm_out applies the row's rsqrt(mean x^2 + eps) after its contraction:
+// (s a) W^T = s (a W^T).  Every CU takes part, where the row-wide form runs
+// one workgroup per row.
+template <int NS>
+__global__ __launch_bounds__(256) void reduce_addnorm_cols_kernel(const EpiArgs e) {
+    int m, n;
+    if (!reduce_tile_rc(e, m, n)) return;   // whole 16-lane groups
+    Quad<NS> q;
+    load_quad<NS>(e, m, n, q);
+    float* xp = static_cast<float*>(e.c) + (e.m_off + m) * e.ldc + n;
+    f32x4 x = *reinterpret_cast<const f32x4*>(xp);
+    const f32x4 gq = *reinterpret_cast<const f32x4*>(e.norm_gamma + n);
+    x += finish_quad<NS>(e, q);
+    *reinterpret_cast<f32x4*>(xp) = x;
+    const f32x4 u = x * gq;
+    const int64_t off = (e.m_off + m) * e.norm_ldo + n;
+    if (e.norm_f32)
+        *reinterpret_cast<f32x4*>(static_cast<float*>(e.norm_out) + off) = u;
+    else
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.norm_out) + off) = pack_16x4(u, e.norm_f16);
+    const float ss = row16_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+    if ((threadIdx.x & 15) == 0) e.norm_ss[(int64_t)(n / 64) * e.M + m] = ss;
+}
+
 // int8 weight codes -> bf16 (exact), row-major [N][K] out of [N][ldw].
 // CH codes per thread (16: one 16-byte load and two 16-byte stores, needs
 // 16-byte aligned rows; 8 otherwise); 32-bit index arithmetic (callers keep
@@ -919,6 +974,8 @@ void launch_reduce(const sf_gemm_desc* d, const EpiArgs& e, hipStream_t s) {
         hipLaunchKernelGGL(heads16_kernel, dim3((unsigned)((int64_t)(e.N / 64) * ((e.M + 31) / 32))), dim3(256), 0, s, e);
     else if (d->epilogue == SF_EPI_HEADS)
         hipLaunchKernelGGL(reduce_heads_kernel<NS>, dim3(tiles), dim3(256), 0, s, e);
+    else if (d->epilogue == SF_EPI_ADD_NORM && e.norm_ss)
+        hipLaunchKernelGGL(reduce_addnorm_cols_kernel<NS>, dim3(tiles), dim3(256), 0, s, e);
     else if (d->epilogue == SF_EPI_ADD_NORM)
         hipLaunchKernelGGL(reduce_addnorm_kernel<NS>, dim3(e.M), dim3(kAddNormThreads), 0, s, e);
     else if ((e.N & 63) == 0)
@@ -1275,6 +1332,20 @@ int validate(const sf_gemm_desc* d, sfk::EpiArgs& e) {
     const int64_t abytes = d->a_dtype == SF_F32 ? 4 : 2;
     if ((int64_t)std::max(1, std::min(80, d->M)) * d->lda * abytes > 0x7fffffffLL) return SF_ENOTSUP;
     if ((int64_t)std::min(64, d->N) * d->ldw * 2 > 0x7fffffffLL) return SF_ENOTSUP;
+    if (d->a_row_ss) {   // the activation rows hold x * gamma of a deferred norm
+        if (d->epilogue != SF_EPI_PLAIN && d->epilogue != SF_EPI_HEADS) return SF_EINVAL;
+        if (d->a_row_tiles < 1 || d->a_row_tiles > 64 || d->a_row_n <= 0 || !(d->a_row_eps >= 0.f)) return SF_EINVAL;
+        if (d->N & 63) return SF_ENOTSUP;
+        e.row_ss = d->a_row_ss;
+        e.row_tiles = d->a_row_tiles;
+        e.row_inv_n = 1.f / (float)d->a_row_n;
+        e.row_eps = d->a_row_eps;
+    }
+    if (d->norm_ss) {    // deferred form of the residual add + RMSNorm
+        if (d->epilogue != SF_EPI_ADD_NORM) return SF_EINVAL;
+        if ((d->N & 63) || !al16(d->norm_ss)) return SF_ENOTSUP;
+        e.norm_ss = d->norm_ss;
+    }
     e.M = d->M;
     e.N = d->N;
     e.w_scale = d->w_dtype == SF_I8 ? d->w_scale : nullptr;
@@ -1517,6 +1588,8 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     if (f16lib && (!d->w_codes16 || !al16(d->w_codes16))) return SF_EINVAL;
     if (a32 && ((d->lda & 3) || !al16(d->A))) return SF_EINVAL;
     const sfk::SkPlan p = sfk::plan_splitk(d->M, d->N, d->K, a32);
+    // the deferred norm (either side) runs on the split-K path only
+    if ((d->norm_ss || d->a_row_ss) && !(d->workspace && p.split && splittable(d))) return SF_ENOTSUP;
     if (d->epilogue == SF_EPI_PARTIALS) {   // the K-slice sums only, for a consumer to finish
         if (!p.split || !d->workspace) return SF_ENOTSUP;
         if (d->workspace_bytes < 0 || (size_t)d->workspace_bytes < p.ws_bytes) return SF_EWORKSPACE;

@@ -74,6 +74,25 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
     }
 }
 
+// Deferred form (no normalisation yet): out = x * gamma and ss[t][row] =
+// the sum of x^2 over the 64 columns of tile t, one workgroup per 16 rows x
+// 64 columns (lanes 16k .. 16k + 15 share a row, 4 columns each); the same
+// layout and summation order as the GEMM's deferred residual add + norm.
+__global__ __launch_bounds__(256) void norm_deferred_kernel(const float* x, int64_t ldx, const float* gamma,
+                                                            void* out, int okind, int64_t ldo, float* ss,
+                                                            int rows, int cols) {
+    const int ntl = cols / 64;
+    const int r = (int)(blockIdx.x / ntl) * 16 + (int)(threadIdx.x >> 4);
+    const int c = 64 * (int)(blockIdx.x % ntl) + 4 * (int)(threadIdx.x & 15);
+    if (r >= rows) return;   // whole 16-lane groups
+    const f32x4 v = *reinterpret_cast<const f32x4*>(x + (int64_t)r * ldx + c);
+    const f32x4 g = *reinterpret_cast<const f32x4*>(gamma + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_elem(out, okind, (int64_t)r * ldo + c + j, v[j] * g[j]);
+    const float t = row16_sum(v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]);
+    if ((threadIdx.x & 15) == 0) ss[(int64_t)(c / 64) * rows + r] = t;
+}
+
 __global__ __launch_bounds__(256) void dequant_int8_kernel(const int8_t* q, const float* scale,
                                                            int per_channel, void* out, int out_bf16,
                                                            int64_t n, int64_t K) {
@@ -97,6 +116,22 @@ extern "C" int sf_rmsnorm(const void* x, int32_t x_dtype, int64_t ldx, const flo
     hipLaunchKernelGGL(sfk::rmsnorm_kernel, dim3(rows), dim3(sfk::kNormThreads), 0,
                        static_cast<hipStream_t>(stream), x, x_dtype == SF_BF16, ldx, nullptr, 0,
                        nullptr, gamma, out, sfk::out_kind(out_dtype), ldo, cols, eps);
+    return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+}
+
+extern "C" int sf_rmsnorm_deferred(const float* x, int64_t ldx, const float* gamma, void* out, int32_t out_dtype,
+                                   int64_t ldo, float* ss, int32_t rows, int32_t cols, void* stream) {
+    if (rows < 0 || cols < 0) return SF_EINVAL;
+    if ((long)rows * cols == 0) return SF_OK;
+    if (!x || !gamma || !out || !ss || ldx < cols || ldo < cols) return SF_EINVAL;
+    if (out_dtype != SF_F32 && out_dtype != SF_BF16 && out_dtype != SF_F16) return SF_ENOTSUP;
+    if ((cols & 63) || (ldx & 3) || ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma)) & 15))
+        return SF_EINVAL;
+    const int64_t blocks = (int64_t)(cols / 64) * ((rows + 15) / 16);
+    if (blocks > 0x7fffffffLL) return SF_ENOTSUP;
+    hipLaunchKernelGGL(sfk::norm_deferred_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, ldx, gamma, out, sfk::out_kind(out_dtype), ldo, ss,
+                       rows, cols);
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
 }
 

@@ -124,6 +124,18 @@ struct sf_rdt {
     // long as the model's activations do.
     int32_t ffn_dtype = SF_F16;
     int32_t act16 = SF_BF16;
+    // Deferred RMSNorm (split-K regime, B*S <= 160): the norm1 / norm2
+    // producers -- the entry norm, the fc2 and attention-proj residual adds --
+    // store x * gamma and per-64-column sums of squares (row_ss, [D/64][B*S])
+    // and the consumers (the QKV and cross-q projections, or the language
+    // attention finishing Q from partials) apply the row's 1/rms after their
+    // contraction: every CU takes part in the residual-add kernels, which
+    // otherwise run one workgroup per row.  norm3 and the final norm keep the
+    // row-wide form (their fp16 outputs need the normalised range).
+    // n_deferred: whether n holds deferred rows (set as kernels are enqueued).
+    bool defer = false;
+    bool n_deferred = false;
+    float* row_ss = nullptr;
     void* n3 = nullptr;            // [B*S, D] norm3 output
     void* h = nullptr;             // [B*S, F] FFN hidden
     uint16_t* act_in = nullptr;    // [B*T, 2A]
@@ -369,6 +381,15 @@ bool kv_batched(const sf_rdt* m, int g, int rows) {
            bytes <= m->kv_prod_bytes;
 }
 
+// A as deferred-norm rows (x * gamma with m->row_ss): the output rows get
+// their 1/rms after the product.
+void set_row_scale(const sf_rdt* m, sf_gemm_desc& d) {
+    d.a_row_ss = m->row_ss;
+    d.a_row_tiles = m->cfg.hidden / 64;
+    d.a_row_n = m->cfg.hidden;
+    d.a_row_eps = m->cfg.eps;
+}
+
 int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, int act, void* C,
            int64_t ldc, int c_dtype, bool accumulate, hipStream_t s, int a_dtype = SF_BF16) {
     const Param& W = m->params[w_idx];
@@ -402,7 +423,7 @@ int linear(sf_rdt* m, const void* A, int64_t lda, int M, int w_idx, int b_idx, i
 // output is stored in bf16 before the add (round_product), as the
 // reference's projection returns it (dit_block.cu:233, 321, 160).
 int linear_add_norm(sf_rdt* m, const void* A, int a_dtype, int M, int w_idx, int b_idx, int gamma_idx,
-                    void* out, int out_dtype, hipStream_t s) {
+                    void* out, int out_dtype, hipStream_t s, bool deferred = false) {
     const Param& W = m->params[w_idx];
     const int D = m->cfg.hidden;
     sf_gemm_desc d{};
@@ -431,6 +452,7 @@ int linear_add_norm(sf_rdt* m, const void* A, int a_dtype, int M, int w_idx, int
     d.workspace = m->gemm_ws;
     d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
     d.round_product = 1;
+    if (deferred) d.norm_ss = m->row_ss;
     return sf_gemm(&d, s);
 }
 
@@ -440,7 +462,7 @@ int linear_add_norm(sf_rdt* m, const void* A, int a_dtype, int M, int w_idx, int
 // (dit_block.cu:207, 284, 291).
 int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
                  uint16_t* const* outs, const int* gamma_idx, int nsec, hipStream_t s,
-                 int a_dtype = SF_BF16, bool round_product = false) {
+                 int a_dtype = SF_BF16, bool round_product = false, bool a_deferred = false) {
     const Param& W = m->params[w_idx];
     const int H = m->cfg.heads;
     sf_gemm_desc d{};
@@ -471,17 +493,20 @@ int linear_heads(sf_rdt* m, const void* A, int M, int S, int w_idx, int b_idx,
     d.workspace = m->gemm_ws;
     d.workspace_bytes = (int64_t)m->gemm_ws_bytes;
     d.round_product = round_product ? 1 : 0;
+    if (a_deferred) set_row_scale(m, d);
     return sf_gemm(&d, s);
 }
 
 // Q of a cross-attention given as the cross-q projection's split-K
-// partials (sf_attn_desc.q_partials).
+// partials (sf_attn_desc.q_partials); row_ss: their input rows were
+// deferred-norm rows.
 struct QPartials {
     const float* p = nullptr;
     int splits = 0;
     const float* bias = nullptr;
     const float* scale = nullptr;
     const float* gamma = nullptr;
+    const float* row_ss = nullptr;
 };
 
 // Q (and for the self-attention K, V) read from a projection's bf16 output
@@ -544,6 +569,12 @@ int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v
         d.q_scale = qp->scale;
         d.q_gamma = qp->gamma;
         d.q_eps = c.eps;
+        if (qp->row_ss) {
+            d.q_row_ss = qp->row_ss;
+            d.q_row_tiles = c.hidden / 64;
+            d.q_row_n = c.hidden;
+            d.q_row_eps = c.eps;
+        }
     }
     // output straight into [B, S, H*64] (head_to_seq fused away)
     d.o_stride[0] = (int64_t)S * c.hidden;
@@ -578,6 +609,7 @@ int cross_q_partials(sf_rdt* m, const LayerIdx& L, int M, hipStream_t s, QPartia
     qp->bias = pf(m, L.cq_b);
     qp->scale = W.scale;
     qp->gamma = pf(m, L.cq_norm);
+    qp->row_ss = m->n_deferred ? m->row_ss : nullptr;
     return SF_OK;
 }
 
@@ -721,10 +753,11 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     } else {
         uint16_t* qkv[3] = {m->q, m->k, m->v};
         const int qk_g[3] = {L.q_norm, L.k_norm, -1};
-        SF_TRY(linear_heads(m, m->n, M, S, L.qkv_w, L.qkv_b, qkv, qk_g, 3, s, SF_BF16, true));
+        SF_TRY(linear_heads(m, m->n, M, S, L.qkv_w, L.qkv_b, qkv, qk_g, 3, s, SF_BF16, true, m->n_deferred));
         SF_TRY(attention(m, m->q, m->k, m->v, S, nullptr, m->a, false, s));
     }
-    SF_TRY(linear_add_norm(m, m->a, ad, M, L.proj_w, L.proj_b, L.norm2, m->n, ad, s));
+    SF_TRY(linear_add_norm(m, m->a, ad, M, L.proj_w, L.proj_b, L.norm2, m->n, ad, s, m->defer));
+    m->n_deferred = m->defer;
     // cross-attention branch: even blocks attend to language, odd to image
     // (dit_block.cu:369)
     const bool lang = (i % 2) == 0;
@@ -748,7 +781,7 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     } else {
         uint16_t* cq[1] = {m->q};
         const int cq_g[1] = {L.cq_norm};
-        SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s, SF_BF16, true));
+        SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s, SF_BF16, true, m->n_deferred));
         SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? m->cond_lang_rows : c.img_len,
                          lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,
                          lang ? c.lang_max : c.img_len));
@@ -758,7 +791,12 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     // writes the next block's norm1 (act16, the QKV input)
     const int F = (int)ffn_dim(c);
     SF_TRY(linear(m, m->n3, D, M, L.fc1_w, L.fc1_b, SF_ACT_GELU_TANH, m->h, F, fd, false, s, fd));
-    return linear_add_norm(m, m->h, fd, M, L.fc2_w, L.fc2_b, next_norm(m, i), m->n, ad, s);
+    // the next block's norm1 deferred; the final norm row-wide (its consumer,
+    // the final layer's fc1, takes normalised rows)
+    const bool defer_next = m->defer && i + 1 < c.layers;
+    SF_TRY(linear_add_norm(m, m->h, fd, M, L.fc2_w, L.fc2_b, next_norm(m, i), m->n, ad, s, defer_next));
+    m->n_deferred = defer_next;
+    return SF_OK;
 }
 
 // m->n = first norm applied to the residual m->x before block `first`.
@@ -766,6 +804,8 @@ int entry_norm(sf_rdt* m, int first, hipStream_t s) {
     const sf_rdt_config& c = m->cfg;
     const int D = c.hidden, M = c.batch * (c.horizon + 3);
     const int g = first < c.layers ? m->layers[first].norm1 : m->fnorm;
+    m->n_deferred = m->defer && first < c.layers;
+    if (m->n_deferred) return sf_rmsnorm_deferred(m->x, D, pf(m, g), m->n, m->act16, D, m->row_ss, M, D, s);
     return sf_rmsnorm(m->x, SF_F32, D, pf(m, g), m->n, m->act16, D, M, D, c.eps, s);
 }
 
@@ -910,6 +950,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     // fp16 once the block GEMMs leave the split-K regime (M > 160 rows)
     m->ffn_dtype = SF_F16;
     m->act16 = c.batch * (c.horizon + 3) <= 160 ? SF_BF16 : SF_F16;
+    m->defer = c.batch * (c.horizon + 3) <= 160 && c.hidden % 64 == 0 && c.hidden / 64 <= 64;
     build_param_table(m);
 
     const int64_t B = c.batch, D = c.hidden, T = c.horizon, S = T + 3, A = c.action_dim;
@@ -1009,6 +1050,7 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     bufs.push_back({&m->gemm_ws, std::max<size_t>(m->gemm_ws_bytes, 256)});
     m->rows_qkv = S * B > 160;
     if (m->rows_qkv) bufs.push_back({(void**)&m->qkv_rows, (size_t)(B * S * 3 * D * 2)});
+    if (m->defer) bufs.push_back({(void**)&m->row_ss, (size_t)(D / 64) * B * S * 4});
     if (S * B > 160) {   // fp16 copies of the block and final-layer projection weights
         for (int w : w16_params(m))
             m->codes16_bytes += align256((size_t)m->params[w].shape[0] * m->params[w].shape[1] * 2);

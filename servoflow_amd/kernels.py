@@ -48,6 +48,13 @@ def workspace_bytes(a, w):
     return abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d))
 
 
+def _row_scale(d, row_ss, row_n, row_eps):
+    """The activation rows are x * gamma of a deferred RMSNorm with tile sums
+    row_ss ([row_n / 64, M] fp32)."""
+    if row_ss is not None:
+        d.a_row_ss, d.a_row_tiles, d.a_row_n, d.a_row_eps = row_ss.data_ptr(), row_ss.shape[0], row_n, row_eps
+
+
 def _w16(d, w16):
     """An fp16 copy of the weights (weights_to_f16) for the library path."""
     if w16 is not None:
@@ -55,7 +62,8 @@ def _w16(d, w16):
 
 
 def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat16,
-         accumulate=False, w_scale=None, workspace="auto", w_codes16=None, w16=None):
+         accumulate=False, w_scale=None, workspace="auto", w_codes16=None, w16=None, row_ss=None, row_n=0,
+         row_eps=1e-6):
     """out[M,N] = act(a[M,K] w[N,K]^T + bias) (bf16 a; bf16 or int8 w with
     per-row fp32 w_scale).  accumulate adds into an fp32 `out`.  w_codes16:
     int8 w's codes as bf16 (int8_codes_to_bf16), read by the library path
@@ -68,6 +76,7 @@ def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat1
     d = _desc(a, w, bias, act, w_scale)
     d.w_codes16 = _p(w_codes16)
     _w16(d, w16)
+    _row_scale(d, row_ss, row_n, row_eps)
     d.epilogue = abi.SF_EPI_PLAIN
     d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), _DT[out.dtype]
     d.accumulate = 1 if accumulate else 0
@@ -76,7 +85,7 @@ def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat1
 
 
 def gemm_add_norm(a, w, bias, residual, gamma, eps=1e-6, act=abi.SF_ACT_NONE, w_scale=None,
-                  norm_dtype=torch.bfloat16, workspace="auto", round_product=False, w16=None):
+                  norm_dtype=torch.bfloat16, workspace="auto", round_product=False, w16=None, norm_ss=None):
     """residual (fp32 [M,N]) += act(a w^T + bias); returns
     rmsnorm(residual) * gamma in norm_dtype.  round_product: above 160 rows
     the branch output is stored in 16 bits before the add (bf16, or fp16
@@ -92,18 +101,21 @@ def gemm_add_norm(a, w, bias, residual, gamma, eps=1e-6, act=abi.SF_ACT_NONE, w_
     d.norm_gamma, d.norm_out = gamma.data_ptr(), out.data_ptr()
     d.norm_ldo, d.norm_dtype = out.stride(0), _DT[norm_dtype]
     d.round_product = 1 if round_product else 0
+    if norm_ss is not None:   # deferred form: out = residual * gamma, tile sums of squares to norm_ss
+        d.norm_ss = norm_ss.data_ptr()
     _run(d, a, workspace)
     return out
 
 
 def gemm_heads(a, w, bias, S, H, outs, gammas=(None, None, None), eps=1e-6, w_scale=None,
-               workspace="auto", round_product=False, w16=None):
+               workspace="auto", round_product=False, w16=None, row_ss=None, row_n=0, row_eps=1e-6):
     """Projection whose N columns are sections of H*64, written per head to
     outs[j] ([B,H,S,64] bf16 views) with optional per-head RMSNorm.
     round_product: above 160 rows the projection is stored in 16 bits
     before the norm (bf16, or fp16 with w16)."""
     d = _desc(a, w, bias, abi.SF_ACT_NONE, w_scale)
     _w16(d, w16)
+    _row_scale(d, row_ss, row_n, row_eps)
     d.epilogue = abi.SF_EPI_HEADS
     d.H, d.S, d.eps = H, S, eps
     d.round_product = 1 if round_product else 0
@@ -138,6 +150,18 @@ def weights_to_f16(ws):
         jobs[j].out, jobs[j].N, jobs[j].K = o.data_ptr(), w.shape[0], w.shape[1]
     abi.check(abi.lib().sf_weights_to_f16(jobs, len(ws), _stream(ws[0]) if ws else None), "sf_weights_to_f16")
     return outs
+
+
+def rmsnorm_deferred(x, gamma, out_dtype=torch.bfloat16):
+    """sf_rmsnorm_deferred on fp32 rows x [rows, cols]: (x * gamma in
+    out_dtype, tile sums of squares [cols / 64, rows] fp32)."""
+    rows, cols = x.shape
+    out = torch.empty(rows, cols, dtype=out_dtype, device=x.device)
+    ss = torch.empty(cols // 64, rows, dtype=torch.float32, device=x.device)
+    st = abi.lib().sf_rmsnorm_deferred(x.data_ptr(), x.stride(0), gamma.data_ptr(), out.data_ptr(), _DT[out_dtype],
+                                       out.stride(0), ss.data_ptr(), rows, cols, _stream(x))
+    abi.check(st, "sf_rmsnorm_deferred")
+    return out, ss
 
 
 def rmsnorm(x, gamma, eps=1e-6, out_dtype=torch.bfloat16, out=None):

@@ -560,20 +560,27 @@ def test_q_from_split_k_partials(B, H, Sk, vl, splits, scale, gamma, exact):
                                  None) == abi.SF_ENOTSUP
 
 
+@pytest.mark.parametrize("deferred", [False, True])
 @pytest.mark.parametrize("w8", [False, True])
-def test_q_partials_bit_identical_to_heads_epilogue(w8):
+def test_q_partials_bit_identical_to_heads_epilogue(w8, deferred):
     """The runtime's two routes to a batch-1 language cross-attention give
     the same bits: (a) the cross-q projection with the per-head RMSNorm
     epilogue (SF_EPI_HEADS, split-K + reduce) writing Q, then sf_attn_fwd;
     (b) the projection's partials (SF_EPI_PARTIALS) finished inside
     sf_attn_fwd (q_partials) -- the same sums, scale, bias and norm in the
-    same order."""
+    same order.  deferred: the projection's input rows are x * gamma of a
+    deferred RMSNorm (sf_rmsnorm_deferred), scaled per row by a_row_ss on
+    route (a) and q_row_ss on route (b)."""
     import ctypes
     from servoflow_amd import kernels as Kn
     dev = torch.device(DEV)
     B, H, S, D, Sk = 1, 32, 67, 2048, 1024
     g = torch.Generator(device=dev).manual_seed(41)
     a = torch.randn(B * S, D, device=dev, generator=g).to(torch.bfloat16)
+    rss = None
+    if deferred:
+        x = torch.randn(B * S, D, device=dev, generator=g) * 3.0
+        a, rss = Kn.rmsnorm_deferred(x, torch.rand(D, device=dev, generator=g) + 0.5)
     if w8:
         w = torch.randint(-127, 128, (D, D), device=dev, generator=g, dtype=torch.int8)
         ws = torch.rand(D, device=dev, generator=g) * 2e-4 + 1e-4
@@ -586,7 +593,7 @@ def test_q_partials_bit_identical_to_heads_epilogue(w8):
     v = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
     vl = torch.tensor([517], dtype=torch.int32, device=dev)
     q = torch.empty(B, H, S, 64, device=dev, dtype=torch.bfloat16)
-    Kn.gemm_heads(a, w, bias, S, H, [q], (gam,), w_scale=ws)
+    Kn.gemm_heads(a, w, bias, S, H, [q], (gam,), w_scale=ws, row_ss=rss, row_n=D)
     ref = attention(q, k, v, out_dtype=torch.float32, valid_len=vl)
     d = Kn._desc(a, w, None, abi.SF_ACT_NONE, ws)
     d.epilogue = abi.SF_EPI_PARTIALS
@@ -599,6 +606,8 @@ def test_q_partials_bit_identical_to_heads_epilogue(w8):
     ad.q_partials, ad.q_splits = part.data_ptr(), ns
     ad.q_bias, ad.q_scale, ad.q_gamma, ad.q_eps = bias.data_ptr(), ws.data_ptr() if ws is not None else None, \
         gam.data_ptr(), 1e-6
+    if deferred:
+        ad.q_row_ss, ad.q_row_tiles, ad.q_row_n, ad.q_row_eps = rss.data_ptr(), rss.shape[0], D, 1e-6
     abi.check(abi.lib().sf_attn_fwd(ctypes.byref(ad), None, k.data_ptr(), v.data_ptr(), out.data_ptr(), None, 0,
                                     torch.cuda.current_stream().cuda_stream), "attention from partials")
     torch.cuda.synchronize()

@@ -566,6 +566,96 @@ def test_gemm_fp16_activations_library_path():
     close(got, O.linear(O.bf16_round(a), w, b), "fp16-activation library gemm")
 
 
+def _tile_ss(x):
+    """Per-64-column sums of squares of fp32 rows x [M, N]: [N / 64, M] (fp64)."""
+    x64 = np.asarray(x, np.float64)
+    return (x64.reshape(x64.shape[0], -1, 64) ** 2).sum(-1).T
+
+
+@pytest.mark.parametrize("M", [1, 67, 134])
+def test_rmsnorm_deferred(M):
+    """sf_rmsnorm_deferred: x * gamma rounded once to bf16 (bit for bit the
+    rounding of the fp32 product) and the per-tile sums of squares; the
+    rows normalised with them equal the row-wide RMSNorm."""
+    N = 2048
+    x = O.randn(191 + M, (M, N))
+    gm = 1.0 + O.randn(192, (N,), 0.1)
+    out, ss = K.rmsnorm_deferred(dev(x, torch.float32), dev(gm, torch.float32))
+    got, gss = host(out), host(ss)
+    assert np.array_equal(got, O.bf16_round(x * gm))
+    assert np.allclose(gss, _tile_ss(x), rtol=1e-5, atol=0)
+    s = 1.0 / np.sqrt(gss.sum(0) / N + 1e-6)
+    close(x * gm * s[:, None], O.rms_norm(x, gm), "deferred rows normalised", rel=1e-6)
+
+
+@pytest.mark.parametrize("w8", [False, True])
+@pytest.mark.parametrize("M", [67, 134])
+def test_gemm_deferred_norm_producer_and_consumers(M, w8):
+    """The deferred RMSNorm on the split-K path.  Producer (SF_EPI_ADD_NORM
+    with norm_ss): the residual add is bit for bit the row-wide kernel's,
+    norm_out is bf16(x * gamma) and norm_ss the per-tile sums of squares.
+    Consumers (a_row_ss): a plain fp32 product and the per-head epilogue of
+    x * gamma rows scaled by the row's 1/rms before the bias, against the
+    oracle's RMSNorm-then-linear on the same rows."""
+    N, Kd, H, S = 2048, 2048, 32, 67
+    a = rounded(201, (M, Kd))
+    w, wdev, sdev = _library_weights(202, N, Kd, w8)
+    b = O.randn(203, (N,), 0.02)
+    g2 = 1.0 + O.randn(204, (N,), 0.1)
+    x = O.randn(205, (M, N))
+    xr, xd = dev(x, torch.float32), dev(x, torch.float32)
+    ref_n = K.gemm_add_norm(dev(a), wdev, dev(b, torch.float32), xr, dev(g2, torch.float32), w_scale=sdev)
+    ss = torch.empty(N // 64, M, device=DEV, dtype=torch.float32)
+    un = K.gemm_add_norm(dev(a), wdev, dev(b, torch.float32), xd, dev(g2, torch.float32), w_scale=sdev, norm_ss=ss)
+    x_new = host(xd)
+    assert np.array_equal(x_new, host(xr))                      # the same residual add
+    assert np.array_equal(host(un), O.bf16_round(x_new * g2))   # not yet normalised
+    assert np.allclose(host(ss), _tile_ss(x_new), rtol=1e-5, atol=0)
+    s = 1.0 / np.sqrt(host(ss).sum(0) / N + 1e-6)
+    # the two forms round to bf16 on either side of the 1/rms scale: within
+    # two bf16 ulps of each other
+    lhs, rhs = host(un) * s[:, None], host(ref_n)
+    assert np.all(np.abs(lhs - rhs) <= np.abs(rhs) * 2.0 ** -7 + 2.0 ** -12)
+    assert mean_rel(lhs, rhs) < 3e-3
+    # consumers of the deferred rows
+    a2 = O.bf16_round(x_new * g2)
+    w2, w2dev, s2dev = _library_weights(206, N, Kd, w8)
+    b2 = O.randn(207, (N,), 0.02)
+    got = host(K.gemm(un, w2dev, dev(b2, torch.float32), out_dtype=torch.float32, w_scale=s2dev, row_ss=ss, row_n=N))
+    ref = O.linear(a2, w2) * s[:, None].astype(np.float32) + b2
+    close(got, ref, f"deferred consumer M={M} w8={w8}")
+    w3, w3dev, s3dev = _library_weights(208, N, Kd, w8)
+    b3 = O.randn(209, (N,), 0.02)
+    gq = 1.0 + O.randn(210, (64,), 0.1)
+    qh = torch.empty(M // S if M % S == 0 else 1, H, S, 64, device=DEV, dtype=torch.bfloat16)
+    if M % S == 0:
+        K.gemm_heads(un, w3dev, dev(b3, torch.float32), S, H, [qh], (dev(gq, torch.float32),), w_scale=s3dev,
+                     row_ss=ss, row_n=N)
+        pre = O.linear(a2, w3) * s[:, None].astype(np.float32) + b3
+        refq = O.rms_norm(O.seq_to_head(pre.reshape(M // S, S, N), H, 64), gq)
+        gh = host(qh)
+        assert np.all(np.abs(gh - refq) <= np.abs(refq) * 2.0 ** -7 + 1e-3)
+        assert mean_rel(gh, refq) < 2e-3
+
+
+def test_gemm_deferred_norm_contract():
+    """The deferred norm runs on the split-K path only (a library-path or
+    workspace-free call is SF_ENOTSUP) and needs N a multiple of 64."""
+    import ctypes
+    for M, ws in ((1072, True), (67, False)):
+        a = torch.zeros(M, 256, dtype=torch.bfloat16, device=DEV)
+        w = torch.zeros(128, 256, dtype=torch.bfloat16, device=DEV)
+        out = torch.empty(M, 128, dtype=torch.float32, device=DEV)
+        ss = torch.zeros(4, M, dtype=torch.float32, device=DEV)
+        d = K._desc(a, w, None, abi.SF_ACT_NONE, None)
+        d.epilogue, d.C, d.ldc, d.c_dtype = abi.SF_EPI_PLAIN, out.data_ptr(), 128, abi.SF_F32
+        d.a_row_ss, d.a_row_tiles, d.a_row_n, d.a_row_eps = ss.data_ptr(), 4, 256, 1e-6
+        wsb = torch.empty(max(abi.lib().sf_gemm_workspace_bytes(ctypes.byref(d)), 16), dtype=torch.uint8, device=DEV)
+        if ws:
+            d.workspace, d.workspace_bytes = wsb.data_ptr(), wsb.numel()
+        assert abi.lib().sf_gemm(ctypes.byref(d), torch.cuda.current_stream().cuda_stream) == abi.SF_ENOTSUP, M
+
+
 def test_weights_to_f16_exact():
     """sf_weights_to_f16: int8 codes widen to fp16 exactly (all 256 codes);
     bf16 weights round to the nearest fp16, bit for bit torch's conversion --
