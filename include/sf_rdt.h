@@ -104,9 +104,10 @@ typedef struct sf_rdt_config {
     int32_t batch;
     int32_t int8_weights;        /* block projections as int8 + fp32 row scale;
                                     at batch * (horizon + 3) > 160 the runtime
-                                    also holds bf16 copies of the six block
-                                    projections' codes (2 bytes per weight),
-                                    rewritten at the start of every pass */
+                                    (int8 or not) also holds fp16 copies of the
+                                    block and final-layer matrices (2 bytes per
+                                    weight), rewritten before the first pass
+                                    after the parameters may have changed */
     float eps;                   /* 1e-6 */
     int32_t mlp_ratio;           /* FFN hidden = mlp_ratio * hidden (1; 0 means 1) */
 } sf_rdt_config;

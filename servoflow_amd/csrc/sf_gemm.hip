@@ -30,7 +30,11 @@
 //   weight loads at once, stages its activation slice in LDS once for its
 //   waves, and writes fp32 partial sums; a reduce kernel sums the K slices in
 //   a fixed order (deterministic) and applies the epilogue, including the
-//   residual add + RMSNorm that follows a block branch.
+//   residual add + RMSNorm that follows a block branch.  That RMSNorm can be
+//   deferred (norm_ss): the reduce then runs over 64-column tiles, stores
+//   x * gamma and each tile's per-row sum of squares, and the consuming
+//   projection (a_row_ss) applies rsqrt(sum / n + eps) to its contraction,
+//   since (s a) W^T = s (a W^T) -- no kernel waits for a whole row.
 //   library path (M > 160, caller workspace): at those sizes the product is
 //   MFMA-bound, a plain library GEMM: hipBLASLt computes it chunk by chunk
 //   (<= 8192 rows) and the same epilogue kernels finish it.  What hipBLASLt
@@ -40,7 +44,7 @@
 //   norm or the residual add + RMSNorm reads (round_product); otherwise the
 //   fp32 product.  Operands are bf16, or -- with fp16 activations and the
 //   caller's fp16 copy of the weights (w16_f16; int8 codes widened exactly,
-//   bf16 weights rounded, sf_weights_to_f16, once per model pass) -- fp16,
+//   bf16 weights rounded, sf_weights_to_f16, once per weight change) -- fp16,
 //   and then the 16-bit outputs are fp16.  int8 weights without a copy are
 //   widened to bf16 codes in the workspace on every call.
 //   single-pass path (no workspace): one workgroup of 8 waves per 16 or 64
