@@ -308,8 +308,11 @@ typedef struct sf_gemm_desc {
                                 library path (M > 160) multiplies the fp16 activations by it in
                                 fp16 -- no rounding of the activations to bf16 -- and its 16-bit
                                 products (round_product, and a plain C written by hipBLASLt, which
-                                must then be SF_F16) are fp16.  Ignored on the other paths, which
-                                read W itself (SF_EINVAL when w_codes16 is NULL on this path) */
+                                must then be SF_F16) are fp16 (SF_EINVAL when w_codes16 is NULL on
+                                this path).  The split-K path (M <= 160) reads the copy instead of
+                                W when one is given: the operands it would otherwise form from W in
+                                registers, so the same results without the conversion.  The
+                                single-pass path reads W itself */
     /* Deferred RMSNorm (split-K path, M <= 160 with a workspace; SF_ENOTSUP
      * elsewhere; N a multiple of 64).  norm_ss (SF_EPI_ADD_NORM): instead of
      * the normalised row, norm_out[m] = C[m] * norm_gamma after the residual

@@ -78,7 +78,11 @@ constexpr int kGemmThreads = 512;   // 8 waves
 // (hi, lo) pair, two MFMAs per weight fragment.  fp16: fp16 MFMAs, with the
 // bf16 weight fragment converted to fp16 in registers (exact for bf16
 // magnitudes in [2^-14, 65504], to within 2^-25 below; int8 codes exact).
-enum ActKind { kActBF16 = 0, kActF32 = 1, kActF16 = 2 };
+// kActF16W16 (split-K path only): fp16 activations and the caller's fp16
+// copy of the weights (2 bytes per weight, loaded as bf16 weights are),
+// used as MFMA operands as they are -- the same operands kActF16 forms in
+// registers from bf16 weights or int8 codes, so the same products.
+enum ActKind { kActBF16 = 0, kActF32 = 1, kActF16 = 2, kActF16W16 = 3 };
 
 struct GemmArgs {
     const void* a;         // [M][lda] bf16, fp32 or fp16 (ActKind)
@@ -122,7 +126,10 @@ __device__ __forceinline__ f16x8 bf16x8_to_f16x8(u32x4 w) {
     return u32x4_as_f16x8(o);
 }
 
-// Eight int8 codes -> fp16x8 (exact).
+// Eight int8 codes -> fp16x8 (exact).  (Building 1024 + (code + 128) as an
+// fp16 bit pattern with one byte permute per two codes and subtracting 1152
+// in packed fp16 is exact too, but made the int8 batch-1 loop slower:
+// 11.83 vs 11.75 ms.)
 __device__ __forceinline__ f16x8 i8x8_to_f16x8(uint2 raw) {
     u32x4 o;
 #pragma unroll
@@ -362,8 +369,10 @@ __device__ __forceinline__ void lds_barrier() {
 // run fp16 MFMAs on weight fragments converted in registers.
 template <int MB, int KT, int NW, bool W8, int NB, int AK>
 __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
+    static_assert(!(W8 && AK == kActF16W16), "an fp16 weight copy is 2 bytes per weight");
     constexpr bool A32 = AK == kActF32;
-    constexpr bool A16 = AK == kActF16;
+    constexpr bool A16 = AK == kActF16 || AK == kActF16W16;
+    constexpr bool WH = AK == kActF16W16;
     constexpr int kSkThreads = 64 * NW;
     constexpr int kSkRows = 16 * NW * NB;     // weight rows (output columns) per workgroup
     constexpr int MR = 16 * MB;
@@ -452,7 +461,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_splitk_kernel(const SkArgs g) {
             f16x8 wh[A16 ? NB : 1];
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                if constexpr (A16) {
+                if constexpr (WH) {
+                    wh[nb] = u32x4_as_f16x8(wv[nb][t]);
+                } else if constexpr (A16) {
                     if constexpr (W8) wh[nb] = i8x8_to_f16x8(wq[nb][t]);
                     else wh[nb] = bf16x8_to_f16x8(wv[nb][t]);
                 } else {
@@ -958,6 +969,11 @@ void launch_splitk_w(const SkArgs& a, const SkPlan& p, int ak, hipStream_t s) {
     } else if (ak == kActF16) {
         if (p.kt == 256) launch_splitk_mb<256, 2, W8, 2, kActF16>(a, p, s);
         else launch_splitk_mb<512, 4, W8, 1, kActF16>(a, p, s);
+    } else if (ak == kActF16W16) {
+        if constexpr (!W8) {
+            if (p.kt == 256) launch_splitk_mb<256, 2, false, 2, kActF16W16>(a, p, s);
+            else launch_splitk_mb<512, 4, false, 1, kActF16W16>(a, p, s);
+        }
     } else if (p.kt == 256) {
         launch_splitk_mb<256, 2, W8, 2, kActBF16>(a, p, s);
     } else {
@@ -1453,6 +1469,24 @@ int gemm_single_pass(const sf_gemm_desc* d, const sfk::EpiArgs& e, hipStream_t s
 }
 }  // namespace
 
+// The split-K partial kernel over the descriptor's weights: W itself, or,
+// with fp16 activations, the caller's fp16 copy when one is given
+// (w16_f16 + w_codes16, [N][K]) -- the operands the kernel would otherwise
+// form in registers, read without the conversion.
+static int launch_splitk_desc(const sf_gemm_desc* d, sfk::SkArgs& a, const sfk::SkPlan& p, hipStream_t s) {
+    if (d->a_dtype == SF_F16 && d->w16_f16 && d->w_codes16) {
+        if (!al16(d->w_codes16)) return SF_EINVAL;
+        a.w = d->w_codes16;
+        a.ldw = d->K;
+        sfk::launch_splitk(a, p, false, sfk::kActF16W16, s);
+        return SF_OK;
+    }
+    a.w = d->W;
+    a.ldw = d->ldw;
+    sfk::launch_splitk(a, p, d->w_dtype == SF_I8, act_kind(d), s);
+    return SF_OK;
+}
+
 // Leading dimensions hipBLASLt sees on the library path: int8 weights are
 // widened into a [N][K] copy, fp32 activations rounded into [chunk][K].
 // fp16 library path: fp16 activations with the caller's fp16 weight copy
@@ -1600,12 +1634,10 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
         if (!al16(d->workspace)) return SF_EINVAL;
         sfk::SkArgs a{};
         a.a = d->A;
-        a.w = d->W;
         a.part = static_cast<float*>(d->workspace);
         a.lda = d->lda;
-        a.ldw = d->ldw;
         a.M = d->M; a.N = d->N; a.K = d->K;
-        sfk::launch_splitk(a, p, d->w_dtype == SF_I8, act_kind(d), s);
+        SF_CHECK_OK(launch_splitk_desc(d, a, p, s));
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
     }
     if (d->workspace && !p.split && splittable(d)) {
@@ -1694,12 +1726,10 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     if (!al16(d->workspace)) return SF_EINVAL;
     sfk::SkArgs a{};
     a.a = d->A;
-    a.w = d->W;
     a.part = static_cast<float*>(d->workspace);
     a.lda = d->lda;
-    a.ldw = d->ldw;
     a.M = d->M; a.N = d->N; a.K = d->K;
-    sfk::launch_splitk(a, p, d->w_dtype == SF_I8, act_kind(d), s);
+    SF_CHECK_OK(launch_splitk_desc(d, a, p, s));
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;
     e.part = a.part;
     e.splits = p.splits;

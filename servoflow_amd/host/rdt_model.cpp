@@ -183,9 +183,10 @@ struct sf_rdt {
     size_t attn_ws_bytes = 0;
     void* gemm_ws = nullptr;       // split-K partial sums, shared by the stream's GEMMs
     size_t gemm_ws_bytes = 0;
-    // Above 160 rows (the library path): fp16 copies of every block's six
-    // projection weights and of the final layer's two (int8 codes widened
-    // exactly, bf16 weights rounded to fp16; sf_weights_to_f16, up to eight
+    // fp16 copies of projection weights (w16_params: above 160 rows every
+    // block's six and the final layer's two; at most 160 rows with bf16
+    // weights the ones multiplying fp16 inputs; int8 codes widened exactly,
+    // bf16 weights rounded to fp16; sf_weights_to_f16, up to eight
     // matrices per launch), made before the first pass and again before
     // the first pass after the parameters may have changed (w16_stale), on
     // the pass's stream and outside any graph capture -- not once per loop:
@@ -613,14 +614,28 @@ int cross_q_partials(sf_rdt* m, const LayerIdx& L, int M, hipStream_t s, QPartia
     return SF_OK;
 }
 
-// The projection weights that get fp16 copies above 160 rows: every
-// block's six and the final layer's two (their K a multiple of 16).
+// The projection weights that get fp16 copies.  Above 160 rows (the
+// library path): every block's six and the final layer's two.  At most 160
+// rows, with bf16 weights: the matrices whose inputs are fp16 there -- each
+// block's fc1 and fc2 and the final layer's fc2 -- so the split-K kernel
+// reads fp16 operands instead of converting every bf16 fragment in
+// registers (the same operands, so the same results); int8 weights keep
+// their 1-byte codes.  Only matrices with K a multiple of 16.
 std::vector<int> w16_params(const sf_rdt* m) {
+    const sf_rdt_config& c = m->cfg;
     std::vector<int> ws;
-    for (const LayerIdx& L : m->layers)
-        for (int w : block_weights(L)) ws.push_back(w);
-    ws.push_back(m->f1w);
-    ws.push_back(m->f2w);
+    if (c.batch * (c.horizon + 3) > 160) {
+        for (const LayerIdx& L : m->layers)
+            for (int w : block_weights(L)) ws.push_back(w);
+        ws.push_back(m->f1w);
+        ws.push_back(m->f2w);
+    } else if (!c.int8_weights) {
+        for (const LayerIdx& L : m->layers) {
+            ws.push_back(L.fc1_w);
+            ws.push_back(L.fc2_w);
+        }
+        ws.push_back(m->f2w);
+    }
     std::vector<int> out;
     for (int w : ws)
         if (m->params[w].shape[1] % 16 == 0) out.push_back(w);
@@ -1051,11 +1066,9 @@ extern "C" int sf_rdt_create(const sf_rdt_config* cfg, sf_rdt** out) {
     m->rows_qkv = S * B > 160;
     if (m->rows_qkv) bufs.push_back({(void**)&m->qkv_rows, (size_t)(B * S * 3 * D * 2)});
     if (m->defer) bufs.push_back({(void**)&m->row_ss, (size_t)(D / 64) * B * S * 4});
-    if (S * B > 160) {   // fp16 copies of the block and final-layer projection weights
-        for (int w : w16_params(m))
-            m->codes16_bytes += align256((size_t)m->params[w].shape[0] * m->params[w].shape[1] * 2);
-        if (m->codes16_bytes) bufs.push_back({(void**)&m->codes16, m->codes16_bytes});
-    }
+    for (int w : w16_params(m))   // fp16 weight copies
+        m->codes16_bytes += align256((size_t)m->params[w].shape[0] * m->params[w].shape[1] * 2);
+    if (m->codes16_bytes) bufs.push_back({(void**)&m->codes16, m->codes16_bytes});
     std::vector<size_t> boff(bufs.size());
     for (size_t i = 0; i < bufs.size(); ++i) {
         boff[i] = off;

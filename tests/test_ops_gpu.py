@@ -535,6 +535,48 @@ def test_gemm_fp16_activations(M, N, Kd, ws, w8):
           rel=1e-5)
 
 
+@pytest.mark.parametrize("w8", [False, True])
+@pytest.mark.parametrize("M,N,Kd", [(67, 2048, 2048), (160, 192, 4096), (5, 128, 512)])
+def test_gemm_splitk_reads_f16_copy_bit_identically(M, N, Kd, w8):
+    """At most 160 rows with fp16 activations, an fp16 weight copy (w16,
+    weights_to_f16) makes the split-K kernel read fp16 operands instead of
+    converting every bf16 fragment (or int8 code) in registers.  Both form
+    the same operands, so every epilogue gives the same bits with and without
+    the copy: GELU + fp16 C, fp32 C, residual add + norm (x and the norm
+    output), per-head outputs with RMSNorm; without a workspace (the
+    single-pass path reads W itself) too."""
+    a = dev(f16r(O.randn(181 + M, (M, Kd))), torch.float16)
+    if w8:
+        q, s = O.quantize_int8_rows(O.randn(182, (N, Kd), 0.02))
+        wdev, sdev = dev(q, torch.int8), dev(s, torch.float32)
+    else:
+        w = rounded(182, (N, Kd), 0.02)
+        w[0, :4] = [1e-6, -3e-7, 2.0 ** -24, 0.0]   # below fp16's normal range: rounded alike
+        wdev, sdev = dev(w), None
+    (w16,) = K.weights_to_f16([wdev])
+    b = dev(O.randn(183, (N,), 0.02), torch.float32)
+    for ws in ("auto", None):
+        for act, od in ((abi.SF_ACT_GELU_TANH, torch.float16), (abi.SF_ACT_NONE, torch.float32)):
+            ref = host(K.gemm(a, wdev, b, act, out_dtype=od, w_scale=sdev, workspace=ws))
+            got = host(K.gemm(a, wdev, b, act, out_dtype=od, w_scale=sdev, workspace=ws, w16=w16))
+            assert np.array_equal(got, ref), (ws, act)
+    g = dev(1.0 + O.randn(184, (N,), 0.1), torch.float32)
+    x = O.randn(185, (M, N))
+    x1, x2 = dev(x, torch.float32), dev(x, torch.float32)
+    n1 = host(K.gemm_add_norm(a, wdev, b, x1, g, w_scale=sdev, norm_dtype=torch.float16))
+    n2 = host(K.gemm_add_norm(a, wdev, b, x2, g, w_scale=sdev, norm_dtype=torch.float16, w16=w16))
+    assert np.array_equal(host(x1), host(x2)) and np.array_equal(n1, n2)
+    if N % 192 == 0:
+        H, S = N // 192, M
+        outs1 = [torch.empty(1, H, S, 64, dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+        outs2 = [torch.empty(1, H, S, 64, dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+        gam = dev(1.0 + O.randn(186, (64,), 0.1), torch.float32)
+        K.gemm_heads(a, wdev, b, S, H, outs1, gammas=(gam, gam, None), w_scale=sdev)
+        K.gemm_heads(a, wdev, b, S, H, outs2, gammas=(gam, gam, None), w_scale=sdev, w16=w16)
+        for o1, o2 in zip(outs1, outs2):
+            assert torch.equal(o1, o2)
+
+
 @pytest.mark.parametrize("ws", PATHS)
 def test_gemm_fp16_outputs(ws):
     """fp16 C (the FFN hidden) and fp16 norm output (norm3): the fp32
