@@ -103,10 +103,13 @@ def time_graph(fn, steps, warmup, reps=20):
 COLD_SET_BYTES = 512 << 20
 
 
-def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=False, reps=20):
+def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=False, reps=20, v16=None):
     """Graph-timed cross-attention op (exact_pv: the bf16 (hi, lo) P.V form
     instead of the default fp16 one): `reps` calls per graph, call i reading
-    K/V copy i % n_sets (COLD_SET_BYTES)."""
+    K/V copy i % n_sets (COLD_SET_BYTES).  v16 (default: the cross-attention
+    calls, Sk > 128, on the fp16 form): V given in fp16, as the model runtime
+    holds its cached V for that form (sf_attn_desc.v_f16); the self-attention
+    (Sk <= 128) reads bf16 V from its projection."""
     import numpy as np
     import torch
 
@@ -119,7 +122,10 @@ def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=Fals
     n_sets = int(min(reps, max(1, -(-COLD_SET_BYTES // kv_bytes))))
     q = torch.randn(B, H, Sq, 64, device=dev, generator=g).to(torch.bfloat16)
     ks = [torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16) for _ in range(n_sets)]
-    vs = [torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16) for _ in range(n_sets)]
+    if v16 is None:
+        v16 = Sk > 128 and not exact_pv
+    vdt = torch.float16 if v16 else torch.bfloat16
+    vs = [torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16).to(vdt) for _ in range(n_sets)]
     # output straight into [B, Sq, H*D], the layout the block's projection reads
     out = torch.empty(B, Sq, H, 64, device=dev, dtype=torch.bfloat16).permute(0, 2, 1, 3)
     vl = None
@@ -678,8 +684,9 @@ def main():
             "traffic": TRAFFIC_B1_IMAGE_BYTES,
             "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE on bench.py --profile-roofline, "
                               "profiles/cross_attention_image_roofline.md",
-            "kernel": "cross-attention op (attn_ring_kernel, fp16 P.V form, + attn_merge_kernel), 1x32x67x4374x64 "
-                      f"bf16, {img1['bytes']} algorithmic bytes per launch, {img1['us']:.2f} us",
+            "kernel": "cross-attention op (attn_ring_kernel, fp16 P.V form, + attn_merge_kernel), 1x32x67x4374x64, "
+                      "bf16 Q/K and the fp16 V the runtime caches for that form, "
+                      f"{img1['bytes']} algorithmic bytes per launch, {img1['us']:.2f} us",
         },
         "cpu_baseline": cpu,
         "extra": extra,

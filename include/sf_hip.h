@@ -169,6 +169,15 @@ typedef struct sf_attn_desc {
     int32_t q_row_tiles;
     int32_t q_row_n;
     float q_row_eps;
+    /* v_f16 != 0 (in_dtype SF_BF16, exact_pv 0): V is given in fp16 while Q
+     * and K are bf16 -- a cross-attention K/V cache whose V was converted
+     * once (sf_bf16_to_f16_below) instead of per tile.  The fast P.V form
+     * multiplies fp16 V by P rounded to fp16, exactly as it does after
+     * converting a bf16 V itself, so a V converted with the same rounding
+     * gives the same bits; the short-key kernel (Sk <= 128) takes fp16 V
+     * with P as an fp16 (hi, lo) pair.  SF_ENOTSUP with another in_dtype or
+     * with exact_pv. */
+    int32_t v_f16;
 } sf_attn_desc;
 
 /* Fills a descriptor for contiguous [B,H,S,D] tensors (the layout

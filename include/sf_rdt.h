@@ -78,6 +78,14 @@ typedef struct sf_absmax_job {
     float* out;
 } sf_absmax_job;
 int sf_absmax_bf16_batched(const sf_absmax_job* jobs, int32_t count, void* stream);
+/* In place bf16 -> fp16 (round to nearest even) of every job's buffer whose
+ * *out -- the max |x| sf_absmax_bf16_batched merged for the same job -- is
+ * below `limit` (> 0, else SF_EINVAL; a NaN maximum is not below any
+ * limit); the other buffers stay bf16.  The
+ * runtime converts each layer's cached V this way with limit 65504, the
+ * rule by which it picks the fp16 P.V form, so the attention reads fp16 V
+ * (sf_attn_desc.v_f16) instead of converting every tile of every step. */
+int sf_bf16_to_f16_below(const sf_absmax_job* jobs, int32_t count, float limit, void* stream);
 
 /* ---- model runtime (libsf_rdt.so) ---------------------------------------- */
 
@@ -127,9 +135,11 @@ int sf_rdt_init_random(sf_rdt* m, uint64_t seed, float std, void* stream);
 int32_t sf_rdt_num_params(const sf_rdt* m);
 int sf_rdt_param_info(const sf_rdt* m, int32_t idx, const char** name, int32_t* dtype,
                       int32_t* ndim, int64_t shape[4]);
-/* Device pointer to parameter idx.  Above 160 projection rows (batch * 67)
- * the runtime multiplies fp16 copies of the block and final-layer weights;
- * they are rebuilt before the first pass after this call, after
+/* Device pointer to parameter idx.  The runtime multiplies fp16 copies of
+ * some weights (above 160 projection rows, batch * 67, every block and
+ * final-layer matrix; at most 160 rows with bf16 weights, the FFN matrices,
+ * whose inputs are fp16); they are rebuilt before the first pass after this
+ * call, after
  * sf_rdt_init_random / sf_rdt_load_safetensors, and after
  * sf_rdt_params_changed -- a caller that writes through a pointer it
  * obtained before a pass must call sf_rdt_params_changed before the next
@@ -206,7 +216,10 @@ int sf_rdt_infer(sf_rdt* m, uint64_t frame_id, const void* lang_tokens, const in
  * condition's encode per new condition); asking here does the same. */
 int32_t sf_rdt_pv_exact(sf_rdt* m, int32_t layer);
 
-/* Cross-attention K or V cache of block `layer` ([B, H, S, 64] bf16). */
+/* Cross-attention K or V cache of block `layer` ([B, H, S, 64]): K in
+ * bf16; V in fp16 when the layer runs the fp16 P.V form
+ * (sf_rdt_pv_exact == 0: converted once when the condition was set), else
+ * bf16. */
 void* sf_rdt_cache_ptr(sf_rdt* m, int32_t layer, int32_t which_v);
 
 /* ---- checkpoints (safetensors) ------------------------------------------- */

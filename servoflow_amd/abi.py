@@ -62,6 +62,7 @@ class AttnDesc(ctypes.Structure):
         ("q_row_tiles", ctypes.c_int32),
         ("q_row_n", ctypes.c_int32),
         ("q_row_eps", ctypes.c_float),
+        ("v_f16", ctypes.c_int32),
     ]
 
 
@@ -191,6 +192,8 @@ def lib() -> ctypes.CDLL:
     L.sf_heads_bf16.restype = ctypes.c_int
     L.sf_absmax_bf16_batched.argtypes = [ctypes.POINTER(AbsmaxJob), i32, vp]
     L.sf_absmax_bf16_batched.restype = ctypes.c_int
+    L.sf_bf16_to_f16_below.argtypes = [ctypes.POINTER(AbsmaxJob), i32, ctypes.c_float, vp]
+    L.sf_bf16_to_f16_below.restype = ctypes.c_int
     L.sf_gemm_set_algo_timing.argtypes = [i32]
     L.sf_gemm_set_algo_timing.restype = ctypes.c_int
     L.sf_strerror.argtypes = [ctypes.c_int]

@@ -33,13 +33,15 @@ def make_desc(q, k, v, out, scale=0.0, is_causal=False, valid_len=None, num_spli
     d = abi.AttnDesc()
     d.B, d.H, d.Sq, d.Sk, d.D = B, H, Sq, Sk, D
     d.scale = float(scale)
-    d.in_dtype = _DT[q.dtype]
-    if q.dtype == torch.float16 and k.dtype == torch.bfloat16:   # fp16 Q rows against bf16 K / V
-        d.in_dtype = abi.SF_BF16
+    d.in_dtype = _DT[k.dtype]
+    if q.dtype == torch.float16 and k.dtype == torch.bfloat16:   # fp16 Q rows against bf16 K
         d.q_f16 = 1
-    elif k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError(f"dtypes q {q.dtype} k {k.dtype} v {v.dtype}: K and V must match Q "
-                         "(or Q fp16 with bf16 K and V)")
+    elif q.dtype != k.dtype:
+        raise ValueError(f"dtypes q {q.dtype} k {k.dtype}: K must match Q (or Q fp16 with bf16 K)")
+    if v.dtype == torch.float16 and k.dtype == torch.bfloat16:   # fp16 V against bf16 K (fp16 P.V form)
+        d.v_f16 = 1
+    elif v.dtype != k.dtype:
+        raise ValueError(f"dtypes k {k.dtype} v {v.dtype}: V must match K (or V fp16 with bf16 K)")
     d.out_dtype = _DT[out.dtype]
     d.is_causal = 1 if is_causal else 0
     d.num_splits = int(num_splits)
@@ -83,7 +85,8 @@ def attention(q, k, v, out=None, scale=0.0, is_causal=False, valid_len=None, num
     (epsilon qk_eps) applied to each Q / K row as it is loaded (bf16 or fp16
     inputs; K only for key sets of at most 128).  An fp16 q with bf16 k and
     v runs the bf16 contraction on Q rounded to bf16 after its norm
-    (sf_attn_desc.q_f16)."""
+    (sf_attn_desc.q_f16).  An fp16 v with bf16 q / k runs the fp16 P.V
+    form on V as given (sf_attn_desc.v_f16)."""
     if out is None:
         od = out_dtype or q.dtype
         out = torch.empty(q.shape, dtype=od, device=q.device)

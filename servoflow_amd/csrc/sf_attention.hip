@@ -466,8 +466,10 @@ __device__ __forceinline__ void ring_wait_k() {
 // (kQB on the (split x chunk, H, B) grid; 1 on the XCD-grouped 1-D grid).
 // kQP (QB = 1, bf16): Q is finished here from its projection's split-K
 // partials (sum, scale, bias, per-head RMSNorm, bf16) instead of loaded.
-template <bool kExactPV, bool kF16, int QB, bool kQP = false>
+// kVH (bf16 Q/K, fp16 form): V is given in fp16 and used as loaded.
+template <bool kExactPV, bool kF16, int QB, bool kQP = false, bool kVH = false>
 __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
+    static_assert(!(kVH && (kExactPV || kF16)), "fp16 V: the fp16 P.V form of bf16 Q/K");
     using v8 = typename In16<kF16>::v8;
     constexpr int QR = 16 * QB;
     __shared__ __attribute__((aligned(16))) char ring[kRingStages * kStageBytes];
@@ -877,7 +879,7 @@ __global__ __launch_bounds__(256, 2) void attn_ring_kernel(const AttnArgs a) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const u32x4 vw = {vt[2 * db][0], vt[2 * db][1], vt[2 * db + 1][0], vt[2 * db + 1][1]};
-                if constexpr (kF16) {
+                if constexpr (kF16 || kVH) {
                     vh[db] = u32x4_as_f16x8(vw);   // fp16 V as loaded
                 } else if constexpr (kExactPV) {
                     vf[db] = u32x4_as_bf16x8(vw);
@@ -1024,8 +1026,10 @@ constexpr int kVPitch = 80;   // LDS row pitch of V (bf16): 160 B keeps the four
 // NW query blocks per workgroup, one wave each: 1 spreads a small batch's
 // few heads over the most CUs; 5 (large batches) runs a head's 67 queries on
 // one CU, whose waves load K and V once between them.
-template <int KB, bool kF16, int NW>   // 16-key blocks covering Sk (even, <= 8); fp16 (else bf16) Q/K/V
+// kVH: bf16 Q/K with fp16 V (P then an fp16 (hi, lo) pair, as for fp16 inputs).
+template <int KB, bool kF16, int NW, bool kVH = false>   // 16-key blocks covering Sk (even, <= 8); fp16 (else bf16) Q/K/V
 __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
+    static_assert(!(kVH && kF16), "fp16 V with bf16 Q/K");
     using v8 = typename In16<kF16>::v8;
     constexpr int KROWS = 16 * KB;
     // NW == 1: the wave loads all of K and V and stages V in LDS.  NW > 1:
@@ -1173,7 +1177,7 @@ __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
             ls += pf[t];
         }
         uint32_t hw[4], lw[4];
-        if constexpr (kF16) {
+        if constexpr (kF16 || kVH) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) split_f16x2(pf[2 * e], pf[2 * e + 1], hw[e], lw[e]);
         } else {
@@ -1197,7 +1201,7 @@ __global__ __launch_bounds__(64 * NW) void attn_short_kernel(const AttnArgs a) {
             const uint2 hi4 = lds_read_tr16(vrow + 16 * kVPitch + 16 * db);
             const u32x4 vw = {lo4.x, lo4.y, hi4.x, hi4.y};
             const u32x4 hv = {hw[0], hw[1], hw[2], hw[3]}, lv = {lw[0], lw[1], lw[2], lw[3]};
-            if constexpr (kF16) {
+            if constexpr (kF16 || kVH) {
                 acc[db] = mfma16x16x32_f16(u32x4_as_f16x8(vw), u32x4_as_f16x8(hv), acc[db]);
                 acc[db] = mfma16x16x32_f16(u32x4_as_f16x8(vw), u32x4_as_f16x8(lv), acc[db]);
             } else {
@@ -1389,29 +1393,33 @@ int choose_splits(const sf_attn_desc* d) {
     return (int)ns;
 }
 
-template <int NW>
-void launch_short(bool f16, int kb, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
+template <int NW, bool F16, bool VH>
+void launch_short_kb(int kb, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
     const dim3 block(64 * NW);
-    if (f16) {
-        if (kb <= 2) hipLaunchKernelGGL((sfk::attn_short_kernel<2, true, NW>), grid, block, 0, s, a);
-        else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, true, NW>), grid, block, 0, s, a);
-        else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, true, NW>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((sfk::attn_short_kernel<8, true, NW>), grid, block, 0, s, a);
-    } else {
-        if (kb <= 2) hipLaunchKernelGGL((sfk::attn_short_kernel<2, false, NW>), grid, block, 0, s, a);
-        else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, false, NW>), grid, block, 0, s, a);
-        else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, false, NW>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((sfk::attn_short_kernel<8, false, NW>), grid, block, 0, s, a);
-    }
+    if (kb <= 2) hipLaunchKernelGGL((sfk::attn_short_kernel<2, F16, NW, VH>), grid, block, 0, s, a);
+    else if (kb <= 4) hipLaunchKernelGGL((sfk::attn_short_kernel<4, F16, NW, VH>), grid, block, 0, s, a);
+    else if (kb <= 6) hipLaunchKernelGGL((sfk::attn_short_kernel<6, F16, NW, VH>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((sfk::attn_short_kernel<8, F16, NW, VH>), grid, block, 0, s, a);
+}
+
+// vh: bf16 Q/K with fp16 V (sf_attn_desc.v_f16)
+template <int NW>
+void launch_short(bool f16, bool vh, int kb, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
+    if (f16) launch_short_kb<NW, true, false>(kb, grid, s, a);
+    else if (vh) launch_short_kb<NW, false, true>(kb, grid, s, a);
+    else launch_short_kb<NW, false, false>(kb, grid, s, a);
 }
 
 // QB: 16-row query blocks per workgroup (kQB: 80-row chunks on a (split x
 // chunk, H, B) grid; 1: the XCD-grouped 1-D query-block grid).
+// vh: bf16 Q/K with fp16 V (sf_attn_desc.v_f16; fp16 P.V form only).
 template <int QB>
-void launch_ring(bool exact, bool f16, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
+void launch_ring(bool exact, bool f16, bool vh, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
     if (exact) {
         if (f16) hipLaunchKernelGGL((sfk::attn_ring_kernel<true, true, QB>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((sfk::attn_ring_kernel<true, false, QB>), grid, dim3(256), 0, s, a);
+    } else if (vh) {
+        hipLaunchKernelGGL((sfk::attn_ring_kernel<false, false, QB, false, true>), grid, dim3(256), 0, s, a);
     } else {
         if (f16) hipLaunchKernelGGL((sfk::attn_ring_kernel<false, true, QB>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((sfk::attn_ring_kernel<false, false, QB>), grid, dim3(256), 0, s, a);
@@ -1419,8 +1427,9 @@ void launch_ring(bool exact, bool f16, dim3 grid, hipStream_t s, const sfk::Attn
 }
 
 // The query-block grid with Q finished from split-K partials (bf16).
-void launch_ring_qp(bool exact, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
+void launch_ring_qp(bool exact, bool vh, dim3 grid, hipStream_t s, const sfk::AttnArgs& a) {
     if (exact) hipLaunchKernelGGL((sfk::attn_ring_kernel<true, false, 1, true>), grid, dim3(256), 0, s, a);
+    else if (vh) hipLaunchKernelGGL((sfk::attn_ring_kernel<false, false, 1, true, true>), grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((sfk::attn_ring_kernel<false, false, 1, true>), grid, dim3(256), 0, s, a);
 }
 
@@ -1461,6 +1470,9 @@ int validate(const sf_attn_desc* d) {
     }
     if (d->q_f16) {   // fp16 Q rows against bf16 K / V
         if (d->in_dtype != SF_BF16 || d->q_partials) return SF_ENOTSUP;
+    }
+    if (d->v_f16) {   // fp16 V against bf16 Q / K, fp16 P.V form
+        if (d->in_dtype != SF_BF16 || d->exact_pv) return SF_ENOTSUP;
     }
     if (d->q_gamma || d->k_gamma) {   // per-head Q / K RMSNorm on load
         if (d->in_dtype == SF_F32) return SF_ENOTSUP;
@@ -1625,6 +1637,7 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f16 = d->in_dtype == SF_F16;
+    const bool vh = d->v_f16 != 0;
     if (d->in_dtype == SF_F32) {
         const long qblocks = (d->Sq + 15) / 16;
         if ((long)ns * qblocks > 0x7fffffffL) return SF_ENOTSUP;
@@ -1638,19 +1651,19 @@ extern "C" int sf_attn_fwd(const sf_attn_desc* d, const void* q, const void* k, 
         const long bh = (long)d->B * d->H;
         const bool grouped = bh >= sfk::kShortGroupMinHeads;
         if (grouped)
-            launch_short<5>(f16, kb, dim3((qb + 4) / 5, d->H, d->B), s, a);
+            launch_short<5>(f16, vh, kb, dim3((qb + 4) / 5, d->H, d->B), s, a);
         else
-            launch_short<1>(f16, kb, dim3(qb, d->H, d->B), s, a);
+            launch_short<1>(f16, vh, kb, dim3(qb, d->H, d->B), s, a);
         return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
     } else {
         if (qblocks) {
             const long groups = (bh + 7) / 8;
             if (8L * nqc * groups > 0x7fffffffL) return SF_ENOTSUP;
             const dim3 grid((unsigned)(8L * nqc * groups));
-            if (q_from_partials) launch_ring_qp(d->exact_pv != 0, grid, s, a);
-            else launch_ring<1>(d->exact_pv != 0, f16, grid, s, a);
+            if (q_from_partials) launch_ring_qp(d->exact_pv != 0, vh, grid, s, a);
+            else launch_ring<1>(d->exact_pv != 0, f16, vh, grid, s, a);
         } else {
-            launch_ring<sfk::kQB>(d->exact_pv != 0, f16, dim3(ns * nqc, d->H, d->B), s, a);
+            launch_ring<sfk::kQB>(d->exact_pv != 0, f16, vh, dim3(ns * nqc, d->H, d->B), s, a);
         }
     }
     if (hipGetLastError() != hipSuccess) return SF_ELAUNCH;

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstring>
 #include <math.h>
 #include <stdint.h>
 
@@ -186,6 +187,31 @@ __global__ __launch_bounds__(256) void absmax_jobs_kernel(const AbsmaxJobs J) {
     }
 }
 
+// In place bf16 -> fp16 (nearest even) of buffer blockIdx.y when the max |x|
+// absmax_jobs_kernel merged for it is below `limit` (a NaN maximum is not):
+// the same conversion the attention's fp16 P.V form applies to bf16 V in
+// registers (pack_f16x2_rn of each element's fp32 value), done once.
+// The maximum is compared as bits: a non-negative float orders like its bit
+// pattern and every NaN pattern lies above +inf, so this holds whatever the
+// compiler assumes about NaN (the library is built with -fno-honor-nans,
+// under which !(mx < limit) may become mx >= limit).  limit > 0.
+__global__ __launch_bounds__(256) void to_f16_below_kernel(const AbsmaxJobs J, uint32_t limit_bits) {
+    const int j = blockIdx.y;
+    if (*J.out[j] >= limit_bits) return;
+    uint16_t* __restrict__ p = const_cast<uint16_t*>(J.p[j]);
+    const int64_t n = J.n[j];
+    const int64_t n8 = n / 8;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += stride) {
+        u32x4 w = *reinterpret_cast<const u32x4*>(p + 8 * i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = pack_f16x2_rn(__uint_as_float(w[e] << 16), __uint_as_float(w[e] & 0xffff0000u));
+        *reinterpret_cast<u32x4*>(p + 8 * i) = w;
+    }
+    for (int64_t i = 8 * n8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        p[i] = (uint16_t)(pack_f16x2_rn(__uint_as_float((uint32_t)p[i] << 16), 0.f) & 0xffffu);
+}
+
 }  // namespace sfk
 
 using sfk::blocks_for;
@@ -279,6 +305,29 @@ extern "C" int sf_absmax_bf16_batched(const sf_absmax_job* jobs, int32_t count, 
     const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 256));
     hipLaunchKernelGGL(sfk::absmax_jobs_kernel, dim3(blocks, (unsigned)count), dim3(256), 0,
                        static_cast<hipStream_t>(stream), J);
+    return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
+}
+
+extern "C" int sf_bf16_to_f16_below(const sf_absmax_job* jobs, int32_t count, float limit, void* stream) {
+    if (count < 0 || count > SF_ABSMAX_MAX_JOBS || (count && !jobs)) return SF_EINVAL;
+    if (!(limit > 0.f)) return SF_EINVAL;
+    sfk::AbsmaxJobs J{};
+    int64_t most = 0;
+    for (int j = 0; j < count; ++j) {
+        const sf_absmax_job& b = jobs[j];
+        if (!b.out || b.n < 0 || (b.n && !b.p) || (reinterpret_cast<uintptr_t>(b.p) & 15)) return SF_EINVAL;
+        J.p[j] = static_cast<const uint16_t*>(b.p);
+        J.n[j] = b.n;
+        J.out[j] = reinterpret_cast<unsigned int*>(b.out);
+        most = std::max(most, b.n);
+    }
+    if (!count || !most) return SF_OK;
+    const int64_t want = (most / 8 + 255) / 256;
+    const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 1024));
+    uint32_t limit_bits;
+    std::memcpy(&limit_bits, &limit, 4);
+    hipLaunchKernelGGL(sfk::to_f16_below_kernel, dim3(blocks, (unsigned)count), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), J, limit_bits);
     return hipGetLastError() == hipSuccess ? SF_OK : SF_ELAUNCH;
 }
 

@@ -526,7 +526,7 @@ struct RowsIn {
 // read.  qp: Q from partials instead of q (which is then not read).
 int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v, int Sk,
               const int32_t* valid_len, void* out, bool exact_pv, hipStream_t s, int Sc = 0,
-              const QPartials* qp = nullptr, const RowsIn* rows = nullptr) {
+              const QPartials* qp = nullptr, const RowsIn* rows = nullptr, bool v_f16 = false) {
     const sf_rdt_config& c = m->cfg;
     const int S = c.horizon + 3;
     sf_attn_desc d;
@@ -563,6 +563,7 @@ int attention(sf_rdt* m, const uint16_t* q, const uint16_t* k, const uint16_t* v
     }
     d.kv_valid_len = valid_len;
     d.exact_pv = exact_pv ? 1 : 0;
+    d.v_f16 = v_f16 ? 1 : 0;
     if (qp) {
         d.q_partials = qp->p;
         d.q_splits = qp->splits;
@@ -776,11 +777,14 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
     // cross-attention branch: even blocks attend to language, odd to image
     // (dit_block.cu:369)
     const bool lang = (i % 2) == 0;
+    // the cached V of a layer on the fp16 P.V form is held in fp16 (converted
+    // once when the condition was set, sf_bf16_to_f16_below)
+    const bool exact = m->exact_pv[i] != 0;
     if (lang && m->cq_splits > 0) {   // Q finished inside the attention
         QPartials qp;
         SF_TRY(cross_q_partials(m, L, M, s, &qp));
         SF_TRY(attention(m, nullptr, m->ck[i], m->cv[i], m->cond_lang_rows, m->lang_len, m->a,
-                         m->exact_pv[i] != 0, s, c.lang_max, &qp));
+                         exact, s, c.lang_max, &qp, nullptr, !exact));
     } else if (m->rows_qkv) {
         // q = x W^T + b in fp16 rows (dit_block.cu:282-284); seq_to_head and
         // q_norm (:298-307) happen as the attention loads them (rounding Q to
@@ -791,15 +795,15 @@ int block_forward(sf_rdt* m, int i, hipStream_t s) {
         r.q_gamma = pf(m, L.cq_norm);
         r.f16 = ad == SF_F16;
         SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? m->cond_lang_rows : c.img_len,
-                         lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,
-                         lang ? c.lang_max : c.img_len, nullptr, &r));
+                         lang ? m->lang_len : nullptr, m->a, exact, s,
+                         lang ? c.lang_max : c.img_len, nullptr, &r, !exact));
     } else {
         uint16_t* cq[1] = {m->q};
         const int cq_g[1] = {L.cq_norm};
         SF_TRY(linear_heads(m, m->n, M, S, L.cq_w, L.cq_b, cq, cq_g, 1, s, SF_BF16, true, m->n_deferred));
         SF_TRY(attention(m, m->q, m->ck[i], m->cv[i], lang ? m->cond_lang_rows : c.img_len,
-                         lang ? m->lang_len : nullptr, m->a, m->exact_pv[i] != 0, s,
-                         lang ? c.lang_max : c.img_len));
+                         lang ? m->lang_len : nullptr, m->a, exact, s,
+                         lang ? c.lang_max : c.img_len, nullptr, nullptr, !exact));
     }
     SF_TRY(linear_add_norm(m, m->a, ad, M, L.cproj_w, L.cproj_b, L.norm3, m->n3, fd, s));
     // FFN branch (Mlp::forward, dit_block.cu:143-163); fc2's add + norm
@@ -1315,6 +1319,11 @@ extern "C" int sf_rdt_set_condition(sf_rdt* m, const void* lang_c, const int32_t
                 jobs[j] = sf_absmax_job{m->cv[i], (int64_t)B * c.heads * Sc * 64, m->v_absmax + i};
             }
             SF_TRY(sf_absmax_bf16_batched(jobs, n, s));
+            // V of every layer below the fp16 range limit -- the layers
+            // resolve_pv_forms puts on the fp16 P.V form, by the same
+            // comparison -- to fp16 in place, the rounding the attention
+            // would otherwise apply to every tile of every step
+            SF_TRY(sf_bf16_to_f16_below(jobs, n, 65504.f, s));
         }
         SF_HIP(hipMemcpyAsync(m->v_absmax_host, m->v_absmax, (size_t)c.layers * 4, hipMemcpyDeviceToHost, s));
         SF_HIP(hipEventRecord(m->cond_event, s));

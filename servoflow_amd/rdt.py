@@ -222,10 +222,15 @@ class RdtModel:
         return {nm: self.param_numpy(i, dt, sh) for i, (nm, dt, sh) in enumerate(self.params())}
 
     def cache_numpy(self, layer, which_v):
+        """Block `layer`'s K (which_v 0) or V cache as fp32 [B, H, S, 64]: K
+        is bf16; V is fp16 for a layer on the fp16 P.V form, else bf16."""
         c = self.cfg
         sc = c.lang_max if layer % 2 == 0 else c.img_len
+        f16 = which_v and self.pv_exact(layer) == 0
         raw = _memcpy_d2h(np.empty(c.batch * c.heads * sc * 64, np.uint16),
                           lib().sf_rdt_cache_ptr(self.h, layer, which_v))
+        if f16:
+            return raw.view(np.float16).astype(np.float32).reshape(c.batch, c.heads, sc, 64)
         return (raw.astype(np.uint32) << 16).view(np.float32).reshape(c.batch, c.heads, sc, 64)
 
     def set_condition(self, lang_c, lang_len, img_c, state_tok):

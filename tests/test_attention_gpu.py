@@ -775,3 +775,110 @@ def test_q_f16_rows_cross_attention(B, Sk, lang, exact):
     ref = O.attention_f32(q, k.float().cpu().numpy(), v.float().cpu().numpy(),
                           valid_len=None if vl is None else vl.cpu().numpy())
     assert_close_bf16(got.cpu().numpy(), ref, f"fp16 Q rows cross-attention B={B} Sk={Sk}")
+
+
+@pytest.mark.parametrize("B,Sk,vl,causal,mask", [
+    (1, 4374, None, False, False),    # batch-1 image: key splits + merge
+    (2, 4374, None, False, False),    # four splits
+    (8, 4374, None, False, True),     # one workgroup per (b, h), key-padding mask
+    (1, 1024, [517], False, False),   # batch-1 language: the query-block grid
+    (8, 1024, "rand", False, False),  # ragged language keys, (b, h) grid
+    (3, 300, [300, 0, 129], True, False),
+])
+def test_v_f16_matches_converting_bf16_v(B, Sk, vl, causal, mask):
+    """sf_attn_desc.v_f16: V given in fp16 (the runtime converts its cached V
+    once, sf_bf16_to_f16_below) against bf16 Q/K.  The fast P.V form
+    converts a bf16 V to fp16 with the same rounding in registers, so the
+    output is bit for bit the bf16-V call's on every grid of the ring
+    kernel."""
+    dev = torch.device(DEV)
+    H, Sq = 32, 67
+    g = torch.Generator(device=dev).manual_seed(900 + B + Sk)
+    q = torch.randn(B, H, Sq, 64, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, H, Sk, 64, device=dev, generator=g).to(torch.bfloat16)
+    v = (torch.randn(B, H, Sk, 64, device=dev, generator=g) * 3.0).to(torch.bfloat16)
+    v[0, 0, :4, :4] = torch.tensor([1e-6, -3e-7, 2.0 ** -20, 60000.0], device=dev).to(torch.bfloat16)
+    v16 = v.to(torch.float16)   # round to nearest even, as the kernel's conversion
+    kw = dict(out_dtype=torch.float32, is_causal=causal)
+    if vl == "rand":
+        kw["valid_len"] = torch.from_numpy(lang_valid_lengths(B + 1, B)).to(dev)
+    elif vl is not None:
+        kw["valid_len"] = torch.tensor(vl, dtype=torch.int32, device=dev)
+    if mask:   # rows padded to a multiple of 4 bytes
+        keep = torch.rand(B, (Sk + 3) // 4 * 4, device=dev, generator=g) > 0.3
+        keep[:, 0] = True
+        kw["kv_mask"] = keep[:, :Sk]
+    ref = attention(q, k, v, **kw)
+    got = attention(q, k, v16, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(ref).all()
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("Sq,Sk,vl", [(67, 67, None), (67, 128, [128, 5, 0]), (67, 100, [100, 37, 64])])
+@pytest.mark.parametrize("B", [3, 8])
+def test_v_f16_short_keys(B, Sq, Sk, vl):
+    """At most 128 keys (the runtime's language cache read at few valid
+    keys above 160 rows) the short-key kernel takes fp16 V with P as an fp16
+    (hi, lo) pair: against the oracle at the bf16 bar and within 1e-4 of the
+    bf16-V call (P carries more bits; V holds the same values); one wave per
+    query block (B*H < 256) and the grouped five-wave form."""
+    dev = torch.device(DEV)
+    H = 32
+    vl = None if vl is None else (vl * ((B + 2) // 3))[:B]
+    q, k, v = rounded(261, (B, H, Sq, 64)), rounded(262, (B, H, Sk, 64)), rounded(263, (B, H, Sk, 64))
+    kw = {}
+    vld = None
+    if vl is not None:
+        vld = np.asarray(vl, np.int32)
+        kw["valid_len"] = to_dev(vld, torch.int32)
+    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+    got = attention(qd, kd, vd.to(torch.float16), out_dtype=torch.float32, **kw).cpu().numpy()
+    ref_b = attention(qd, kd, vd, out_dtype=torch.float32, **kw).cpu().numpy()
+    ref = O.attention_f32(q, k, v, valid_len=vld)
+    assert_close_bf16(got, ref, f"short fp16 V B={B} {Sq}x{Sk}")
+    assert np.abs(got - ref_b).max() < 1e-4
+
+
+def test_v_f16_rejected_forms():
+    """v_f16 needs bf16 Q/K and the fast P.V form: SF_ENOTSUP with the exact
+    form, fp16 or fp32 inputs, before any launch."""
+    import ctypes
+    dev = torch.device(DEV)
+    q = torch.zeros(1, 2, 16, 64, device=dev, dtype=torch.bfloat16)
+    kv = torch.zeros(1, 2, 256, 64, device=dev, dtype=torch.bfloat16)
+    out = torch.zeros(1, 2, 16, 64, device=dev, dtype=torch.float32)
+    for field, value in (("exact_pv", 1), ("in_dtype", abi.SF_F16), ("in_dtype", abi.SF_F32)):
+        d = make_desc(q, kv, kv.to(torch.float16), out)
+        assert d.v_f16 == 1
+        setattr(d, field, value)
+        st = abi.lib().sf_attn_fwd(ctypes.byref(d), q.data_ptr(), kv.data_ptr(), kv.data_ptr(), out.data_ptr(),
+                                   None, 0, None)
+        assert st == abi.SF_ENOTSUP, (field, st)
+
+
+def test_bf16_to_f16_below_converts_only_in_range_buffers():
+    """sf_bf16_to_f16_below: each buffer whose measured max |x| is below the
+    limit becomes its fp16 rounding (torch's conversion, bit for bit); a
+    buffer at or above the limit, or with a NaN, is left untouched."""
+    import ctypes
+    dev = torch.device(DEV)
+    g = torch.Generator(device=dev).manual_seed(77)
+    bufs = [(torch.randn(n, device=dev, generator=g) * 100).to(torch.bfloat16) for n in (4096 + 5, 1 << 16, 24, 40)]
+    bufs[1][123] = 70000.0      # out of fp16 range
+    bufs[2][3] = float("nan")
+    bufs[3][7] = 65000.0        # in range, rounds to a different fp16 neighbour grid
+    orig = [b.clone() for b in bufs]
+    amax = torch.zeros(len(bufs), dtype=torch.float32, device=dev)
+    jobs = (abi.AbsmaxJob * len(bufs))()
+    for j, b in enumerate(bufs):
+        jobs[j].p, jobs[j].n, jobs[j].out = b.data_ptr(), b.numel(), amax.data_ptr() + 4 * j
+    s = torch.cuda.current_stream().cuda_stream
+    abi.check(abi.lib().sf_absmax_bf16_batched(jobs, len(bufs), s), "absmax")
+    abi.check(abi.lib().sf_bf16_to_f16_below(jobs, len(bufs), ctypes.c_float(65504.0), s), "to_f16")
+    torch.cuda.synchronize()
+    for j, b in enumerate(bufs):
+        conv = bool(amax[j] < 65504.0)
+        assert conv == (j in (0, 3)), (j, float(amax[j]))
+        want = orig[j].to(torch.float16).view(torch.int16) if conv else orig[j].view(torch.int16)
+        assert torch.equal(b.view(torch.int16), want), j
