@@ -43,12 +43,12 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 # HBM bytes per roofline op measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (x2.0 / x1.0, scales read off a 256 MiB copy kernel) on `bench.py
-# --profile-roofline`: ring kernel 18656.8 KiB fetched (38.21 MB read) +
-# 3874.5 KiB written, merge 2179.0 KiB fetched + 268.0 KiB written
+# --profile-roofline`: ring kernel 18650.9 KiB fetched (38.20 MB read) +
+# 5123.1 KiB written, merge 2182.0 KiB fetched + 268.0 KiB written
 # (profiles/cross_attention_image_roofline.md).  Re-measured whenever the
 # attention kernels change.
-TRAFFIC_B1_IMAGE_BYTES = 46913638
-TRAFFIC_B8_IMAGE_BYTES = 291511091   # same profile, batch-8 op (no key split)
+TRAFFIC_B1_IMAGE_BYTES = 48186266
+TRAFFIC_B8_IMAGE_BYTES = 291492659   # same profile, batch-8 op (no key split)
 
 
 def attn_bytes(B, H, Sq, Sk_valid_total, D=64, eb=2):
