@@ -169,16 +169,17 @@ def test_loop_large_batch_graph_and_oracle(batch, int8):
         assert_within_floor(eager[b:b + 1], ref, floor, f"loop B={batch} slot {b}")
 
 
-@pytest.mark.parametrize("int8", [0, 1])
-def test_weight_writes_reach_the_large_batch_copies(int8):
-    """Above 160 rows the projections multiply fp16 copies of the weights,
-    rebuilt before a pass only when the parameters may have changed.  A
-    write through sf_rdt_param_data after a pass (param_write), and a write
+@pytest.mark.parametrize("batch,int8", [(3, 0), (3, 1), (1, 0)])
+def test_weight_writes_reach_the_fp16_copies(batch, int8):
+    """The runtime multiplies fp16 copies of weights -- above 160 rows every
+    projection's, at batch 1 with bf16 weights the FFN matrices' -- rebuilt
+    before a pass only when the parameters may have changed.  A write
+    through sf_rdt_param_data after a pass (param_write), and a write
     through a pointer taken before a pass followed by sf_rdt_params_changed,
-    both reach the next graph replay: its velocity matches the oracle on
-    the new weights (a stale copy would give the old weights' result)."""
+    both reach the next graph replay: its result matches the oracle on the
+    new weights (a stale copy would give the old weights' result)."""
     import ctypes
-    c = small_cfg(layers=2, batch=3, int8_weights=int8)
+    c = small_cfg(layers=2, batch=batch, int8_weights=int8)
     m = build(c)
     lang, ll, img, state = make_condition(c)
     set_cond(m, lang, ll, img, state)
