@@ -151,7 +151,7 @@ def bench_attention(B, Sk, steps, warmup, valid=None, Sq=67, H=32, exact_pv=Fals
     return res
 
 
-def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
+def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain", a16=False, w16=False):
     """Graph-timed block projection C[M,N] = A[M,K] W[N,K]^T + bias through
     sf_gemm with a caller workspace (split-K kernel + reduce for M <= 160;
     above, hipBLASLt writes the bf16 C with its bias epilogue, int8 codes
@@ -160,8 +160,12 @@ def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
     copies totalling >= COLD_SET_BYTES (at most 64 calls), so weights stream
     from HBM as in the loop, where each is read once per step.  epilogue:
     "plain" (bf16 out) or "addnorm" (fp32 residual += product, then RMSNorm
-    to bf16).  Returns time, MFMA rate against the dense bf16 peak and the
-    weight-streaming HBM rate."""
+    to bf16).  a16: fp16 activations and an fp16 C -- with int8 weights
+    above 160 rows the direct int8 kernel (no 16-bit weight copy), or with
+    w16 hipBLASLt on fp16 copies of the weights (the int8_weights = 1
+    runtime's product).  Returns
+    time, MFMA rate against the dense bf16 peak and the weight-streaming HBM
+    rate."""
     import ctypes
 
     import torch
@@ -173,7 +177,7 @@ def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
     g.manual_seed(M + N + K)
     wbytes = N * K * (1 if int8 else 2)
     n_sets = int(min(64, max(1, -(-COLD_SET_BYTES // wbytes))))
-    a = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    a = torch.randn(M, K, device=dev, generator=g).to(torch.float16 if a16 else torch.bfloat16)
     if int8:
         ws_ = [torch.randint(-127, 128, (N, K), device=dev, generator=g, dtype=torch.int32).to(torch.int8)
                for _ in range(n_sets)]
@@ -195,16 +199,21 @@ def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
         d.norm_gamma, d.norm_out = gamma.data_ptr(), out.data_ptr()
         d.norm_ldo, d.norm_dtype = out.stride(0), abi.SF_BF16
     else:
-        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        out = torch.empty(M, N, dtype=torch.float16 if a16 else torch.bfloat16, device=dev)
         d.epilogue = abi.SF_EPI_PLAIN
-        d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), abi.SF_BF16
+        d.C, d.ldc, d.c_dtype = out.data_ptr(), out.stride(0), abi.SF_F16 if a16 else abi.SF_BF16
     d.workspace, d.workspace_bytes = wsp.data_ptr(), wsp.numel()
+    copies = [c for i in range(0, n_sets, 8) for c in kernels.weights_to_f16(ws_[i:i + 8])] if w16 else []
+    if w16:
+        d.w_codes16, d.w16_f16 = copies[0].data_ptr(), 1
     abi.check(abi.lib().sf_gemm_prepare(ctypes.byref(d)), "sf_gemm_prepare")
     descs = []
-    for w in ws_:
+    for i, w in enumerate(ws_):
         di = abi.GemmDesc()
         ctypes.pointer(di)[0] = d
         di.W = w.data_ptr()
+        if w16:
+            di.w_codes16 = copies[i].data_ptr()
         descs.append(di)
     calls = [0]
 
@@ -214,7 +223,7 @@ def bench_gemm(M, N, K, steps, warmup, int8=False, epilogue="plain"):
         abi.check(abi.lib().sf_gemm(ctypes.byref(di), torch.cuda.current_stream(dev).cuda_stream), "sf_gemm")
 
     ms = time_graph(fn, steps, warmup, reps=max(20, n_sets))
-    del ws_
+    del ws_, copies
     torch.cuda.empty_cache()
     flops = 2.0 * M * N * K
     nbytes = wbytes + M * K * 2 + M * N * 2
@@ -234,6 +243,7 @@ GEMM_SHAPES = (
     ("proj_b16", 1072, 2048, 2048, False),
     ("qkv_b16", 1072, 6144, 2048, False),
     ("proj_int8_b32", 2144, 2048, 2048, True),
+    ("proj_int8_direct_b32", 2144, 2048, 2048, 2),   # fp16 activations, int8 read directly
     ("kv_img_b1", 4374, 4096, 2048, False),
 )
 
@@ -241,14 +251,16 @@ GEMM_SHAPES = (
 def make_model(B, int8=False, seed=1234, mlp_ratio=1, lens_out=None):
     """RDT-1B (28 layers) with random weights and a synthetic condition:
     language N(0,1) with valid lengths ~ U{32..1024}, image N(0,1) 4374 tokens,
-    state token N(0,1).  Returns (model, encode_ms); lens_out (a list)
-    receives the drawn language lengths."""
+    state token N(0,1).  int8: 0 bf16 weights, 1 int8 (fp16 copies above
+    160 rows), 2 int8 read directly (sf_rdt_config.int8_weights).  Returns
+    (model, encode_ms); lens_out (a list) receives the drawn language
+    lengths."""
     import numpy as np
     import torch
 
     from servoflow_amd import rdt as R
 
-    cfg = R.default_config(batch=B, int8_weights=1 if int8 else 0, mlp_ratio=mlp_ratio)
+    cfg = R.default_config(batch=B, int8_weights=int(int8), mlp_ratio=mlp_ratio)
     m = R.RdtModel(cfg)
     m.init_random(seed, 0.02)
     dev = torch.device("cuda:0")
@@ -530,9 +542,30 @@ def profile_mfma():
     r = bench_attention(1, 67, steps=5, warmup=1)
     print(f"profile: self-attention 1x32x67x67x64, graph-timed {r['us']:.2f} us per op", flush=True)
     for name, M, N, K, int8 in GEMM_SHAPES:
-        r = bench_gemm(M, N, K, steps=5, warmup=1, int8=int8)
+        r = bench_gemm(M, N, K, steps=5, warmup=1, int8=bool(int8), a16=int8 == 2)
         print(f"profile: gemm {name} {M}x{N}x{K}{' int8' if int8 else ''}, graph-timed "
               f"{r['us']:.2f} us per call", flush=True)
+
+
+def profile_int8_b32(iters=3):
+    """Runs only what the int8 large-batch traffic profile measures: the
+    2144 x 2048 x 2048 projection (int8 batch 32) with fp16 activations and
+    an fp16 C through the graph-timed bench_gemm -- the direct int8 kernel,
+    then hipBLASLt on fp16 copies of the codes -- and a plain 256 MiB
+    device-to-device copy `iters` times (the counters' calibration)."""
+    import torch
+
+    for w16 in (False, True):
+        r = bench_gemm(2144, 2048, 2048, steps=3, warmup=1, int8=True, a16=True, w16=w16)
+        print(f"profile: int8 gemm 2144x2048x2048 {'hipBLASLt on fp16 copies' if w16 else 'direct'}, "
+              f"graph-timed {r['us']:.2f} us per call", flush=True)
+    dev = torch.device("cuda:0")
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"profile: {iters} copies of 256 MiB done", flush=True)
 
 
 def main():
@@ -546,7 +579,9 @@ def main():
                     help="run only the roofline op and the copy calibration kernel (for rocprofv3)")
     ap.add_argument("--profile-mfma", action="store_true",
                     help="run only the self-attention op and the projection GEMMs (for rocprofv3 --pmc)")
-    ap.add_argument("--profile-loop", choices=["b16", "b32int8"],
+    ap.add_argument("--profile-int8", action="store_true",
+                    help="run only the int8 batch-32 projection, direct and on fp16 copies (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-loop", choices=["b16", "b32int8", "b32int8direct"],
                     help="build one large-batch model and replay its loop 3 times (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -564,8 +599,11 @@ def main():
     if args.profile_mfma:
         profile_mfma()
         return
+    if args.profile_int8:
+        profile_int8_b32()
+        return
     if args.profile_loop:
-        B, int8 = (16, False) if args.profile_loop == "b16" else (32, True)
+        B, int8 = {"b16": (16, 0), "b32int8": (32, 1), "b32int8direct": (32, 2)}[args.profile_loop]
         m, _ = make_model(B, int8=int8)
         ms = bench_loop(m, 3, 1)
         print(f"profile: loop batch {B}{' int8' if int8 else ''}: {ms:.3f} ms", flush=True)
@@ -628,19 +666,20 @@ def main():
             "self_b1_mfma_frac": round(self1["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS, 5),
         })
         for name, M, N, K, int8 in GEMM_SHAPES:
-            r = bench_gemm(M, N, K, att_steps, args.warmup, int8=int8)
+            r = bench_gemm(M, N, K, att_steps, args.warmup, int8=bool(int8), a16=int8 == 2)
             extra[f"gemm_{name}_us"] = round(r["us"], 3)
             extra[f"gemm_{name}_TFLOPs"] = round(r["TFLOPs"], 1)
             extra[f"gemm_{name}_mfma_frac"] = round(r["mfma_frac"], 4)
             if M <= 160:   # weight streaming: the HBM rate is the bound that matters
                 extra[f"gemm_{name}_GBps"] = round(r["GBps"], 1)
                 extra[f"gemm_{name}_hbm_frac"] = round(r["hbm_frac"], 4)
-        for B, int8, key in ((16, False, "loop_b16_ms"), (32, True, "loop_int8_b32_ms"),
-                             (32, False, "loop_b32_bf16_ms")):
+        for B, int8, key in ((16, 0, "loop_b16_ms"), (32, 1, "loop_int8_b32_ms"),
+                             (32, 2, "loop_int8_direct_b32_ms"), (32, 0, "loop_b32_bf16_ms")):
             m, enc = make_model(B, int8=int8)
             extra[key] = round(bench_loop(m, max(3, args.steps // 10), 2), 3)
             extra[key.replace("loop", "encode")] = round(enc, 3)
-            extra[key.replace("loop", "gemm_picks").replace("_ms", "")] = gemm_picks(B, int8)
+            if int8 < 2:   # int8_weights = 2: the block products run the direct int8 kernel
+                extra[key.replace("loop", "gemm_picks").replace("_ms", "")] = gemm_picks(B, bool(int8))
             m.close()
             del m
             torch.cuda.empty_cache()

@@ -262,6 +262,13 @@ int sf_attn_fwd_noalloc(const sf_attn_desc* desc, const void* q, const void* k,
  *     RMSNorm or the residual add + RMSNorm read bf16(A.W^T + bias) -- the
  *     reference's own storage point (the projection's bf16 output feeds
  *     split_qkv / fused_add_rms_norm) -- instead of the fp32 product.
+ * int8 weights above 160 rows with no w_codes16 copy are read directly when
+ * the call fits (sf_gemm_int8_direct): K = 2048, N a multiple of 256, ldw a
+ * multiple of 16, fp16 activations, act NONE or GELU_TANH, and one of the
+ * two 16-bit cases above in fp16 (an fp16 C, or round_product); the codes
+ * are widened in registers and the product is stored in fp16 with the row
+ * scale, bias and activation applied.
+ * Other int8 calls there widen the codes into the workspace on every call.
  * With workspace == NULL a single-pass kernel runs instead and nothing
  * beyond A, W and the outputs is touched.  A non-NULL workspace that is too
  * small is SF_EWORKSPACE.  Calls that may run concurrently need separate
@@ -351,6 +358,13 @@ int sf_gemm(const sf_gemm_desc* desc, void* stream);
 /* K slices the split-K path uses for this shape (M, N, K, a_dtype), 0 when
  * the call does not run split-K. */
 int32_t sf_gemm_num_splits(const sf_gemm_desc* desc);
+
+/* 1 when sf_gemm multiplies this call's int8 weights directly above 160
+ * rows (no 16-bit copy: w_codes16 NULL, the shape, types and epilogue
+ * listed with the workspace above), else 0; pointers are not inspected.
+ * Replaces the dequantize_int8_fp16_kernel pass (quantization.cu:18-51)
+ * ahead of gemm_bias_act (cuda_backend.cu:337-467) for those calls. */
+int32_t sf_gemm_int8_direct(const sf_gemm_desc* desc);
 
 /* The SF_EPI_HEADS epilogue on a bf16 projection already in memory -- the
  * reference's split_qkv / split_kv followed by apply_qk_norm

@@ -110,12 +110,18 @@ typedef struct sf_rdt_config {
     int32_t ctrl_freq;           /* 25 */
     int32_t num_steps;           /* 5 Euler steps */
     int32_t batch;
-    int32_t int8_weights;        /* block projections as int8 + fp32 row scale;
-                                    at batch * (horizon + 3) > 160 the runtime
-                                    (int8 or not) also holds fp16 copies of the
-                                    block and final-layer matrices (2 bytes per
-                                    weight), rewritten before the first pass
-                                    after the parameters may have changed */
+    int32_t int8_weights;        /* nonzero: block projections as int8 + fp32
+                                    row scale.  At batch * (horizon + 3) > 160
+                                    the runtime (int8 or not) also holds fp16
+                                    copies of the block and final-layer
+                                    matrices (2 bytes per weight), rewritten
+                                    before the first pass after the parameters
+                                    may have changed; with 2, no copy of the
+                                    int8 matrices sf_gemm multiplies directly
+                                    there (sf_gemm_int8_direct: every block
+                                    matrix with K = 2048), which read their
+                                    1-byte codes instead -- less memory and
+                                    half the weight bytes, slower products */
     float eps;                   /* 1e-6 */
     int32_t mlp_ratio;           /* FFN hidden = mlp_ratio * hidden (1; 0 means 1) */
 } sf_rdt_config;
@@ -137,8 +143,9 @@ int sf_rdt_param_info(const sf_rdt* m, int32_t idx, const char** name, int32_t* 
                       int32_t* ndim, int64_t shape[4]);
 /* Device pointer to parameter idx.  The runtime multiplies fp16 copies of
  * some weights (above 160 projection rows, batch * 67, every block and
- * final-layer matrix; at most 160 rows with bf16 weights, the FFN matrices,
- * whose inputs are fp16); they are rebuilt before the first pass after this
+ * final-layer matrix but, with int8_weights = 2, the int8 ones read
+ * directly; at most 160 rows with bf16 weights, the FFN matrices, whose
+ * inputs are fp16); they are rebuilt before the first pass after this
  * call, after
  * sf_rdt_init_random / sf_rdt_load_safetensors, and after
  * sf_rdt_params_changed -- a caller that writes through a pointer it

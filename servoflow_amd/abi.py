@@ -188,6 +188,8 @@ def lib() -> ctypes.CDLL:
     L.sf_weights_to_f16.restype = ctypes.c_int
     L.sf_gemm_num_splits.argtypes = [ctypes.POINTER(GemmDesc)]
     L.sf_gemm_num_splits.restype = ctypes.c_int32
+    L.sf_gemm_int8_direct.argtypes = [ctypes.POINTER(GemmDesc)]
+    L.sf_gemm_int8_direct.restype = ctypes.c_int32
     L.sf_heads_bf16.argtypes = [ctypes.POINTER(GemmDesc), vp, i64, vp]
     L.sf_heads_bf16.restype = ctypes.c_int
     L.sf_absmax_bf16_batched.argtypes = [ctypes.POINTER(AbsmaxJob), i32, vp]

@@ -621,15 +621,37 @@ int cross_q_partials(sf_rdt* m, const LayerIdx& L, int M, hipStream_t s, QPartia
 // block's fc1 and fc2 and the final layer's fc2 -- so the split-K kernel
 // reads fp16 operands instead of converting every bf16 fragment in
 // registers (the same operands, so the same results); int8 weights keep
-// their 1-byte codes.  Only matrices with K a multiple of 16.
+// their 1-byte codes.  Only matrices with K a multiple of 16.  With
+// int8_weights = 2, no copy of the int8 matrices sf_gemm multiplies directly
+// at the block's rows (sf_gemm_int8_direct; every such call the block makes
+// has fp16 activations and a 16-bit fp16 product).
 std::vector<int> w16_params(const sf_rdt* m) {
     const sf_rdt_config& c = m->cfg;
     std::vector<int> ws;
-    if (c.batch * (c.horizon + 3) > 160) {
+    const int rows = c.batch * (c.horizon + 3);
+    if (rows > 160) {
         for (const LayerIdx& L : m->layers)
             for (int w : block_weights(L)) ws.push_back(w);
         ws.push_back(m->f1w);
         ws.push_back(m->f2w);
+        if (c.int8_weights == 2) {
+            std::vector<int> keep;
+            for (int w : ws) {
+                const Param& P = m->params[w];
+                sf_gemm_desc d{};
+                d.M = rows;
+                d.N = (int32_t)P.shape[0];
+                d.K = (int32_t)P.shape[1];
+                d.lda = d.K;
+                d.a_dtype = SF_F16;
+                d.ldw = P.shape[1];
+                d.w_dtype = P.dtype;
+                d.epilogue = SF_EPI_PLAIN;
+                d.c_dtype = SF_F16;
+                if (!sf_gemm_int8_direct(&d)) keep.push_back(w);
+            }
+            ws.swap(keep);
+        }
     } else if (!c.int8_weights) {
         for (const LayerIdx& L : m->layers) {
             ws.push_back(L.fc1_w);

@@ -68,7 +68,9 @@ def gemm(a, w, bias=None, act=abi.SF_ACT_NONE, out=None, out_dtype=torch.bfloat1
     per-row fp32 w_scale).  accumulate adds into an fp32 `out`.  w_codes16:
     int8 w's codes as bf16 (int8_codes_to_bf16), read by the library path
     instead of widening them.  w16: an fp16 copy of w (weights_to_f16) for
-    fp16 `a`: the library path then multiplies in fp16."""
+    fp16 `a`: the library path then multiplies in fp16.  int8 w without a
+    copy above 160 rows is read directly when the call fits
+    (sf_gemm_int8_direct: K = 2048, N % 256 == 0, fp16 a and out)."""
     M, K = a.shape
     N = w.shape[0]
     if out is None:
@@ -112,7 +114,8 @@ def gemm_heads(a, w, bias, S, H, outs, gammas=(None, None, None), eps=1e-6, w_sc
     """Projection whose N columns are sections of H*64, written per head to
     outs[j] ([B,H,S,64] bf16 views) with optional per-head RMSNorm.
     round_product: above 160 rows the projection is stored in 16 bits
-    before the norm (bf16, or fp16 with w16)."""
+    before the norm (bf16, or fp16 with w16 or with int8 w multiplied
+    directly, sf_gemm_int8_direct)."""
     d = _desc(a, w, bias, abi.SF_ACT_NONE, w_scale)
     _w16(d, w16)
     _row_scale(d, row_ss, row_n, row_eps)

@@ -599,6 +599,114 @@ def test_gemm_fp16_outputs(ws):
     assert np.all(np.abs(n16 - f16r(n32)) <= np.abs(n32) * 2.0 ** -10 + 2.0 ** -24)
 
 
+def _direct_desc(a, w, act, epilogue, c_dtype, round_product=0, accumulate=0):
+    import ctypes
+    d = K._desc(a, w, None, act, None)
+    d.epilogue, d.c_dtype, d.round_product, d.accumulate = epilogue, c_dtype, round_product, accumulate
+    return abi.lib().sf_gemm_int8_direct(ctypes.byref(d))
+
+
+def _f16_product_matches(got, ref, what):
+    """An fp16 product against the oracle's fp32 result rounded to fp16:
+    equal but where the two fp32 sums (2048 terms of ~0.02 in another order,
+    ~1e-6 apart) straddle a rounding midpoint -- then one fp16 ulp apart, or
+    for results near zero, whose ulp is below that, the sums' difference."""
+    r16 = f16r(ref)
+    assert np.isfinite(got).all(), what
+    assert np.all(np.abs(got - r16) <= np.abs(r16) * 2.0 ** -10 + 2e-5), what
+    assert float(np.mean(got == r16)) >= 0.995, what
+
+
+@pytest.mark.parametrize("M,N,act", [(161, 256, abi.SF_ACT_NONE), (1000, 2048, abi.SF_ACT_GELU_TANH),
+                                     (8300, 256, abi.SF_ACT_GELU_TANH)])
+def test_gemm_int8_direct_plain(M, N, act):
+    """int8 weights above 160 rows without a 16-bit copy, multiplied directly
+    (sf_gemm_int8_direct): the codes widened exactly in registers, fp32 sums,
+    row scale, bias and GELU applied, one rounding to the fp16 C.  M = 161
+    (one partial 80-row tile), 1000 (ragged), 8300 (two library chunks of
+    rows).  Against the oracle on the same fp16 activations and dequantised
+    weights, and against hipBLASLt on the exact fp16 copy of the codes (the
+    same storage point, another summation order)."""
+    Kd = 2048
+    a = f16r(O.randn(401 + M, (M, Kd)))
+    q, s = O.quantize_int8_rows(O.randn(402 + N, (N, Kd), 0.02))
+    w, wdev, sdev = O.dequant_int8(q, s), dev(q, torch.int8), dev(s, torch.float32)
+    b = O.randn(403, (N,), 0.02)
+    ad = dev(a, torch.float16)
+    assert _direct_desc(ad, wdev, act, abi.SF_EPI_PLAIN, abi.SF_F16) == 1
+    got = host(K.gemm(ad, wdev, dev(b, torch.float32), act, out_dtype=torch.float16, w_scale=sdev))
+    _f16_product_matches(got, O.linear(a, w, b, act=act), f"direct int8 {M}x{N}")
+    (w16,) = K.weights_to_f16([wdev])
+    lib = host(K.gemm(ad, wdev, dev(b, torch.float32), act, out_dtype=torch.float16, w_scale=sdev, w16=w16))
+    assert np.all(np.abs(got - lib) <= np.abs(lib) * 2.0 ** -9 + 4e-5)
+    assert float(np.mean(got == lib)) >= 0.99
+
+
+def test_gemm_int8_direct_epilogues():
+    """The direct int8 product (fp16, bias and row scale in) feeding the
+    per-head RMSNorm and the residual add + RMSNorm (round_product), as the
+    batch-32 block runs them, against the oracle on the fp16 product."""
+    B, S, H, Kd = 16, 67, 4, 2048
+    M = B * S
+    a = f16r(O.randn(411, (M, Kd)))
+    ad = dev(a, torch.float16)
+    q, s = O.quantize_int8_rows(O.randn(412, (3 * H * 64, Kd), 0.02))
+    w, wdev, sdev = O.dequant_int8(q, s), dev(q, torch.int8), dev(s, torch.float32)
+    b = O.randn(413, (3 * H * 64,), 0.02)
+    gq, gk = 1.0 + O.randn(414, (64,), 0.1), 1.0 + O.randn(415, (64,), 0.1)
+    assert _direct_desc(ad, wdev, abi.SF_ACT_NONE, abi.SF_EPI_HEADS, abi.SF_BF16, round_product=1) == 1
+    outs = [torch.empty(B, H, S, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3)]
+    K.gemm_heads(ad, wdev, dev(b, torch.float32), S, H, outs,
+                 (dev(gq, torch.float32), dev(gk, torch.float32), None), w_scale=sdev, round_product=True)
+    Q, Kh, V = O.split_qkv(f16r(O.linear(a, w, b)).reshape(B, S, 3 * H * 64), H, 64)
+    for got, ref, what in zip(outs, (O.rms_norm(Q, gq), O.rms_norm(Kh, gk), V), "QKV"):
+        g = host(got)
+        assert np.all(np.abs(g - ref) <= np.abs(ref) * 2.0 ** -6 + 1e-3), what
+        assert float(np.mean(g == O.bf16_round(ref))) >= 0.99, what
+    q2, s2 = O.quantize_int8_rows(O.randn(416, (512, Kd), 0.02))
+    w2, w2dev, s2dev = O.dequant_int8(q2, s2), dev(q2, torch.int8), dev(s2, torch.float32)
+    b2, g2 = O.randn(417, (512,), 0.02), 1.0 + O.randn(418, (512,), 0.1)
+    x = O.randn(419, (M, 512))
+    xd = dev(x, torch.float32)
+    assert _direct_desc(ad, w2dev, abi.SF_ACT_NONE, abi.SF_EPI_ADD_NORM, abi.SF_F32, round_product=1) == 1
+    n = K.gemm_add_norm(ad, w2dev, dev(b2, torch.float32), xd, dev(g2, torch.float32), w_scale=s2dev,
+                        norm_dtype=torch.float32, round_product=True)
+    x_ref = x + f16r(O.linear(a, w2, b2))
+    close(host(xd), x_ref, "residual (direct int8 fp16 product)", rel=1e-5)
+    close(host(n), O.rms_norm(x_ref, g2), "norm (direct int8 fp16 product)", rel=1e-4)
+
+
+def test_gemm_int8_direct_full_size_and_routing():
+    """2144 x 2048 x 2048 (int8 batch 32) against hipBLASLt on the fp16 copy
+    of the codes, and the calls the direct kernel does not take: a copy
+    given, bf16 activations, K != 2048, N not a multiple of 256, SiLU, an
+    fp32 or accumulated C, M <= 160."""
+    M, N, Kd = 2144, 2048, 2048
+    a = f16r(O.randn(421, (M, Kd)))
+    ad = dev(a, torch.float16)
+    q, s = O.quantize_int8_rows(O.randn(422, (N, Kd), 0.02))
+    wdev, sdev = dev(q, torch.int8), dev(s, torch.float32)
+    bd = dev(O.randn(423, (N,), 0.02), torch.float32)
+    (w16,) = K.weights_to_f16([wdev])
+    got = host(K.gemm(ad, wdev, bd, abi.SF_ACT_GELU_TANH, out_dtype=torch.float16, w_scale=sdev))
+    lib = host(K.gemm(ad, wdev, bd, abi.SF_ACT_GELU_TANH, out_dtype=torch.float16, w_scale=sdev, w16=w16))
+    assert np.isfinite(got).all()
+    assert np.all(np.abs(got - lib) <= np.abs(lib) * 2.0 ** -9 + 4e-5)
+    assert float(np.mean(got == lib)) >= 0.99
+    P, F16, BF16, F32 = abi.SF_EPI_PLAIN, abi.SF_F16, abi.SF_BF16, abi.SF_F32
+    assert _direct_desc(ad, wdev, 0, P, F16) == 1
+    assert _direct_desc(ad, wdev, 0, P, BF16) == 0                     # C not the activations' type
+    assert _direct_desc(ad, wdev, 0, P, F32) == 0
+    assert _direct_desc(ad, wdev, 0, abi.SF_EPI_ADD_NORM, F32) == 0    # no round_product
+    assert _direct_desc(ad, wdev, abi.SF_ACT_SILU, P, F16) == 0
+    assert _direct_desc(ad, wdev, 0, P, F16, accumulate=1) == 0
+    assert _direct_desc(ad.bfloat16(), wdev, 0, P, BF16) == 0
+    assert _direct_desc(ad[:160], wdev, 0, P, F16) == 0
+    assert _direct_desc(ad[:, :1024], wdev[:, :1024], 0, P, F16) == 0
+    assert _direct_desc(ad, wdev[:200], 0, P, F16) == 0
+    assert _direct_desc(ad, dev(O.dequant_int8(q, s)), 0, P, F16) == 0  # bf16 weights
+
+
 def test_gemm_fp16_activations_library_path():
     """M > 160: fp16 activations are rounded to bf16 for the library product."""
     M, N, Kd = 1072, 2048, 2048

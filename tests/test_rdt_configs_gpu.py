@@ -71,8 +71,9 @@ def test_block_vs_fp32_oracle(blk):
 
 # ---- batch 16 and int8 batch 32: the library-path regime ----------------------
 
-@pytest.mark.parametrize("batch,int8,blk", [(16, 0, 0), (16, 0, 1), (32, 1, 0), (32, 1, 1)],
-                         ids=["b16-language", "b16-image", "int8_b32-language", "int8_b32-image"])
+@pytest.mark.parametrize("batch,int8,blk", [(16, 0, 0), (16, 0, 1), (32, 1, 0), (32, 1, 1), (32, 2, 0), (32, 2, 1)],
+                         ids=["b16-language", "b16-image", "int8_b32-language", "int8_b32-image",
+                              "int8direct_b32-language", "int8direct_b32-image"])
 def test_block_vs_fp32_oracle_large_batch(batch, int8, blk):
     """RDTBlock::forward (dit_block.cu:349-387) at batch 16 (bf16 weights)
     and batch 32 (int8 weights): 1072 / 2144 rows per projection, the
@@ -86,8 +87,10 @@ def test_block_vs_fp32_oracle_large_batch(batch, int8, blk):
     Above 160 rows the runtime multiplies fp16 activations by fp16 copies
     of the weights and keeps the products in fp16 (the oracle's CPU model
     of that storage put the block at 5.6-7.9e-4 from fp32; with the bf16
-    inputs and bf16 products used before, 1.6-1.8e-3).  The GPU is also held
-    to the oracle with the same storage points (rb_of) at the same bar."""
+    inputs and bf16 products used before, 1.6-1.8e-3).  int8 = 2 multiplies
+    the int8 codes directly instead (no copies; the same fp16 storage
+    points).  The GPU is also held to the oracle with the same storage
+    points (rb_of) at the same bar."""
     print(f"block {blk} batch {batch} int8 {int8} vs fp32 oracle", flush=True)
     c = small_cfg(layers=2, batch=batch, int8_weights=int8)
     m = build(c)
@@ -140,7 +143,7 @@ def test_denoise_step_large_batch(batch, int8):
     assert_within_floor(got, ref, floor, f"denoise step B={batch} int8={int8}")
 
 
-@pytest.mark.parametrize("batch,int8", [(16, 0), (32, 1)], ids=["b16", "int8_b32"])
+@pytest.mark.parametrize("batch,int8", [(16, 0), (32, 1), (32, 2)], ids=["b16", "int8_b32", "int8direct_b32"])
 def test_loop_large_batch_graph_and_oracle(batch, int8):
     """The 5-step hipGraph loop at batch 16 / int8 batch 32: graph replays
     equal the eager loop bit for bit, and batch slots 0 and B-1 match the
@@ -169,7 +172,7 @@ def test_loop_large_batch_graph_and_oracle(batch, int8):
         assert_within_floor(eager[b:b + 1], ref, floor, f"loop B={batch} slot {b}")
 
 
-@pytest.mark.parametrize("batch,int8", [(3, 0), (3, 1), (1, 0)])
+@pytest.mark.parametrize("batch,int8", [(3, 0), (3, 1), (3, 2), (1, 0)])
 def test_weight_writes_reach_the_fp16_copies(batch, int8):
     """The runtime multiplies fp16 copies of weights -- above 160 rows every
     projection's, at batch 1 with bf16 weights the FFN matrices' -- rebuilt
