@@ -109,10 +109,15 @@ struct GemmArgs {
 };
 
 __device__ __forceinline__ float gelu_tanh(float x) {
-    // GeluOp, src/backend/cuda/ops/elementwise.cuh:35-54.
+    // GeluOp, src/backend/cuda/ops/elementwise.cuh:35-54: 0.5 x (1 + tanh u),
+    // u = sqrt(2 / pi) (x + 0.044715 x^3), evaluated as x / (1 + e^(-2u))
+    // (0.5 (1 + tanh u) = 1 / (1 + e^(-2u))): one hardware exp2 and one
+    // reciprocal, ~1 ulp each; x -> -inf gives -0, x -> +inf gives x.
     const float kAlpha = 0.7978845608028654f;
     const float kBeta = 0.044715f;
-    return 0.5f * x * (1.f + tanhf(kAlpha * (x + kBeta * x * x * x)));
+    const float kM2Log2e = -2.f * 1.4426950408889634f;
+    const float u = kAlpha * (x + kBeta * x * x * x);
+    return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(kM2Log2e * u));
 }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
