@@ -116,6 +116,42 @@ def test_gemm_single_pass_rejects_weights_beyond_32bit_range():
     assert abi.lib().sf_gemm(ctypes.byref(g), None) == abi.SF_ENOTSUP
 
 
+def _int8_direct(**over):
+    g = abi.GemmDesc()
+    g.M, g.N, g.K = 2144, 2048, 2048
+    g.lda, g.a_dtype, g.ldw, g.w_dtype = 2048, abi.SF_F16, 2048, abi.SF_I8
+    g.epilogue, g.c_dtype, g.act = abi.SF_EPI_PLAIN, abi.SF_F16, abi.SF_ACT_NONE
+    for k, v in over.items():
+        setattr(g, k, v)
+    return abi.lib().sf_gemm_int8_direct(ctypes.byref(g))
+
+
+def test_gemm_int8_direct_routing():
+    """Which int8 calls above 160 rows sf_gemm multiplies directly (no
+    16-bit copy of the codes): K = 2048, N % 256 == 0, ldw % 16 == 0, fp16
+    activations, act NONE or GELU, an fp16 C or a round_product epilogue.
+    Host logic only (no pointer is inspected)."""
+    assert _int8_direct() == 1
+    assert _int8_direct(act=abi.SF_ACT_GELU_TANH) == 1
+    assert _int8_direct(M=161, N=256) == 1
+    assert _int8_direct(N=6144) == 1
+    assert _int8_direct(epilogue=abi.SF_EPI_ADD_NORM, c_dtype=abi.SF_F32, round_product=1) == 1
+    assert _int8_direct(epilogue=abi.SF_EPI_HEADS, round_product=1) == 1
+    assert _int8_direct(M=160) == 0                                   # the split-K regime
+    assert _int8_direct(K=1024) == 0
+    assert _int8_direct(N=2000) == 0
+    assert _int8_direct(ldw=2056) == 0                                # rows not 16-byte aligned
+    assert _int8_direct(w_codes16=256) == 0                           # a copy given: hipBLASLt on it
+    assert _int8_direct(w_dtype=abi.SF_BF16) == 0
+    assert _int8_direct(a_dtype=abi.SF_BF16, c_dtype=abi.SF_BF16) == 0
+    assert _int8_direct(c_dtype=abi.SF_BF16) == 0
+    assert _int8_direct(c_dtype=abi.SF_F32) == 0
+    assert _int8_direct(accumulate=1) == 0
+    assert _int8_direct(act=abi.SF_ACT_SILU) == 0
+    assert _int8_direct(epilogue=abi.SF_EPI_ADD_NORM, c_dtype=abi.SF_F32) == 0   # fp32 product wanted
+    assert abi.lib().sf_gemm_int8_direct(None) == 0
+
+
 def test_empty_problem_is_a_noop():
     d = abi.attn_desc_bhsd(0, 32, 67, 4374)
     assert _fwd(d, None, None, None, None) == abi.SF_OK
