@@ -355,19 +355,20 @@ def test_full_depth_batch16_slots_match_batch1():
         assert mr <= 3e-3, (b, mr)
 
 
-def test_full_size_int8_batch32_graph_loop():
-    """Config 5 at full size: 28 layers, hidden 2048, int8 weights, batch
-    32, full condition lengths (ragged language rows, 4374 image keys), the
-    5-step loop.  Properties that do not need the oracle at this size: the
-    graph replays equal the eager loop bit for bit (twice), every action
-    stays finite, and each batch slot moved from its noise."""
-    print("full-size int8 batch 32 loop", flush=True)
-    c = R.default_config(batch=32, int8_weights=1)
-    m = build(c)
+def _full_size_condition():
+    c = R.default_config(batch=32)
     lang_len = np.random.default_rng(32).integers(32, c.lang_max + 1, size=32).astype(np.int32)
-    lang, ll, img, state = make_condition(c, lang_len=lang_len)
-    set_cond(m, lang, ll, img, state)
-    del lang, img
+    return make_condition(c, lang_len=lang_len)
+
+
+def _full_size_int8_b32_loop(int8_weights, cond):
+    """Config 5 at full size (28 layers, hidden 2048, int8 weights, batch 32,
+    ragged language rows, 4374 image keys), the 5-step loop from seeded
+    noise: checks graph == eager (twice), finiteness and that every slot
+    moved; returns (x0, the eager result)."""
+    c = R.default_config(batch=32, int8_weights=int8_weights)
+    m = build(c)
+    set_cond(m, *cond)
     x0 = O.randn(23, (32, c.horizon, c.action_dim))
     xe = torch.from_numpy(x0).to(DEV)
     m.sample(xe, use_graph=False)
@@ -379,7 +380,37 @@ def test_full_size_int8_batch32_graph_loop():
         xg = torch.from_numpy(x0).to(DEV)
         m.sample(xg, use_graph=True)
         assert np.array_equal(xg.cpu().numpy(), eager), rep
-    print(f"int8 b32 full size: finite, graph == eager, min per-slot move {moved.min():.3e}", flush=True)
+    m.close()
+    print(f"int8 b32 full size (int8_weights {int8_weights}): finite, graph == eager, "
+          f"min per-slot move {moved.min():.3e}", flush=True)
+    return x0, eager
+
+
+def test_full_size_int8_batch32_graph_loop():
+    """Config 5 at full size: 28 layers, hidden 2048, int8 weights, batch
+    32, full condition lengths (ragged language rows, 4374 image keys), the
+    5-step loop.  Properties that do not need the oracle at this size: the
+    graph replays equal the eager loop bit for bit (twice), every action
+    stays finite, and each batch slot moved from its noise."""
+    print("full-size int8 batch 32 loop", flush=True)
+    _full_size_int8_b32_loop(1, _full_size_condition())
+
+
+def test_full_size_int8_batch32_direct_matches_copies():
+    """The same full-size loop with int8_weights = 2 (every block matrix's
+    codes read directly, no fp16 copies): graph == eager, finite, and each
+    slot's action update within 1.5e-3 mean-rel of the int8_weights = 1
+    loop (fp16 copies of the same codes: the same storage points, other
+    summation orders; measured 4.4e-4 for the worst slot)."""
+    print("full-size int8 batch 32 loop, codes read directly vs fp16 copies", flush=True)
+    cond = _full_size_condition()
+    x0, ref = _full_size_int8_b32_loop(1, cond)
+    _, got = _full_size_int8_b32_loop(2, cond)
+    for b in range(32):
+        mr = mean_rel(got[b] - x0[b], ref[b] - x0[b])
+        assert mr <= 1.5e-3, (b, mr)
+    print(f"direct vs copies: worst slot mean-rel "
+          f"{max(mean_rel(got[b] - x0[b], ref[b] - x0[b]) for b in range(32)):.3e}", flush=True)
 
 
 # ---- V beyond the fp16 range: the layer switches to the exact P.V form --------
